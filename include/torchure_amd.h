@@ -1,0 +1,169 @@
+/*
+ * torchure_amd.h -- C ABI of the MI355X (gfx950) mixed-precision optimizer step.
+ *
+ * The library replaces the device work of torchure's optimizer tail
+ * (torchure/train/trainer.py:391-397):
+ *   clip_grad_norm  (torchure/core/grad_helper.py:8-34)
+ *       = torch._foreach_norm + stack + vector_norm + clamp + torch._foreach_mul_
+ *   optimizer.step() (torch.optim.AdamW(fused=True), built at torchure/optimizer/builder.py:46)
+ *       = torch._foreach_add_(state_steps, 1) + torch._fused_adamw_
+ *         (torch/optim/adam.py:877-895; device math in
+ *          torch/include/ATen/native/hip/fused_adam_utils.cuh:22-199,
+ *          launcher signature torch/include/ATen/native/hip/fused_adam_impl.cuh:8-21)
+ *   plus the bf16 working-copy refresh that autocast performs at every forward
+ *   (torchure/train/trainer.py:374; rounding rule torch/headeronly/util/BFloat16.h:100-114).
+ *
+ * Conventions
+ *   - Every pointer named d_* is device memory; h_* is host memory.
+ *   - Nothing here allocates device memory or synchronises the stream: all work is
+ *     enqueued on `stream` (a hipStream_t passed as void*; NULL = the null stream).
+ *   - Return value: TM_OK (0) or a negative TM_E* code; tm_last_error() gives a
+ *     thread-local message for the last failure.
+ *   - Tensors are described by tm_tensor_t records in device memory and split into
+ *     fixed-size chunks by a tm_chunk_t table (device memory) built with
+ *     tm_fill_chunks(). Both tables are plain data owned by the caller.
+ */
+#ifndef TORCHURE_AMD_H
+#define TORCHURE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TM_ABI_VERSION 1
+
+/* status codes */
+#define TM_OK 0
+#define TM_EINVAL (-1)   /* bad argument (null pointer, size out of range) */
+#define TM_ELAUNCH (-2)  /* kernel launch failed */
+
+/* tm_tensor_t.flags */
+#define TM_GRAD_BF16 0u  /* grad is bfloat16 (uint16 storage) */
+#define TM_GRAD_F32 1u   /* grad is float32 (e.g. an fp32 accumulation buffer) */
+#define TM_FLAG_CLIP 2u  /* multiply the grad by *d_coef before use (deferred clip) */
+
+/* Largest number of hyper-parameter groups one call accepts. */
+#define TM_MAX_GROUPS 16
+
+/* Chunk granularity: chunk_elems must be a positive multiple of this. */
+#define TM_CHUNK_ALIGN 2048
+
+/* Number of partial sums the grad-norm pass writes (fixed, so the reduction
+ * order -- and therefore the result bits -- never depend on the device). */
+#define TM_NORM_PARTIALS 2048
+
+/*
+ * One tensor of the parameter list (64 bytes, device memory).
+ *   master      fp32 master weights, updated in place (torch: the nn.Parameter)
+ *   exp_avg     fp32 first moment, updated in place   (state['exp_avg'])
+ *   exp_avg_sq  fp32 second moment, updated in place  (state['exp_avg_sq'])
+ *   grad        bf16 or fp32 gradient (flags), read only
+ *   param_bf16  bf16 working copy written as RNE(master) after the update, or 0
+ *   step        fp32 0-d step counter, incremented in place (state['step'])
+ *   numel       element count (0 allowed: the step still advances)
+ *   group       index into the tm_hyper_t array of the call
+ *   flags       TM_GRAD_* | TM_FLAG_CLIP
+ * The norm / scale / accumulate entry points read only grad, numel and flags.
+ */
+typedef struct tm_tensor {
+  uint64_t master;
+  uint64_t exp_avg;
+  uint64_t exp_avg_sq;
+  uint64_t grad;
+  uint64_t param_bf16;
+  uint64_t step;
+  int64_t numel;
+  int32_t group;
+  uint32_t flags;
+} tm_tensor_t;
+
+/* One work item: elements [chunk*chunk_elems, min((chunk+1)*chunk_elems, numel))
+ * of tensor `tensor`. */
+typedef struct tm_chunk {
+  uint32_t tensor;
+  uint32_t chunk;
+} tm_chunk_t;
+
+/* Hyper-parameters of one param group, as torch.optim.AdamW holds them
+ * (python floats = double): torch/optim/adam.py:35-113, fused_adam_utils.cuh:110-121. */
+typedef struct tm_hyper {
+  double lr;
+  double beta1;
+  double beta2;
+  double weight_decay;
+  double eps;
+} tm_hyper_t;
+
+/* ---- library / table helpers (host only, no GPU work) ---- */
+
+int tm_abi_version(void);
+const char* tm_last_error(void);
+
+/* Device workspace bytes needed by tm_grad_norm / tm_adamw_step for n_tensors. */
+size_t tm_workspace_bytes(int64_t n_tensors);
+
+/* Number of chunks the tensors split into (zero-size tensors give none). */
+int64_t tm_count_chunks(const int64_t* h_numels, int64_t n_tensors, int64_t chunk_elems);
+
+/* Writes the chunk table into h_out (capacity `cap` entries) in tensor order.
+ * Returns the number written, or a negative TM_E* code. */
+int64_t tm_fill_chunks(const int64_t* h_numels, int64_t n_tensors, int64_t chunk_elems,
+                       tm_chunk_t* h_out, int64_t cap);
+
+/* ---- device entry points ---- */
+
+/*
+ * Global L2 norm of all grads, deterministic two-pass (no atomics).
+ * Replaces torch._foreach_norm + torch.stack + torch.linalg.vector_norm
+ * (torchure/core/grad_helper.py:17-18) and the clip coefficient
+ * clamp(max_norm / (total + 1e-6), max=1.0) (grad_helper.py:32, evaluated as
+ * reciprocal-then-multiply per torch/_tensor.py:1119-1122).
+ *   d_norm  receives the pre-clip norm (fp32, grad_helper.py:34)
+ *   d_coef  receives the clip coefficient when clip != 0 (else untouched; may be NULL)
+ *   d_ws    at least tm_workspace_bytes(n_tensors) bytes
+ */
+int tm_grad_norm(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                 int64_t n_chunks, int64_t chunk_elems, float max_norm, int clip, void* d_ws,
+                 float* d_norm, float* d_coef, void* stream);
+
+/*
+ * In-place grad *= *d_coef for every tensor (the eager clip).
+ * Replaces torch._foreach_mul_(grads, clip_coef) (grad_helper.py:33): fp32 grads
+ * get one fp32 multiply, bf16 grads are widened, multiplied and rounded back RNE.
+ */
+int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                  int64_t n_chunks, int64_t chunk_elems, const float* d_coef, void* stream);
+
+/*
+ * One fused AdamW step over every tensor in the table, all groups in one launch.
+ * Replaces torch._foreach_add_(state_steps, 1) + torch._fused_adamw_
+ * (torch/optim/adam.py:877-895; math fused_adam_utils.cuh:22-92,106-199), fuses
+ * the deferred clip scale (tensors with TM_FLAG_CLIP read *d_coef) and the bf16
+ * working-copy refresh (param_bf16 != 0).
+ *   h_groups  n_groups (1..TM_MAX_GROUPS) host records; tm_tensor_t.group indexes them
+ *   d_coef    clip coefficient (device fp32), required if any tensor has TM_FLAG_CLIP
+ *   d_ws      at least tm_workspace_bytes(n_tensors) bytes
+ */
+int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                  int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups,
+                  int32_t n_groups, const float* d_coef, void* d_ws, void* stream);
+
+/*
+ * Micro-step gradient accumulation: d_acc[i] (fp32) += (float)d_micro[i] (bf16),
+ * over `numel` elements. The fp32 accumulation buffer is what torch autograd
+ * builds in p.grad across micro-batches (torchure/train/trainer.py:383-390).
+ */
+int tm_grad_accumulate_bf16(float* d_acc, const uint16_t* d_micro, int64_t numel, void* stream);
+
+/* Writes RNE(src) into dst (bf16 working-copy refresh without an update).
+ * Rounding rule of torch/headeronly/util/BFloat16.h:100-114 (NaN -> 0x7FC0). */
+int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCHURE_AMD_H */

@@ -1,0 +1,595 @@
+// tm_optim.hip -- gfx950 kernels and C ABI of the mixed-precision optimizer step.
+//
+// Kernels (all memory-bound, no MFMA):
+//   norm_partials_kernel  pass 1 of the deterministic global grad norm: a fixed grid of
+//                         TM_NORM_PARTIALS blocks, block b owns chunks b, b+G, ...; each
+//                         writes one fp64 partial sum of squares (no atomics).
+//   norm_finalize_kernel  pass 2: one block sums the partials in a fixed order, then
+//                         sqrt and the clip coefficient, both on device.
+//   adamw_prep_kernel     one thread per tensor: step += 1, bias corrections in fp64,
+//                         per-tensor constants for the update.
+//   adamw_update_kernel   one block per chunk: reads grad, master, m, v once, writes
+//                         master, m, v and the bf16 working copy once, 16-byte accesses.
+//   grad_scale_kernel     eager in-place clip (grad *= coef).
+//   accumulate_kernel     fp32 accumulation buffer += bf16 micro-step grad.
+//   cast_bf16_kernel      bf16 working copy = RNE(master).
+//
+// Arithmetic of the update follows torch's fused AdamW device functor
+// (torch/include/ATen/native/hip/fused_adam_utils.cuh:22-92,106-199): hyper-parameters
+// are double; the decay and both moment updates are evaluated in double and rounded
+// to float; bias corrections are double, narrowed to float; the final division chain
+// is float. Every rounding point is written with an explicit *_rn intrinsic so the
+// compiler cannot contract or reorder it, which lets the C oracle reproduce the
+// result bit for bit.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "torchure_amd.h"
+
+namespace {
+
+constexpr int kThreads = 256;  // 4 wave64 per block
+constexpr int kVec = 8;        // elements per thread per iteration (16 B of bf16)
+constexpr int kWaves = kThreads / 64;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(TM_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return TM_OK;
+}
+
+// Per-tensor constants produced by adamw_prep_kernel (64 bytes).
+struct alignas(16) TensorScal {
+  double neg_lrwd;  // -(lr * weight_decay)
+  double beta1;
+  double omb1;  // 1 - beta1
+  double beta2;
+  double omb2;  // 1 - beta2
+  double eps;
+  float step_size;  // float(lr / double(float(1 - beta1^step)))
+  float bc2s;       // float(sqrt(1 - beta2^step))
+  uint32_t decay;   // weight_decay != 0
+  uint32_t pad;
+};
+
+constexpr size_t kPartialBytes = sizeof(double) * TM_NORM_PARTIALS;
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// ---------------------------------------------------------------- element helpers
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ float bf16_at(const uint16_t* p, int64_t i) {
+  return __uint_as_float(static_cast<uint32_t>(p[i]) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16, NaN -> 0x7FC0
+// (torch/include/torch/headeronly/util/BFloat16.h:100-114).
+__device__ __forceinline__ uint32_t bf16_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (f != f) ? 0x7FC0u : r;
+}
+
+template <bool kNT, typename T>
+__device__ __forceinline__ T ld(const T* p) {
+  if constexpr (kNT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <bool kNT, typename T>
+__device__ __forceinline__ void st(T* p, T v) {
+  if constexpr (kNT) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
+// One AdamW element. p, m, v are the fp32 values in memory; g is the (clipped) fp32
+// grad. Statement by statement (fused_adam_utils.cuh line numbers):
+//   :63-64  p = float(double(p) - (lr*wd) * double(p))           [if wd != 0]
+//   :69     m = float(beta1 * double(m) + (1 - beta1) * double(g))
+//   :70     v = float(beta2 * double(v) + (1 - beta2) * double(g) * double(g))
+//   :77     denom = float(double(sqrtf(v) / bc2s) + eps)
+//   :79     p = p - (step_size * m) / denom                       [float]
+// The double sums are single fused multiply-adds (the contraction hipcc applies to
+// the functor's expressions); the oracle uses the same fma() calls.
+__device__ __forceinline__ void adamw_elem(float& p, float& m, float& v, float g,
+                                           const TensorScal& c) {
+  if (c.decay) {
+    const double pd = static_cast<double>(p);
+    p = static_cast<float>(__fma_rn(c.neg_lrwd, pd, pd));
+  }
+  const double gd = static_cast<double>(g);
+  m = static_cast<float>(__fma_rn(c.beta1, static_cast<double>(m), __dmul_rn(c.omb1, gd)));
+  v = static_cast<float>(
+      __fma_rn(c.beta2, static_cast<double>(v), __dmul_rn(__dmul_rn(c.omb2, gd), gd)));
+  const float q = __fdiv_rn(__fsqrt_rn(v), c.bc2s);
+  const float denom = static_cast<float>(__dadd_rn(static_cast<double>(q), c.eps));
+  p = __fsub_rn(p, __fdiv_rn(__fmul_rn(c.step_size, m), denom));
+}
+
+__device__ __forceinline__ bool aligned16(uint64_t a) { return (a & 15u) == 0; }
+
+// ------------------------------------------------------------------- reductions
+
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// Fixed-order block sum; the result is valid in thread 0.
+__device__ __forceinline__ double block_sum(double x) {
+  __shared__ double lds[kWaves];
+  x = wave_sum(x);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (lane == 0) lds[wave] = x;
+  __syncthreads();
+  double s = 0.0;
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += lds[w];
+  }
+  return s;
+}
+
+// ------------------------------------------------------------------- norm pass 1
+
+__global__ __launch_bounds__(kThreads) void norm_partials_kernel(
+    const tm_tensor_t* __restrict__ tensors, int64_t n_tensors,
+    const tm_chunk_t* __restrict__ chunks, int64_t n_chunks, int64_t chunk_elems,
+    double* __restrict__ partials) {
+  double acc = 0.0;
+  for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+    const tm_chunk_t ck = chunks[c];
+    if (ck.tensor >= n_tensors) continue;
+    const tm_tensor_t d = tensors[ck.tensor];
+    const int64_t start = static_cast<int64_t>(ck.chunk) * chunk_elems;
+    if (start >= d.numel) continue;
+    const int64_t end = min(start + chunk_elems, d.numel);
+    if (d.flags & TM_GRAD_F32) {
+      const float* __restrict__ g = reinterpret_cast<const float*>(d.grad);
+      if (aligned16(d.grad)) {
+        const int64_t vend = start + ((end - start) & ~int64_t(kVec - 1));
+        for (int64_t i = start + threadIdx.x * kVec; i < vend; i += kThreads * kVec) {
+          const f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(g + i));
+          const f32x4 b = ld<true>(reinterpret_cast<const f32x4*>(g + i + 4));
+          double s = 0.0;
+          s = __fma_rn((double)a.x, (double)a.x, s);
+          s = __fma_rn((double)a.y, (double)a.y, s);
+          s = __fma_rn((double)a.z, (double)a.z, s);
+          s = __fma_rn((double)a.w, (double)a.w, s);
+          s = __fma_rn((double)b.x, (double)b.x, s);
+          s = __fma_rn((double)b.y, (double)b.y, s);
+          s = __fma_rn((double)b.z, (double)b.z, s);
+          s = __fma_rn((double)b.w, (double)b.w, s);
+          acc += s;
+        }
+        for (int64_t i = vend + threadIdx.x; i < end; i += kThreads)
+          acc = __fma_rn((double)g[i], (double)g[i], acc);
+      } else {
+        for (int64_t i = start + threadIdx.x; i < end; i += kThreads)
+          acc = __fma_rn((double)g[i], (double)g[i], acc);
+      }
+    } else {
+      const uint16_t* __restrict__ g = reinterpret_cast<const uint16_t*>(d.grad);
+      if (aligned16(d.grad)) {
+        const int64_t vend = start + ((end - start) & ~int64_t(kVec - 1));
+        for (int64_t i = start + threadIdx.x * kVec; i < vend; i += kThreads * kVec) {
+          const u32x4 w = ld<true>(reinterpret_cast<const u32x4*>(g + i));
+          // bf16 squares are exact in fp32 (8-bit significands); 8 of them are summed
+          // in fp32 and the group sum is accumulated in fp64.
+          float s = 0.f;
+          float x;
+          x = bf16_lo(w.x); s = __fmaf_rn(x, x, s);
+          x = bf16_hi(w.x); s = __fmaf_rn(x, x, s);
+          x = bf16_lo(w.y); s = __fmaf_rn(x, x, s);
+          x = bf16_hi(w.y); s = __fmaf_rn(x, x, s);
+          x = bf16_lo(w.z); s = __fmaf_rn(x, x, s);
+          x = bf16_hi(w.z); s = __fmaf_rn(x, x, s);
+          x = bf16_lo(w.w); s = __fmaf_rn(x, x, s);
+          x = bf16_hi(w.w); s = __fmaf_rn(x, x, s);
+          acc += static_cast<double>(s);
+        }
+        for (int64_t i = vend + threadIdx.x; i < end; i += kThreads) {
+          const double x = bf16_at(g, i);
+          acc = __fma_rn(x, x, acc);
+        }
+      } else {
+        for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
+          const double x = bf16_at(g, i);
+          acc = __fma_rn(x, x, acc);
+        }
+      }
+    }
+  }
+  const double s = block_sum(acc);
+  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+}
+
+// ------------------------------------------------------------------- norm pass 2
+
+// clip coefficient of torchure/core/grad_helper.py:32, evaluated as torch evaluates
+// `max_norm / (total + 1e-6)` on a 0-d fp32 tensor: fp32 add of 1e-6f, fp32
+// reciprocal, fp32 multiply by float(max_norm), then clamp(max=1) with NaN passing
+// through (torch/_tensor.py:1119-1122).
+__global__ __launch_bounds__(kThreads) void norm_finalize_kernel(
+    const double* __restrict__ partials, float max_norm, int clip, float* __restrict__ norm_out,
+    float* __restrict__ coef_out) {
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < TM_NORM_PARTIALS; i += kThreads) acc += partials[i];
+  const double total = block_sum(acc);
+  if (threadIdx.x == 0) {
+    const float norm = static_cast<float>(sqrt(total));
+    *norm_out = norm;
+    if (clip) {
+      const float r = __fdiv_rn(1.0f, __fadd_rn(norm, 1e-6f));
+      const float c = __fmul_rn(r, max_norm);
+      *coef_out = (c > 1.0f) ? 1.0f : c;
+    }
+  }
+}
+
+// ------------------------------------------------------------------- grad scale
+
+__global__ __launch_bounds__(kThreads) void grad_scale_kernel(
+    const tm_tensor_t* __restrict__ tensors, int64_t n_tensors,
+    const tm_chunk_t* __restrict__ chunks, int64_t chunk_elems, const float* __restrict__ coef_p) {
+  const tm_chunk_t ck = chunks[blockIdx.x];
+  if (ck.tensor >= n_tensors) return;
+  const tm_tensor_t d = tensors[ck.tensor];
+  const int64_t start = static_cast<int64_t>(ck.chunk) * chunk_elems;
+  if (start >= d.numel) return;
+  const int64_t end = min(start + chunk_elems, d.numel);
+  const float coef = *coef_p;
+  if (d.flags & TM_GRAD_F32) {
+    float* __restrict__ g = reinterpret_cast<float*>(d.grad);
+    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) g[i] = __fmul_rn(g[i], coef);
+  } else {
+    uint16_t* __restrict__ g = reinterpret_cast<uint16_t*>(d.grad);
+    for (int64_t i = start + threadIdx.x; i < end; i += kThreads)
+      g[i] = static_cast<uint16_t>(bf16_rne(__fmul_rn(bf16_at(g, i), coef)));
+  }
+}
+
+// ------------------------------------------------------------------- AdamW prep
+
+struct HyperArgs {
+  tm_hyper_t g[TM_MAX_GROUPS];
+  int32_t n;
+};
+
+// step += 1 and the per-tensor constants (fused_adam_utils.cuh:128-139; adam.py:877).
+__global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
+    const tm_tensor_t* __restrict__ tensors, int64_t n_tensors, HyperArgs hyper,
+    TensorScal* __restrict__ scal) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (t >= n_tensors) return;
+  const tm_tensor_t d = tensors[t];
+  int32_t gi = d.group;
+  if (gi < 0 || gi >= hyper.n) gi = 0;
+  const tm_hyper_t h = hyper.g[gi];
+  float* step_p = reinterpret_cast<float*>(d.step);
+  const float step = __fadd_rn(*step_p, 1.0f);
+  *step_p = step;
+  const double bc1 = 1.0 - pow(h.beta1, static_cast<double>(step));
+  const double bc2 = 1.0 - pow(h.beta2, static_cast<double>(step));
+  const float bc1f = static_cast<float>(bc1);
+  TensorScal s;
+  s.neg_lrwd = -(h.lr * h.weight_decay);
+  s.beta1 = h.beta1;
+  s.omb1 = 1.0 - h.beta1;
+  s.beta2 = h.beta2;
+  s.omb2 = 1.0 - h.beta2;
+  s.eps = h.eps;
+  s.step_size = static_cast<float>(h.lr / static_cast<double>(bc1f));
+  s.bc2s = static_cast<float>(sqrt(bc2));
+  s.decay = h.weight_decay != 0.0;
+  s.pad = 0;
+  scal[t] = s;
+}
+
+// ------------------------------------------------------------------- AdamW update
+
+template <bool kGradF32, bool kOut, bool kNT>
+__device__ __forceinline__ void update_vector(const tm_tensor_t& d, int64_t start, int64_t vend,
+                                              const TensorScal& c, bool clip, float coef) {
+  float* __restrict__ P = reinterpret_cast<float*>(d.master);
+  float* __restrict__ M = reinterpret_cast<float*>(d.exp_avg);
+  float* __restrict__ V = reinterpret_cast<float*>(d.exp_avg_sq);
+  uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(d.param_bf16);
+#pragma unroll 2
+  for (int64_t i = start + threadIdx.x * kVec; i < vend; i += kThreads * kVec) {
+    float g[kVec];
+    if constexpr (kGradF32) {
+      const float* G = reinterpret_cast<const float*>(d.grad);
+      const f32x4 a = ld<kNT>(reinterpret_cast<const f32x4*>(G + i));
+      const f32x4 b = ld<kNT>(reinterpret_cast<const f32x4*>(G + i + 4));
+      g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
+      g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
+    } else {
+      const uint16_t* G = reinterpret_cast<const uint16_t*>(d.grad);
+      const u32x4 w = ld<kNT>(reinterpret_cast<const u32x4*>(G + i));
+      g[0] = bf16_lo(w.x); g[1] = bf16_hi(w.x); g[2] = bf16_lo(w.y); g[3] = bf16_hi(w.y);
+      g[4] = bf16_lo(w.z); g[5] = bf16_hi(w.z); g[6] = bf16_lo(w.w); g[7] = bf16_hi(w.w);
+    }
+    const f32x4 p0 = ld<kNT>(reinterpret_cast<const f32x4*>(P + i));
+    const f32x4 p1 = ld<kNT>(reinterpret_cast<const f32x4*>(P + i + 4));
+    const f32x4 m0 = ld<kNT>(reinterpret_cast<const f32x4*>(M + i));
+    const f32x4 m1 = ld<kNT>(reinterpret_cast<const f32x4*>(M + i + 4));
+    const f32x4 v0 = ld<kNT>(reinterpret_cast<const f32x4*>(V + i));
+    const f32x4 v1 = ld<kNT>(reinterpret_cast<const f32x4*>(V + i + 4));
+    float p[kVec] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    float m[kVec] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    float v[kVec] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const float gj = clip ? __fmul_rn(g[j], coef) : g[j];
+      adamw_elem(p[j], m[j], v[j], gj, c);
+    }
+    st<kNT>(reinterpret_cast<f32x4*>(P + i), f32x4{p[0], p[1], p[2], p[3]});
+    st<kNT>(reinterpret_cast<f32x4*>(P + i + 4), f32x4{p[4], p[5], p[6], p[7]});
+    st<kNT>(reinterpret_cast<f32x4*>(M + i), f32x4{m[0], m[1], m[2], m[3]});
+    st<kNT>(reinterpret_cast<f32x4*>(M + i + 4), f32x4{m[4], m[5], m[6], m[7]});
+    st<kNT>(reinterpret_cast<f32x4*>(V + i), f32x4{v[0], v[1], v[2], v[3]});
+    st<kNT>(reinterpret_cast<f32x4*>(V + i + 4), f32x4{v[4], v[5], v[6], v[7]});
+    if constexpr (kOut) {
+      u32x4 o;
+      o.x = bf16_rne(p[0]) | (bf16_rne(p[1]) << 16);
+      o.y = bf16_rne(p[2]) | (bf16_rne(p[3]) << 16);
+      o.z = bf16_rne(p[4]) | (bf16_rne(p[5]) << 16);
+      o.w = bf16_rne(p[6]) | (bf16_rne(p[7]) << 16);
+      st<kNT>(reinterpret_cast<u32x4*>(O + i), o);
+    }
+  }
+}
+
+// Element-at-a-time path: the tail of a tensor whose length is not a multiple of 8,
+// and whole tensors whose pointers are not 16-byte aligned.
+__device__ __forceinline__ void update_scalar(const tm_tensor_t& d, int64_t start, int64_t end,
+                                              const TensorScal& c, bool clip, float coef) {
+  float* P = reinterpret_cast<float*>(d.master);
+  float* M = reinterpret_cast<float*>(d.exp_avg);
+  float* V = reinterpret_cast<float*>(d.exp_avg_sq);
+  uint16_t* O = reinterpret_cast<uint16_t*>(d.param_bf16);
+  const bool f32 = (d.flags & TM_GRAD_F32) != 0;
+  for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
+    float g = f32 ? reinterpret_cast<const float*>(d.grad)[i]
+                  : bf16_at(reinterpret_cast<const uint16_t*>(d.grad), i);
+    if (clip) g = __fmul_rn(g, coef);
+    float p = P[i], m = M[i], v = V[i];
+    adamw_elem(p, m, v, g, c);
+    P[i] = p;
+    M[i] = m;
+    V[i] = v;
+    if (O) O[i] = static_cast<uint16_t>(bf16_rne(p));
+  }
+}
+
+template <bool kNT>
+__global__ __launch_bounds__(kThreads) void adamw_update_kernel(
+    const tm_tensor_t* __restrict__ tensors, int64_t n_tensors,
+    const tm_chunk_t* __restrict__ chunks, int64_t chunk_elems,
+    const TensorScal* __restrict__ scal, const float* __restrict__ coef_p) {
+  const tm_chunk_t ck = chunks[blockIdx.x];
+  if (ck.tensor >= n_tensors) return;
+  const tm_tensor_t d = tensors[ck.tensor];
+  const int64_t start = static_cast<int64_t>(ck.chunk) * chunk_elems;
+  if (start >= d.numel) return;
+  const int64_t end = min(start + chunk_elems, d.numel);
+  const TensorScal c = scal[ck.tensor];
+  const bool clip = (d.flags & TM_FLAG_CLIP) != 0;
+  const float coef = clip ? *coef_p : 1.0f;
+  const bool out = d.param_bf16 != 0;
+  const bool vec = aligned16(d.master) && aligned16(d.exp_avg) && aligned16(d.exp_avg_sq) &&
+                   aligned16(d.grad) && (!out || aligned16(d.param_bf16));
+  int64_t vend = start;
+  if (vec) {
+    vend = start + ((end - start) & ~int64_t(kVec - 1));
+    if (d.flags & TM_GRAD_F32) {
+      if (out) update_vector<true, true, kNT>(d, start, vend, c, clip, coef);
+      else update_vector<true, false, kNT>(d, start, vend, c, clip, coef);
+    } else {
+      if (out) update_vector<false, true, kNT>(d, start, vend, c, clip, coef);
+      else update_vector<false, false, kNT>(d, start, vend, c, clip, coef);
+    }
+  }
+  if (vend < end) update_scalar(d, vend, end, c, clip, coef);
+}
+
+// ------------------------------------------------------------------- elementwise
+
+__global__ __launch_bounds__(kThreads) void accumulate_kernel(float* __restrict__ acc,
+                                                              const uint16_t* __restrict__ micro,
+                                                              int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads * kVec;
+  const bool vec = aligned16(reinterpret_cast<uint64_t>(acc)) &&
+                   aligned16(reinterpret_cast<uint64_t>(micro));
+  const int64_t vend = vec ? (n & ~int64_t(kVec - 1)) : 0;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * kVec; i < vend;
+       i += stride) {
+    const u32x4 w = ld<true>(reinterpret_cast<const u32x4*>(micro + i));
+    f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(acc + i));
+    f32x4 b = ld<true>(reinterpret_cast<const f32x4*>(acc + i + 4));
+    a.x = __fadd_rn(a.x, bf16_lo(w.x)); a.y = __fadd_rn(a.y, bf16_hi(w.x));
+    a.z = __fadd_rn(a.z, bf16_lo(w.y)); a.w = __fadd_rn(a.w, bf16_hi(w.y));
+    b.x = __fadd_rn(b.x, bf16_lo(w.z)); b.y = __fadd_rn(b.y, bf16_hi(w.z));
+    b.z = __fadd_rn(b.z, bf16_lo(w.w)); b.w = __fadd_rn(b.w, bf16_hi(w.w));
+    st<true>(reinterpret_cast<f32x4*>(acc + i), a);
+    st<true>(reinterpret_cast<f32x4*>(acc + i + 4), b);
+  }
+  for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    acc[i] = __fadd_rn(acc[i], bf16_at(micro, i));
+}
+
+__global__ __launch_bounds__(kThreads) void cast_bf16_kernel(uint16_t* __restrict__ dst,
+                                                             const float* __restrict__ src,
+                                                             int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride)
+    dst[i] = static_cast<uint16_t>(bf16_rne(src[i]));
+}
+
+int grid_for(int64_t n, int64_t per_block) {
+  int64_t b = (n + per_block - 1) / per_block;
+  if (b < 1) b = 1;
+  if (b > 65536) b = 65536;
+  return static_cast<int>(b);
+}
+
+int check_table(const void* d_tensors, int64_t n_tensors, const void* d_chunks, int64_t n_chunks,
+                int64_t chunk_elems, const char* who) {
+  if (n_tensors < 0 || n_chunks < 0) return fail(TM_EINVAL, "%s: negative size", who);
+  if (n_tensors > 0 && !d_tensors) return fail(TM_EINVAL, "%s: null tensor table", who);
+  if (n_chunks > 0 && !d_chunks) return fail(TM_EINVAL, "%s: null chunk table", who);
+  if (n_tensors > 0xFFFFFFFFll) return fail(TM_EINVAL, "%s: too many tensors", who);
+  if (n_chunks > 0x7FFFFFFFll) return fail(TM_EINVAL, "%s: too many chunks", who);
+  if (chunk_elems <= 0 || chunk_elems % TM_CHUNK_ALIGN != 0 || chunk_elems > (int64_t(1) << 30))
+    return fail(TM_EINVAL, "%s: chunk_elems %lld must be a positive multiple of %d, <= 2^30", who,
+                (long long)chunk_elems, TM_CHUNK_ALIGN);
+  return TM_OK;
+}
+
+}  // namespace
+
+// ======================================================================= C ABI
+
+extern "C" {
+
+int tm_abi_version(void) { return TM_ABI_VERSION; }
+
+const char* tm_last_error(void) { return g_err; }
+
+size_t tm_workspace_bytes(int64_t n_tensors) {
+  if (n_tensors < 0) n_tensors = 0;
+  return align_up(kPartialBytes, 256) + align_up(sizeof(TensorScal) * n_tensors, 256);
+}
+
+int64_t tm_count_chunks(const int64_t* h_numels, int64_t n_tensors, int64_t chunk_elems) {
+  if (!h_numels && n_tensors > 0) return fail(TM_EINVAL, "tm_count_chunks: null numels");
+  if (chunk_elems <= 0) return fail(TM_EINVAL, "tm_count_chunks: chunk_elems <= 0");
+  int64_t total = 0;
+  for (int64_t t = 0; t < n_tensors; ++t) {
+    if (h_numels[t] < 0) return fail(TM_EINVAL, "tm_count_chunks: negative numel at %lld", (long long)t);
+    total += (h_numels[t] + chunk_elems - 1) / chunk_elems;
+  }
+  return total;
+}
+
+int64_t tm_fill_chunks(const int64_t* h_numels, int64_t n_tensors, int64_t chunk_elems,
+                       tm_chunk_t* h_out, int64_t cap) {
+  const int64_t need = tm_count_chunks(h_numels, n_tensors, chunk_elems);
+  if (need < 0) return need;
+  if (need > cap || (need > 0 && !h_out))
+    return fail(TM_EINVAL, "tm_fill_chunks: need %lld entries, capacity %lld", (long long)need,
+                (long long)cap);
+  if (n_tensors > 0xFFFFFFFFll) return fail(TM_EINVAL, "tm_fill_chunks: too many tensors");
+  int64_t k = 0;
+  for (int64_t t = 0; t < n_tensors; ++t) {
+    const int64_t nc = (h_numels[t] + chunk_elems - 1) / chunk_elems;
+    if (nc > 0xFFFFFFFFll) return fail(TM_EINVAL, "tm_fill_chunks: tensor %lld too large", (long long)t);
+    for (int64_t c = 0; c < nc; ++c) {
+      h_out[k].tensor = static_cast<uint32_t>(t);
+      h_out[k].chunk = static_cast<uint32_t>(c);
+      ++k;
+    }
+  }
+  return k;
+}
+
+int tm_grad_norm(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                 int64_t n_chunks, int64_t chunk_elems, float max_norm, int clip, void* d_ws,
+                 float* d_norm, float* d_coef, void* stream) {
+  int rc = check_table(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, "tm_grad_norm");
+  if (rc) return rc;
+  if (!d_ws || !d_norm) return fail(TM_EINVAL, "tm_grad_norm: null workspace or norm output");
+  if (clip && !d_coef) return fail(TM_EINVAL, "tm_grad_norm: clip requested with null coef output");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  double* partials = static_cast<double*>(d_ws);
+  hipLaunchKernelGGL(norm_partials_kernel, dim3(TM_NORM_PARTIALS), dim3(kThreads), 0, s, d_tensors,
+                     n_tensors, d_chunks, n_chunks, chunk_elems, partials);
+  if ((rc = check_launch("norm_partials_kernel"))) return rc;
+  hipLaunchKernelGGL(norm_finalize_kernel, dim3(1), dim3(kThreads), 0, s, partials, max_norm, clip,
+                     d_norm, d_coef);
+  return check_launch("norm_finalize_kernel");
+}
+
+int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                  int64_t n_chunks, int64_t chunk_elems, const float* d_coef, void* stream) {
+  int rc = check_table(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, "tm_grad_scale");
+  if (rc) return rc;
+  if (!d_coef) return fail(TM_EINVAL, "tm_grad_scale: null coef");
+  if (n_chunks == 0) return TM_OK;
+  hipLaunchKernelGGL(grad_scale_kernel, dim3(static_cast<uint32_t>(n_chunks)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), d_tensors, n_tensors, d_chunks, chunk_elems,
+                     d_coef);
+  return check_launch("grad_scale_kernel");
+}
+
+int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                  int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups,
+                  int32_t n_groups, const float* d_coef, void* d_ws, void* stream) {
+  int rc = check_table(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, "tm_adamw_step");
+  if (rc) return rc;
+  if (n_groups < 1 || n_groups > TM_MAX_GROUPS || !h_groups)
+    return fail(TM_EINVAL, "tm_adamw_step: n_groups %d outside 1..%d", n_groups, TM_MAX_GROUPS);
+  if (!d_ws) return fail(TM_EINVAL, "tm_adamw_step: null workspace");
+  if (n_tensors == 0) return TM_OK;
+  HyperArgs hyper;
+  memset(&hyper, 0, sizeof(hyper));
+  for (int i = 0; i < n_groups; ++i) hyper.g[i] = h_groups[i];
+  hyper.n = n_groups;
+  TensorScal* scal =
+      reinterpret_cast<TensorScal*>(static_cast<char*>(d_ws) + align_up(kPartialBytes, 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(adamw_prep_kernel, dim3(static_cast<uint32_t>((n_tensors + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, s, d_tensors, n_tensors, hyper, scal);
+  if ((rc = check_launch("adamw_prep_kernel"))) return rc;
+  if (n_chunks == 0) return TM_OK;
+  // d_coef may be null only when no tensor asks for the clip; the kernel reads it
+  // only for TM_FLAG_CLIP tensors, so point it at the workspace otherwise.
+  const float* coef = d_coef ? d_coef : reinterpret_cast<const float*>(d_ws);
+  hipLaunchKernelGGL(adamw_update_kernel<true>, dim3(static_cast<uint32_t>(n_chunks)), dim3(kThreads),
+                     0, s, d_tensors, n_tensors, d_chunks, chunk_elems, scal, coef);
+  return check_launch("adamw_update_kernel");
+}
+
+int tm_grad_accumulate_bf16(float* d_acc, const uint16_t* d_micro, int64_t numel, void* stream) {
+  if (numel < 0) return fail(TM_EINVAL, "tm_grad_accumulate_bf16: negative numel");
+  if (numel == 0) return TM_OK;
+  if (!d_acc || !d_micro) return fail(TM_EINVAL, "tm_grad_accumulate_bf16: null pointer");
+  hipLaunchKernelGGL(accumulate_kernel, dim3(grid_for(numel, kThreads * kVec * 4)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), d_acc, d_micro, numel);
+  return check_launch("accumulate_kernel");
+}
+
+int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* stream) {
+  if (numel < 0) return fail(TM_EINVAL, "tm_cast_bf16: negative numel");
+  if (numel == 0) return TM_OK;
+  if (!d_dst || !d_src) return fail(TM_EINVAL, "tm_cast_bf16: null pointer");
+  hipLaunchKernelGGL(cast_bf16_kernel, dim3(grid_for(numel, kThreads * 8)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), d_dst, d_src, numel);
+  return check_launch("cast_bf16_kernel");
+}
+
+}  // extern "C"
