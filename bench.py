@@ -1,0 +1,264 @@
+"""Benchmark of the MI355X optimizer step (clip + fused AdamW + bf16 refresh).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen3-4b|qwen3-0.6b|...]
+
+One "step" = clip_grad_norm (two-pass norm) + AdamW.step() (step counters,
+fused update, bf16 working copies) over the whole parameter set, through the
+package's public API, with every tensor already resident in HBM. Inputs are
+synthetic (steady state of BASELINE config 4: master ~ N(0, .02),
+m ~ N(0, 1e-4), v = |N(0,1)| * 1e-8, bf16 grads ~ N(0, 1e-3), step 1000,
+lr 3e-4, betas (0.9, 0.95), wd 0.1 on >=2-D, clip 1.0).
+
+Prints one JSON line. ``value`` is whole-step throughput in GB/s of
+algorithmic traffic (30 B/param: 2 for the norm pass, 28 for the update);
+``roofline`` is for the dominant kernel (the fused update, 28 B/param), timed
+with events on the stream it runs on; ``cpu_baseline`` times the reference
+composition (torch CPU: foreach-norm clip + torch.optim.AdamW(fused=True) +
+bf16 cast) on a bounded sample of the same parameter set on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+UPDATE_BYTES_PER_PARAM = 28  # grad 2 + master/m/v 12 read; master/m/v 12 + bf16 2 written
+NORM_BYTES_PER_PARAM = 2
+STEP_BYTES_PER_PARAM = UPDATE_BYTES_PER_PARAM + NORM_BYTES_PER_PARAM
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="qwen3-4b")
+    ap.add_argument("--chunk-elems", type=int, default=None)
+    ap.add_argument("--cpu-sample-blocks", type=int, default=2,
+                    help="transformer blocks of the config timed for the CPU baseline (0 = skip)")
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--also", default="qwen3-0.6b",
+                    help="comma list of extra configs reported under 'extra' (empty = none)")
+    return ap.parse_args()
+
+
+def build_state(config: str, chunk_elems, dev):
+    import torch
+
+    import torchure_amd as ta
+    from torchure_amd.core import tables
+    from torchure_amd.workloads import shapes_for
+
+    shapes = shapes_for(config)
+    g = torch.Generator(device=dev).manual_seed(1234)
+    params = [torch.nn.Parameter(torch.randn(s, device=dev, generator=g) * 0.02) for s in shapes]
+    work = ta.attach_bf16_working_params(params)
+    for w in work:
+        w.grad = (torch.randn(w.shape, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
+                             {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True,
+                              "chunk_elems": chunk_elems or tables.DEFAULT_CHUNK_ELEMS})
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=dev)
+        st["exp_avg"] = torch.randn(p.shape, device=dev, generator=g) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, device=dev, generator=g).abs_() * 1e-8
+    torch.cuda.synchronize()
+    n_params = sum(p.numel() for p in params)
+    return params, work, opt, n_params
+
+
+def run_gpu(config: str, steps: int, warmup: int, chunk_elems, dev):
+    import torch
+
+    import torchure_amd as ta
+
+    params, work, opt, n_params = build_state(config, chunk_elems, dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def one_step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        ta.clip_grad_norm(params, None, 1.0)
+        if ev is not None:
+            ev[1].record(stream)
+        opt.step()
+        if ev is not None:
+            ev[2].record(stream)
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        one_step(evs[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ev_ms = [e[0].elapsed_time(e[2]) for e in evs]
+
+    # Kernel timing: the same launches back to back, bracketed by events on the
+    # stream they run on, so host-side work never shows up as device time.
+    from torchure_amd.core.grad_helper import NormLaunch
+
+    norm_l = NormLaunch([w.grad for w in work], 1.0)
+    norm_l()
+    upd = opt.plan_step(norm_l.coef, {id(p) for p in params})  # clip fused, as in a step
+    assert len(upd) == 1
+    reps = max(5, min(steps, 50))
+    a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        norm_l()
+    b.record(stream)
+    for _ in range(reps):
+        upd[0]()
+    c.record(stream)
+    torch.cuda.synchronize()
+    norm_ms = [a.elapsed_time(b) / reps]
+    upd_ms = [b.elapsed_time(c) / reps]
+    out = dict(
+        config=config,
+        n_params=n_params,
+        n_tensors=len(params),
+        ms_per_step=wall * 1e3 / steps,
+        ms_per_step_events_median=statistics.median(step_ev_ms),
+        norm_ms_mean=statistics.fmean(norm_ms),
+        update_ms_mean=statistics.fmean(upd_ms),
+        kernel_reps=reps,
+    )
+    del params, work, opt
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_cpu_baseline(config: str, blocks: int, steps: int):
+    """Reference composition on torch CPU over the first ``blocks`` transformer
+    blocks of ``config`` (the sample), bf16 grads widened to fp32."""
+    import torch
+
+    from oracle.torch_composition import make_reference_optimizer, reference_step
+    from torchure_amd.workloads import shapes_for
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    shapes = shapes_for(config)
+    sample = shapes[1:1 + 11 * blocks]
+    g = torch.Generator().manual_seed(99)
+    params = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in sample]
+    for p in params:
+        p.grad = (torch.randn(p.shape, generator=g) * 1e-3).to(torch.bfloat16).float()
+    opt = make_reference_optimizer(params)
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(1000.0)
+        st["exp_avg"] = torch.randn(p.shape, generator=g) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, generator=g).abs_() * 1e-8
+    bf16 = [torch.empty(p.shape, dtype=torch.bfloat16) for p in params]
+    n = sum(p.numel() for p in params)
+    reference_step(params, opt, 1.0, bf16)  # warm-up
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        reference_step(params, opt, 1.0, bf16)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return dict(
+        value=round(n * STEP_BYTES_PER_PARAM / med / 1e9, 3),
+        unit="GB/s",
+        cores=threads,
+        kind="port",
+        sample=(f"{config} blocks 0..{blocks - 1} ({len(params)} tensors, {n} params), median of "
+                f"{steps} steps after 1 warm-up, {med * 1e3:.1f} ms/step; torch CPU foreach-norm clip + "
+                f"AdamW(fused=True) + bf16 cast; GB/s on the same 30 B/param basis"),
+    )
+
+
+def load_traffic(config: str):
+    path = os.path.join(ROOT, "profiles", f"adamw_update_{config}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "optimizer step has no cross-GPU path here", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    import torchure_amd
+
+    torchure_amd._native.lib()
+
+    main_res = run_gpu(args.config, args.steps, args.warmup, args.chunk_elems, dev)
+    print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
+    extra = {}
+    for cfg in [c for c in args.also.split(",") if c and c != args.config]:
+        r = run_gpu(cfg, args.steps, args.warmup, args.chunk_elems, dev)
+        r["GBps"] = round(r["n_params"] * STEP_BYTES_PER_PARAM / (r["ms_per_step"] * 1e-3) / 1e9, 1)
+        r["frac_of_peak"] = round(r["GBps"] / PEAK_HBM_GBS, 4)
+        extra[cfg] = r
+        print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
+
+    n = main_res["n_params"]
+    ms = main_res["ms_per_step"]
+    value = n * STEP_BYTES_PER_PARAM / (ms * 1e-3) / 1e9
+    upd_gbs = n * UPDATE_BYTES_PER_PARAM / (main_res["update_ms_mean"] * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_sample_blocks > 0:
+        cpu = run_cpu_baseline(args.config, args.cpu_sample_blocks, args.cpu_steps)
+    line = {
+        "metric": "optimizer step ms + achieved HBM GB/s (% of peak), Qwen3-0.6B & 4B shapes",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 (fp64 intermediates), bf16 grads/params",
+        "data": "synthetic (seeded steady-state optimizer inputs; no dataset)",
+        "config": {"workload": f"{args.config} optimizer step: clip 1.0 + AdamW + bf16 refresh",
+                   "params": n, "tensors": main_res["n_tensors"], "bytes_per_param": STEP_BYTES_PER_PARAM,
+                   "grad_dtype": "bf16"},
+        "frac_of_peak": round(value / PEAK_HBM_GBS, 4),
+        "params_per_s": round(n / (ms * 1e-3), 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "adamw_update_kernel",
+            "achieved": round(upd_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(upd_gbs / PEAK_HBM_GBS, 4),
+            "traffic": load_traffic(args.config),
+            "launch_ms_mean": round(main_res["update_ms_mean"], 4),
+            "norm_ms_mean": round(main_res["norm_ms_mean"], 4),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

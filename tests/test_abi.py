@@ -1,0 +1,103 @@
+"""The C-ABI library loads and exports everything include/torchure_amd.h declares.
+
+No compute call needs a GPU here: only the host-side table helpers and the
+argument validation, which return before any HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from torchure_amd import _native
+
+
+def _header() -> str:
+    with open(_native.HEADER_PATH) as f:
+        return f.read()
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", _header(), flags=re.S)
+    return sorted(set(re.findall(r"\b(tm_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    declared = _declared_functions()
+    assert declared, "no tm_* functions parsed from the header"
+    assert sorted(_native.EXPORTED) == declared
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_constants():
+    h = _header()
+    assert int(re.search(r"#define TM_ABI_VERSION (\d+)", h).group(1)) == _native.lib().tm_abi_version()
+    for name in ("TM_GRAD_F32", "TM_FLAG_CLIP", "TM_MAX_GROUPS", "TM_CHUNK_ALIGN", "TM_NORM_PARTIALS"):
+        val = int(re.search(rf"#define {name} (\d+)u?", h).group(1))
+        assert getattr(_native, name) == val, name
+
+
+def test_tensor_record_layout_matches_header():
+    body = re.search(r"typedef struct tm_tensor \{(.*?)\} tm_tensor_t;", _header(), re.S).group(1)
+    fields = re.findall(r"\b(?:uint64_t|int64_t|int32_t|uint32_t)\s+(\w+);", body)
+    assert tuple(fields) == _native.TENSOR_DTYPE.names
+    assert _native.TENSOR_DTYPE.itemsize == 64
+    body = re.search(r"typedef struct tm_hyper \{(.*?)\} tm_hyper_t;", _header(), re.S).group(1)
+    assert tuple(re.findall(r"double\s+(\w+);", body)) == tuple(f for f, _ in _native.TmHyper._fields_)
+
+
+def test_chunk_table():
+    numels = np.array([0, 1, 2048, 2049, 5000, 0, 4096], dtype=np.int64)
+    t = _native.fill_chunks(numels, 2048)
+    want = [(i, c) for i, n in enumerate(numels) for c in range(-(-int(n) // 2048))]
+    assert [(int(a), int(b)) for a, b in zip(t["tensor"], t["chunk"])] == want
+    assert len(_native.fill_chunks(np.zeros(3, np.int64), 2048)) == 0
+
+
+def test_chunk_table_errors():
+    lib = _native.lib()
+    numels = np.array([5, -1], dtype=np.int64)
+    assert lib.tm_count_chunks(numels.ctypes.data, 2, 2048) < 0
+    assert b"negative numel" in lib.tm_last_error()
+    ok = np.array([5000], dtype=np.int64)
+    out = np.zeros(1, dtype=_native.CHUNK_DTYPE)
+    assert lib.tm_fill_chunks(ok.ctypes.data, 1, 2048, out.ctypes.data, 1) < 0  # capacity too small
+
+
+def test_workspace_bytes():
+    a = _native.workspace_bytes(0)
+    b = _native.workspace_bytes(1000)
+    assert a >= 8 * _native.TM_NORM_PARTIALS and a % 256 == 0
+    assert b - a >= 64 * 1000
+
+
+def test_argument_validation_without_gpu():
+    """Invalid arguments are rejected on the host before any HIP call."""
+    lib = _native.lib()
+    hyper = _native.hyper_array([(3e-4, 0.9, 0.95, 0.1, 1e-8)])
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.tm_adamw_step(fake, 1, fake, 1, 2048, hyper, 0, None, fake, None) == _native.TM_OK - 1
+    assert b"n_groups" in lib.tm_last_error()
+    assert lib.tm_adamw_step(fake, 1, fake, 1, 1000, hyper, 1, None, fake, None) < 0
+    assert b"chunk_elems" in lib.tm_last_error()
+    assert lib.tm_grad_norm(fake, 1, fake, 1, 2048, 1.0, 1, None, fake, fake, None) < 0
+    assert lib.tm_grad_norm(fake, 1, fake, 1, 2048, 1.0, 1, fake, fake, None, None) < 0
+    assert lib.tm_grad_scale(fake, 1, fake, 1, 2048, None, None) < 0
+    assert lib.tm_grad_accumulate_bf16(None, None, 10, None) < 0
+    assert lib.tm_cast_bf16(None, None, -1, None) < 0
+    assert lib.tm_grad_norm(None, 1, fake, 1, 2048, 1.0, 0, fake, fake, None, None) < 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_native, "_LIB", None)
+    monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        _native.lib()

@@ -1,0 +1,127 @@
+"""Host-side API of the drop-in (no GPU): constructor, groups, schedule, state layout, errors."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import torchure_amd as ta
+from oracle import oracle
+from torchure_amd.optimizer import AdamW, build_optimizer, build_scheduler, wsd_scale
+
+
+def _model():
+    return torch.nn.Sequential(torch.nn.Linear(8, 4), torch.nn.LayerNorm(4), torch.nn.Linear(4, 2, bias=False))
+
+
+def test_constructor_rejects_unsupported():
+    p = [torch.nn.Parameter(torch.zeros(3))]
+    for kw in ({"amsgrad": True}, {"maximize": True}, {"capturable": True}, {"differentiable": True},
+               {"fused": False}):
+        with pytest.raises(NotImplementedError):
+            AdamW(p, **kw)
+    with pytest.raises(RuntimeError, match="foreach"):
+        AdamW(p, foreach=True)
+    for kw in ({"lr": -1.0}, {"eps": -1.0}, {"betas": (1.0, 0.9)}, {"betas": (0.9, -0.1)},
+               {"weight_decay": -0.1}):
+        with pytest.raises(ValueError):
+            AdamW(p, **kw)
+    with pytest.raises(NotImplementedError):
+        AdamW(p, lr=torch.tensor(1e-3))
+    with pytest.raises(ValueError):
+        AdamW(p, chunk_elems=1000)
+
+
+def test_param_groups_have_torch_adamw_keys():
+    m1, m2 = _model(), _model()
+    mine = build_optimizer(m1, "adamw", {"lr": 3e-4, "weight_decay": 0.1, "betas": [0.9, 0.95], "fused": True})
+    groups = [
+        {"params": [p for p in m2.parameters() if p.dim() >= 2], "weight_decay": 0.1},
+        {"params": [p for p in m2.parameters() if p.dim() < 2], "weight_decay": 0.0},
+    ]
+    ref = torch.optim.AdamW(groups, lr=3e-4, betas=[0.9, 0.95], fused=True)
+    a, b = mine.state_dict(), ref.state_dict()
+    assert [sorted(g) for g in a["param_groups"]] == [sorted(g) for g in b["param_groups"]]
+    for ga, gb in zip(a["param_groups"], b["param_groups"]):
+        for k in gb:
+            if k != "betas":
+                assert ga[k] == gb[k], k
+        assert tuple(ga["betas"]) == tuple(gb["betas"])
+    # builder.py:37-43 split: 2-D weights decay, biases / norm weights do not
+    assert [len(g["params"]) for g in mine.param_groups] == [2, 3]
+    assert [g["weight_decay"] for g in mine.param_groups] == [0.1, 0.0]
+
+
+def test_load_torch_cpu_state_dict():
+    """A checkpoint of torch.optim.AdamW (what torchure's Checkpointer saves)
+    loads into the drop-in with identical state tensors and groups."""
+    m = _model()
+    ref = torch.optim.AdamW(m.parameters(), lr=1e-3)
+    for _ in range(3):
+        m(torch.randn(5, 8)).sum().backward()
+        ref.step()
+        ref.zero_grad()
+    sd = ref.state_dict()
+    mine = AdamW(m.parameters(), lr=1e-3)
+    mine.load_state_dict(sd)
+    got = mine.state_dict()
+    assert got["param_groups"] == sd["param_groups"]
+    for k in sd["state"]:
+        for key in ("step", "exp_avg", "exp_avg_sq"):
+            assert torch.equal(got["state"][k][key], sd["state"][k][key])
+
+
+def test_step_on_cpu_params_fails_loudly():
+    m = _model()
+    opt = AdamW(m.parameters())
+    m(torch.randn(2, 8)).sum().backward()
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        opt.step()
+
+
+def test_clip_errors():
+    with pytest.raises(AssertionError):
+        ta.clip_grad_norm([torch.nn.Parameter(torch.zeros(4))], None, 1.0)
+    p = torch.nn.Parameter(torch.zeros(4))
+    p.grad = torch.ones(4)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ta.clip_grad_norm([p], None, 1.0)
+    with pytest.raises(NotImplementedError):
+        ta.clip_grad_norm([p], None, 1.0, shard_dims=("dp",))
+
+
+def test_wsd_scheduler_matches_closed_form():
+    m = _model()
+    opt = AdamW(m.parameters(), lr=3e-4)
+    sched = build_scheduler(opt, {"type": "wsd", "total_steps": 100, "warmup_ratio": 0.05, "decay_ratio": 0.2})
+    for k in range(130):
+        want = 3e-4 * oracle.wsd_scale(k, 100, 0.05, 0.2)
+        assert opt.param_groups[0]["lr"] == want, k
+        assert opt.param_groups[1 if len(opt.param_groups) > 1 else 0]["lr"] == want
+        assert wsd_scale(k, 100, 0.05, 0.2) == oracle.wsd_scale(k, 100, 0.05, 0.2)
+        sched.step()
+    assert opt.param_groups[0]["initial_lr"] == 3e-4
+
+
+def test_scheduler_state_roundtrip():
+    m = _model()
+    opt = AdamW(m.parameters(), lr=3e-4)
+    s1 = build_scheduler(opt, {"type": "wsd", "total_steps": 50, "warmup_ratio": 0.1, "decay_ratio": 0.2})
+    for _ in range(17):
+        s1.step()
+    opt2 = AdamW(m.parameters(), lr=3e-4)
+    s2 = build_scheduler(opt2, {"type": "wsd", "total_steps": 50, "warmup_ratio": 0.1, "decay_ratio": 0.2})
+    s2.load_state_dict(s1.state_dict())
+    assert s2.last_epoch == 17 and s2.get_last_lr() == s1.get_last_lr()
+
+
+def test_cosine_is_refused():
+    opt = AdamW(_model().parameters())
+    with pytest.raises(NotImplementedError):
+        build_scheduler(opt, {"type": "cosine", "total_steps": 10, "warmup_ratio": 0.1, "decay_phase": 0.1,
+                              "last_epoch": -1})
+
+
+def test_sgd_registry_entry_passes_through():
+    opt = build_optimizer(_model(), "sgd", {"lr": 0.1, "weight_decay": 0.0})
+    assert isinstance(opt, torch.optim.SGD)

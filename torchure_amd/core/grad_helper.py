@@ -1,0 +1,160 @@
+"""Global grad-norm clipping on the gfx950 kernels.
+
+Counterpart of torchure/core/grad_helper.py:8-34 with the same signature,
+return value and error behaviour:
+  - the pre-clip global L2 norm is returned as a 0-d fp32 device tensor
+    (grad_helper.py:34), computed by the deterministic two-pass kernel
+    (replaces torch._foreach_norm + stack + vector_norm, grad_helper.py:17-18);
+  - clip_coef = clamp(max_norm / (total + 1e-6), max=1.0) stays on device
+    (grad_helper.py:32); it is always applied, also when it is 1.0
+    (grad_helper.py:33), which is bitwise a no-op;
+  - ``max_norm=None`` measures only (grad_helper.py:29-30);
+  - no grads at all raises AssertionError (grad_helper.py:15-16).
+
+Deferred clip. When every grad passed in belongs to one torchure_amd AdamW
+built with ``defer_clip=True`` (the default), the in-place multiply of
+grad_helper.py:33 is not run as a separate pass: the coefficient is handed to
+that optimizer, whose next ``step()`` multiplies each grad by it inside the
+fused update kernel (the same single fp32 multiply, so the update is bitwise
+the same). Until that step, ``p.grad`` holds the unscaled values;
+``AdamW.materialize_clip()`` applies the pending scale in place if a caller
+needs the clipped grads before stepping. In every other case (plain tensors,
+params of several optimizers, or ``defer_clip=False``) the grads are scaled in
+place immediately by the scale kernel, as the reference does.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from torchure_amd import _native
+from torchure_amd.core import tables
+
+
+def grads_of(params) -> tuple[list[torch.Tensor], list[torch.nn.Parameter]]:
+    """(grads, holders) for params that carry a grad, in order.
+
+    A master parameter without its own ``.grad`` contributes the bf16 grad of
+    its attached working copy (torchure_amd.optimizer.working), if any.
+    """
+    grads, holders = [], []
+    for p in params:
+        g = p.grad
+        if g is None:
+            w = getattr(p, "_tm_working", None)
+            g = w.grad if w is not None else None
+        if g is not None:
+            grads.append(g)
+            holders.append(p)
+    return grads, holders
+
+
+class NormLaunch:
+    """One ``tm_grad_norm`` call with its device tables kept alive; calling it
+    enqueues both passes on the device's current stream and writes ``norm``
+    (and ``coef`` when clipping)."""
+
+    def __init__(self, grads: list[torch.Tensor], max_norm: float | None,
+                 chunk_elems: int = tables.DEFAULT_CHUNK_ELEMS):
+        who = "clip_grad_norm"
+        device = grads[0].device
+        for g in grads:
+            if g.device != device:
+                raise RuntimeError(f"{who}: all grads must be on one device ({g.device} vs {device})")
+        rows = tables.grad_table(grads, who)
+        self.device = device
+        self.n = len(grads)
+        self.chunk_elems = chunk_elems
+        self.chunks, self.n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]),
+                                                       chunk_elems, device)
+        self.d_rows = tables.upload(rows, device)
+        self.ws = torch.empty(_native.workspace_bytes(len(grads)), dtype=torch.uint8, device=device)
+        self.norm = torch.empty((), dtype=torch.float32, device=device)
+        self.clip = max_norm is not None
+        self.max_norm = float(max_norm) if self.clip else 0.0
+        self.coef = torch.empty((), dtype=torch.float32, device=device) if self.clip else None
+
+    def __call__(self) -> None:
+        rc = _native.lib().tm_grad_norm(
+            self.d_rows.data_ptr(),
+            self.n,
+            self.chunks.data_ptr(),
+            self.n_chunks,
+            self.chunk_elems,
+            self.max_norm,
+            int(self.clip),
+            self.ws.data_ptr(),
+            self.norm.data_ptr(),
+            self.coef.data_ptr() if self.clip else None,
+            _native.stream_handle(self.device),
+        )
+        _native.check(rc, "tm_grad_norm")
+
+
+def grad_norm_launch(
+    grads: list[torch.Tensor],
+    max_norm: float | None,
+    chunk_elems: int = tables.DEFAULT_CHUNK_ELEMS,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Launch the two-pass norm over ``grads``; returns (norm, coef-or-None) device scalars."""
+    launch = NormLaunch(grads, max_norm, chunk_elems)
+    launch()
+    return launch.norm, launch.coef
+
+
+def scale_grads_(
+    grads: list[torch.Tensor], coef: torch.Tensor, chunk_elems: int = tables.DEFAULT_CHUNK_ELEMS
+) -> None:
+    """In-place grads *= coef (the reference's torch._foreach_mul_, grad_helper.py:33)."""
+    if not grads:
+        return
+    who = "clip_grad_norm"
+    device = grads[0].device
+    rows = tables.grad_table(grads, who)
+    chunks, n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]), chunk_elems, device)
+    d_rows = tables.upload(rows, device)
+    rc = _native.lib().tm_grad_scale(
+        d_rows.data_ptr(),
+        len(grads),
+        chunks.data_ptr(),
+        n_chunks,
+        chunk_elems,
+        coef.data_ptr(),
+        _native.stream_handle(device),
+    )
+    _native.check(rc, "tm_grad_scale")
+
+
+def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
+    """Returns the pre-clip global grad norm; clips grads (in place or deferred).
+
+    Signature and semantics of torchure/core/grad_helper.py:8-34. ``mesh`` is
+    unused on the local path, as in the reference. ``shard_dims`` (the sharded
+    sum-of-squares all-reduce, grad_helper.py:20-24) needs collectives, which
+    this single-GPU build does not provide.
+    """
+    if shard_dims:
+        raise NotImplementedError(
+            "clip_grad_norm: shard_dims needs a cross-GPU all_reduce of the squared norm; "
+            "this single-GPU build supports only the local path (shard_dims=())"
+        )
+    grads, holders = grads_of(params)
+    if not grads:
+        assert grads, "clip_grad_norm got no grads; backward didn't run, or all params are frozen"
+
+    # A clip pending from an earlier call must land before these grads are measured.
+    from torchure_amd.optimizer.adamw import owner_of, materialize_pending_for
+
+    materialize_pending_for(holders)
+
+    norm, coef = grad_norm_launch(grads, max_norm)
+    if max_norm is None:
+        return norm
+
+    owners = {id(owner_of(p)) for p in holders}
+    opt = owner_of(holders[0])
+    if len(owners) == 1 and opt is not None and opt.defer_clip:
+        opt._set_pending_clip(coef, holders)
+    else:
+        scale_grads_(grads, coef)
+    return norm

@@ -1,0 +1,318 @@
+"""AdamW for MI355X: torch.optim.AdamW's API and state layout, one fused gfx950 launch.
+
+Drop-in for the optimizer torchure builds at torchure/optimizer/builder.py:46
+(``torch.optim.AdamW(param_groups, lr=..., betas=..., fused=True)``):
+
+- constructor: same positional/keyword parameters as torch.optim.AdamW
+  (torch/optim/adamw.py:20-49, validation of torch/optim/adam.py:35-113);
+  amsgrad, maximize, capturable, differentiable, tensor lr/betas and
+  fused=False raise NotImplementedError (RuntimeError for fused+foreach, as torch);
+- ``param_groups`` carry exactly torch AdamW's keys (adam.py:91-103, with
+  decoupled_weight_decay=True), so schedulers that read/write ``lr`` and
+  ``initial_lr`` work unchanged (torch/optim/lr_scheduler.py:135-145,284-297);
+- per-param state is ``{'step': fp32 0-d tensor on the param's device,
+  'exp_avg', 'exp_avg_sq'}`` created lazily on the first step that sees a grad
+  (adam.py:139-212), so ``state_dict()``/``load_state_dict()`` round-trip with
+  torch.optim.AdamW checkpoints in both directions
+  (torch/optim/optimizer.py:677-767,877-1014; torchure/checkpoint/checkpointer.py:43-60);
+- params whose grad is None are skipped and their step does not advance
+  (adam.py:150-153); all-zero grads still update.
+
+One ``step()`` is one native call (``tm_adamw_step``) per device covering
+every group and tensor: a tiny prep kernel (step += 1, fp64 bias corrections)
+and one update kernel that reads grad/master/m/v once and writes
+master/m/v and, when a bf16 working copy is attached, RNE(master) once.
+
+Mixed precision: masters are the fp32 ``nn.Parameter``s, as in the reference
+(torchure/train/trainer.py:246-262). A master may carry a bf16 working copy
+(``torchure_amd.optimizer.working``); when its own ``.grad`` is None the bf16
+grad of the working copy is consumed, and the working copy is refreshed with
+RNE(master) after the update.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+from torch.utils.weak import WeakIdKeyDictionary
+
+from torchure_amd import _native
+from torchure_amd.core import tables
+
+# param -> owning AdamW (weak on both sides' lifetimes via the param key).
+_OWNERS: WeakIdKeyDictionary = WeakIdKeyDictionary()
+
+
+def owner_of(p: torch.Tensor):
+    return _OWNERS.get(p)
+
+
+def materialize_pending_for(params) -> None:
+    """Apply any deferred clip pending on the optimizers that own ``params``."""
+    seen = set()
+    for p in params:
+        opt = _OWNERS.get(p)
+        if opt is not None and id(opt) not in seen:
+            seen.add(id(opt))
+            if opt._pending is not None:
+                opt.materialize_clip()
+
+
+class AdamW(torch.optim.Optimizer):
+    def __init__(
+        self,
+        params,
+        lr: float = 1e-3,
+        betas: tuple[float, float] = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 1e-2,
+        amsgrad: bool = False,
+        *,
+        maximize: bool = False,
+        foreach: bool | None = None,
+        capturable: bool = False,
+        differentiable: bool = False,
+        fused: bool | None = None,
+        chunk_elems: int = tables.DEFAULT_CHUNK_ELEMS,
+        defer_clip: bool = True,
+    ) -> None:
+        if isinstance(lr, torch.Tensor) or any(isinstance(b, torch.Tensor) for b in betas):
+            raise NotImplementedError("torchure_amd.AdamW: tensor lr/betas are not supported")
+        if not 0.0 <= lr:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        if not 0.0 <= eps:
+            raise ValueError(f"Invalid epsilon value: {eps}")
+        if not 0.0 <= betas[0] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 0: {betas[0]}")
+        if not 0.0 <= betas[1] < 1.0:
+            raise ValueError(f"Invalid beta parameter at index 1: {betas[1]}")
+        if not 0.0 <= weight_decay:
+            raise ValueError(f"Invalid weight_decay value: {weight_decay}")
+        if amsgrad:
+            raise NotImplementedError("torchure_amd.AdamW: amsgrad is not supported")
+        if maximize:
+            raise NotImplementedError("torchure_amd.AdamW: maximize is not supported")
+        if capturable:
+            raise NotImplementedError("torchure_amd.AdamW: capturable is not supported")
+        if differentiable:
+            raise NotImplementedError("torchure_amd.AdamW: differentiable is not supported")
+        if fused is False:
+            raise NotImplementedError("torchure_amd.AdamW is always fused; fused=False is not supported")
+        if foreach:
+            raise RuntimeError("`fused` and `foreach` cannot be `True` together.")
+        defaults = {
+            "lr": lr,
+            "betas": (float(betas[0]), float(betas[1])),
+            "eps": eps,
+            "weight_decay": weight_decay,
+            "amsgrad": False,
+            "maximize": False,
+            "foreach": foreach,
+            "capturable": False,
+            "differentiable": False,
+            "fused": True,
+            "decoupled_weight_decay": True,
+        }
+        self.chunk_elems = tables.check_chunk_elems(chunk_elems)
+        self.defer_clip = bool(defer_clip)
+        self._pending = None  # (coef device tensor, set of ids of params it applies to)
+        super().__init__(params, defaults)
+        if len(self.param_groups) > _native.TM_MAX_GROUPS:
+            raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
+
+    def add_param_group(self, param_group: dict) -> None:
+        super().add_param_group(param_group)
+        if len(self.param_groups) > _native.TM_MAX_GROUPS:
+            raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
+        for p in self.param_groups[-1]["params"]:
+            _OWNERS[p] = self
+
+    def __setstate__(self, state):
+        super().__setstate__(state)
+        for group in self.param_groups:
+            group["decoupled_weight_decay"] = True
+        self.__dict__.setdefault("chunk_elems", tables.DEFAULT_CHUNK_ELEMS)
+        self.__dict__.setdefault("defer_clip", True)
+        self.__dict__.setdefault("_pending", None)
+
+    # ------------------------------------------------------------ deferred clip
+
+    def _set_pending_clip(self, coef: torch.Tensor, params) -> None:
+        self._pending = (coef, {id(p) for p in params})
+
+    def materialize_clip(self) -> None:
+        """Apply a pending clip coefficient to the grads in place and drop it."""
+        if self._pending is None:
+            return
+        coef, ids = self._pending
+        self._pending = None
+        from torchure_amd.core.grad_helper import grads_of, scale_grads_
+
+        held = [p for g in self.param_groups for p in g["params"] if id(p) in ids]
+        grads, _ = grads_of(held)
+        scale_grads_(grads, coef)
+
+    # ------------------------------------------------------------ step
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+
+        pending = self._pending
+        self._pending = None
+        coef, clip_ids = pending if pending is not None else (None, ())
+        for launch in self.plan_step(coef, clip_ids):
+            launch()
+        return loss
+
+    @torch.no_grad()
+    def plan_step(self, coef: torch.Tensor | None = None, clip_ids=()) -> list["StepLaunch"]:
+        """Collect the params with grads (creating their state lazily) and return
+        the native launches of one step without running them. ``step()`` runs
+        them once; calling a launch again applies one more step to the same
+        tensors and grads (bench.py uses this to time the kernels back to back)."""
+        per_dev: dict = {}
+        hyper = []
+        for gi, group in enumerate(self.param_groups):
+            lr = group["lr"]
+            if isinstance(lr, torch.Tensor):
+                raise NotImplementedError("torchure_amd.AdamW: tensor lr is not supported")
+            beta1, beta2 = group["betas"]
+            for key in ("amsgrad", "maximize", "capturable", "differentiable"):
+                if group.get(key):
+                    raise NotImplementedError(f"torchure_amd.AdamW: {key}=True is not supported")
+            hyper.append((float(lr), float(beta1), float(beta2), float(group["weight_decay"]), float(group["eps"])))
+            for p in group["params"]:
+                g = p.grad
+                work = getattr(p, "_tm_working", None)
+                if g is None and work is not None:
+                    g = work.grad
+                if g is None:
+                    continue
+                self._check_param(p, g, work)
+                state = self.state[p]
+                if len(state) == 0:
+                    state["step"] = torch.zeros((), dtype=torch.float32, device=p.device)
+                    state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                    state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                else:
+                    st = state["step"]
+                    if st.device != p.device or st.dtype != torch.float32:
+                        state["step"] = st.to(dtype=torch.float32, device=p.device)
+                    for k in ("exp_avg", "exp_avg_sq"):
+                        t = state[k]
+                        if t.device != p.device or t.dtype != torch.float32 or not t.is_contiguous():
+                            state[k] = t.to(dtype=torch.float32, device=p.device).contiguous()
+                flags = tables.grad_flags(g, "torchure_amd.AdamW")
+                if id(p) in clip_ids:
+                    flags |= _native.TM_FLAG_CLIP
+                cols = per_dev.setdefault(p.device, ([], [], [], [], [], [], [], [], []))
+                cols[0].append(p.data_ptr())
+                cols[1].append(state["exp_avg"].data_ptr())
+                cols[2].append(state["exp_avg_sq"].data_ptr())
+                cols[3].append(g.data_ptr())
+                cols[4].append(work.data_ptr() if work is not None else 0)
+                cols[5].append(state["step"].data_ptr())
+                cols[6].append(p.numel())
+                cols[7].append(gi)
+                cols[8].append(flags)
+
+        if not per_dev:
+            return []
+        return self._plan_launches(per_dev, hyper, coef)
+
+    def _plan_launches(self, per_dev, hyper, coef) -> list["StepLaunch"]:
+        groups_c = _native.hyper_array(hyper)
+        out = []
+        for device, cols in per_dev.items():
+            n = len(cols[0])
+            rows = np.zeros(n, dtype=_native.TENSOR_DTYPE)
+            for name, col, dt in zip(
+                _native.TENSOR_DTYPE.names,
+                cols,
+                (np.uint64,) * 6 + (np.int64, np.int32, np.uint32),
+            ):
+                rows[name] = np.asarray(col, dtype=dt)
+            if coef is not None and coef.device != device:
+                raise RuntimeError("torchure_amd.AdamW: clip coefficient on another device")
+            chunks, n_chunks = tables.CHUNKS.get(tuple(cols[6]), self.chunk_elems, device)
+            out.append(StepLaunch(device, tables.upload(rows, device), n, chunks, n_chunks,
+                                  self.chunk_elems, groups_c, len(hyper), coef))
+        return out
+
+    @staticmethod
+    def _check_param(p: torch.Tensor, g: torch.Tensor, work) -> None:
+        who = "torchure_amd.AdamW"
+        tables.require_device_tensor(p, who, "param")
+        if p.dtype != torch.float32:
+            raise RuntimeError(f"{who}: params (fp32 masters) must be float32, got {p.dtype}")
+        if g.is_sparse:
+            raise RuntimeError("Adam does not support sparse gradients, please consider SparseAdam instead")
+        tables.require_device_tensor(g, who, "grad")
+        if g.device != p.device or g.numel() != p.numel():
+            raise RuntimeError(f"{who}: grad of shape {tuple(g.shape)} on {g.device} does not match "
+                               f"param {tuple(p.shape)} on {p.device}")
+        if work is not None:
+            tables.require_device_tensor(work, who, "bf16 working copy")
+            if work.dtype != torch.bfloat16 or work.numel() != p.numel() or work.device != p.device:
+                raise RuntimeError(f"{who}: working copy must be bf16 of the param's size and device")
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        self._pending = None
+        super().zero_grad(set_to_none=set_to_none)
+        for group in self.param_groups:
+            for p in group["params"]:
+                w = getattr(p, "_tm_working", None)
+                if w is not None and w.grad is not None:
+                    if set_to_none:
+                        w.grad = None
+                    else:
+                        w.grad.zero_()
+
+
+class StepLaunch:
+    """One ``tm_adamw_step`` call with its device tables kept alive.
+
+    Calling it enqueues the prep + update kernels on the device's current
+    stream. Calling it again re-applies one more AdamW step to the same
+    tensors with the same grads (used to time the kernels back to back).
+    """
+
+    def __init__(self, device, d_rows, n, chunks, n_chunks, chunk_elems, groups_c, n_groups, coef):
+        self.device = device
+        self.d_rows = d_rows
+        self.n = n
+        self.chunks = chunks
+        self.n_chunks = n_chunks
+        self.chunk_elems = chunk_elems
+        self.groups_c = groups_c
+        self.n_groups = n_groups
+        self.coef = coef
+        self.ws = torch.empty(_native.workspace_bytes(n), dtype=torch.uint8, device=device)
+
+    def __call__(self) -> None:
+        rc = _native.lib().tm_adamw_step(
+            self.d_rows.data_ptr(),
+            self.n,
+            self.chunks.data_ptr(),
+            self.n_chunks,
+            self.chunk_elems,
+            self.groups_c,
+            self.n_groups,
+            self.coef.data_ptr() if self.coef is not None else None,
+            self.ws.data_ptr(),
+            _native.stream_handle(self.device),
+        )
+        _native.check(rc, "tm_adamw_step")
+
+
+def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out: bool = True) -> int:
+    """Algorithmic HBM bytes per parameter of one step (norm pass + update)."""
+    upd = grad_bytes + 3 * 4 + 3 * 4 + (2 if with_bf16_out else 0)
+    return upd + (grad_bytes if with_norm else 0)
+
+
+__all__ = ["AdamW", "owner_of", "materialize_pending_for", "step_bytes_per_param"]
