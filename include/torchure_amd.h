@@ -132,7 +132,8 @@ int tm_grad_norm(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk
 /*
  * In-place grad *= *d_coef for every tensor (the eager clip).
  * Replaces torch._foreach_mul_(grads, clip_coef) (grad_helper.py:33): fp32 grads
- * get one fp32 multiply, bf16 grads are widened, multiplied and rounded back RNE.
+ * get one fp32 multiply; bf16 grads are widened and multiplied by the coefficient
+ * rounded to bf16 (torch holds the scalar in the list's dtype), then rounded back RNE.
  */
 int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
                   int64_t n_chunks, int64_t chunk_elems, const float* d_coef, void* stream);

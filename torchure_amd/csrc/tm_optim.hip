@@ -18,9 +18,10 @@
 // (torch/include/ATen/native/hip/fused_adam_utils.cuh:22-92,106-199): hyper-parameters
 // are double; the decay and both moment updates are evaluated in double and rounded
 // to float; bias corrections are double, narrowed to float; the final division chain
-// is float. Every rounding point is written with an explicit *_rn intrinsic so the
-// compiler cannot contract or reorder it, which lets the C oracle reproduce the
-// result bit for bit.
+// is float. Floating-point contraction is switched off for the whole file and every
+// fused multiply-add is an explicit fma()/fmaf() call, so each rounding point is the
+// one written here and the C oracle reproduces the result bit for bit. Division and
+// sqrtf are the correctly rounded HIP defaults (never the native approximations).
 
 #include <hip/hip_runtime.h>
 
@@ -31,6 +32,8 @@
 #include <string.h>
 
 #include "torchure_amd.h"
+
+#pragma clang fp contract(off)
 
 namespace {
 
@@ -115,15 +118,14 @@ __device__ __forceinline__ void adamw_elem(float& p, float& m, float& v, float g
                                            const TensorScal& c) {
   if (c.decay) {
     const double pd = static_cast<double>(p);
-    p = static_cast<float>(__fma_rn(c.neg_lrwd, pd, pd));
+    p = static_cast<float>(fma(c.neg_lrwd, pd, pd));
   }
   const double gd = static_cast<double>(g);
-  m = static_cast<float>(__fma_rn(c.beta1, static_cast<double>(m), __dmul_rn(c.omb1, gd)));
-  v = static_cast<float>(
-      __fma_rn(c.beta2, static_cast<double>(v), __dmul_rn(__dmul_rn(c.omb2, gd), gd)));
-  const float q = __fdiv_rn(__fsqrt_rn(v), c.bc2s);
-  const float denom = static_cast<float>(__dadd_rn(static_cast<double>(q), c.eps));
-  p = __fsub_rn(p, __fdiv_rn(__fmul_rn(c.step_size, m), denom));
+  m = static_cast<float>(fma(c.beta1, static_cast<double>(m), c.omb1 * gd));
+  v = static_cast<float>(fma(c.beta2, static_cast<double>(v), (c.omb2 * gd) * gd));
+  const float q = sqrtf(v) / c.bc2s;
+  const float denom = static_cast<float>(static_cast<double>(q) + c.eps);
+  p = p - (c.step_size * m) / denom;
 }
 
 __device__ __forceinline__ bool aligned16(uint64_t a) { return (a & 15u) == 0; }
@@ -174,21 +176,21 @@ __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
           const f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(g + i));
           const f32x4 b = ld<true>(reinterpret_cast<const f32x4*>(g + i + 4));
           double s = 0.0;
-          s = __fma_rn((double)a.x, (double)a.x, s);
-          s = __fma_rn((double)a.y, (double)a.y, s);
-          s = __fma_rn((double)a.z, (double)a.z, s);
-          s = __fma_rn((double)a.w, (double)a.w, s);
-          s = __fma_rn((double)b.x, (double)b.x, s);
-          s = __fma_rn((double)b.y, (double)b.y, s);
-          s = __fma_rn((double)b.z, (double)b.z, s);
-          s = __fma_rn((double)b.w, (double)b.w, s);
+          s = fma((double)a.x, (double)a.x, s);
+          s = fma((double)a.y, (double)a.y, s);
+          s = fma((double)a.z, (double)a.z, s);
+          s = fma((double)a.w, (double)a.w, s);
+          s = fma((double)b.x, (double)b.x, s);
+          s = fma((double)b.y, (double)b.y, s);
+          s = fma((double)b.z, (double)b.z, s);
+          s = fma((double)b.w, (double)b.w, s);
           acc += s;
         }
         for (int64_t i = vend + threadIdx.x; i < end; i += kThreads)
-          acc = __fma_rn((double)g[i], (double)g[i], acc);
+          acc = fma((double)g[i], (double)g[i], acc);
       } else {
         for (int64_t i = start + threadIdx.x; i < end; i += kThreads)
-          acc = __fma_rn((double)g[i], (double)g[i], acc);
+          acc = fma((double)g[i], (double)g[i], acc);
       }
     } else {
       const uint16_t* __restrict__ g = reinterpret_cast<const uint16_t*>(d.grad);
@@ -200,24 +202,24 @@ __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
           // in fp32 and the group sum is accumulated in fp64.
           float s = 0.f;
           float x;
-          x = bf16_lo(w.x); s = __fmaf_rn(x, x, s);
-          x = bf16_hi(w.x); s = __fmaf_rn(x, x, s);
-          x = bf16_lo(w.y); s = __fmaf_rn(x, x, s);
-          x = bf16_hi(w.y); s = __fmaf_rn(x, x, s);
-          x = bf16_lo(w.z); s = __fmaf_rn(x, x, s);
-          x = bf16_hi(w.z); s = __fmaf_rn(x, x, s);
-          x = bf16_lo(w.w); s = __fmaf_rn(x, x, s);
-          x = bf16_hi(w.w); s = __fmaf_rn(x, x, s);
+          x = bf16_lo(w.x); s = fmaf(x, x, s);
+          x = bf16_hi(w.x); s = fmaf(x, x, s);
+          x = bf16_lo(w.y); s = fmaf(x, x, s);
+          x = bf16_hi(w.y); s = fmaf(x, x, s);
+          x = bf16_lo(w.z); s = fmaf(x, x, s);
+          x = bf16_hi(w.z); s = fmaf(x, x, s);
+          x = bf16_lo(w.w); s = fmaf(x, x, s);
+          x = bf16_hi(w.w); s = fmaf(x, x, s);
           acc += static_cast<double>(s);
         }
         for (int64_t i = vend + threadIdx.x; i < end; i += kThreads) {
           const double x = bf16_at(g, i);
-          acc = __fma_rn(x, x, acc);
+          acc = fma(x, x, acc);
         }
       } else {
         for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
           const double x = bf16_at(g, i);
-          acc = __fma_rn(x, x, acc);
+          acc = fma(x, x, acc);
         }
       }
     }
@@ -242,8 +244,8 @@ __global__ __launch_bounds__(kThreads) void norm_finalize_kernel(
     const float norm = static_cast<float>(sqrt(total));
     *norm_out = norm;
     if (clip) {
-      const float r = __fdiv_rn(1.0f, __fadd_rn(norm, 1e-6f));
-      const float c = __fmul_rn(r, max_norm);
+      const float r = 1.0f / (norm + 1e-6f);
+      const float c = r * max_norm;
       *coef_out = (c > 1.0f) ? 1.0f : c;
     }
   }
@@ -263,11 +265,15 @@ __global__ __launch_bounds__(kThreads) void grad_scale_kernel(
   const float coef = *coef_p;
   if (d.flags & TM_GRAD_F32) {
     float* __restrict__ g = reinterpret_cast<float*>(d.grad);
-    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) g[i] = __fmul_rn(g[i], coef);
+    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) g[i] = g[i] * coef;
   } else {
+    // torch._foreach_mul_ on a bf16 list holds the 0-d scalar in the list's dtype
+    // (BinaryOpScalarTensorFunctor, torch/include/ATen/native/hip/ForeachFunctors.cuh:
+    // 309-342): the coefficient is rounded to bf16 before the fp32 multiply.
+    const float coef_b = __uint_as_float(bf16_rne(coef) << 16);
     uint16_t* __restrict__ g = reinterpret_cast<uint16_t*>(d.grad);
     for (int64_t i = start + threadIdx.x; i < end; i += kThreads)
-      g[i] = static_cast<uint16_t>(bf16_rne(__fmul_rn(bf16_at(g, i), coef)));
+      g[i] = static_cast<uint16_t>(bf16_rne(bf16_at(g, i) * coef_b));
   }
 }
 
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
   if (gi < 0 || gi >= hyper.n) gi = 0;
   const tm_hyper_t h = hyper.g[gi];
   float* step_p = reinterpret_cast<float*>(d.step);
-  const float step = __fadd_rn(*step_p, 1.0f);
+  const float step = *step_p + 1.0f;
   *step_p = step;
   const double bc1 = 1.0 - pow(h.beta1, static_cast<double>(step));
   const double bc2 = 1.0 - pow(h.beta2, static_cast<double>(step));
@@ -343,7 +349,7 @@ __device__ __forceinline__ void update_vector(const tm_tensor_t& d, int64_t star
     float v[kVec] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
     for (int j = 0; j < kVec; ++j) {
-      const float gj = clip ? __fmul_rn(g[j], coef) : g[j];
+      const float gj = clip ? g[j] * coef : g[j];
       adamw_elem(p[j], m[j], v[j], gj, c);
     }
     st<kNT>(reinterpret_cast<f32x4*>(P + i), f32x4{p[0], p[1], p[2], p[3]});
@@ -375,7 +381,7 @@ __device__ __forceinline__ void update_scalar(const tm_tensor_t& d, int64_t star
   for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
     float g = f32 ? reinterpret_cast<const float*>(d.grad)[i]
                   : bf16_at(reinterpret_cast<const uint16_t*>(d.grad), i);
-    if (clip) g = __fmul_rn(g, coef);
+    if (clip) g = g * coef;
     float p = P[i], m = M[i], v = V[i];
     adamw_elem(p, m, v, g, c);
     P[i] = p;
@@ -430,16 +436,16 @@ __global__ __launch_bounds__(kThreads) void accumulate_kernel(float* __restrict_
     const u32x4 w = ld<true>(reinterpret_cast<const u32x4*>(micro + i));
     f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(acc + i));
     f32x4 b = ld<true>(reinterpret_cast<const f32x4*>(acc + i + 4));
-    a.x = __fadd_rn(a.x, bf16_lo(w.x)); a.y = __fadd_rn(a.y, bf16_hi(w.x));
-    a.z = __fadd_rn(a.z, bf16_lo(w.y)); a.w = __fadd_rn(a.w, bf16_hi(w.y));
-    b.x = __fadd_rn(b.x, bf16_lo(w.z)); b.y = __fadd_rn(b.y, bf16_hi(w.z));
-    b.z = __fadd_rn(b.z, bf16_lo(w.w)); b.w = __fadd_rn(b.w, bf16_hi(w.w));
+    a.x = a.x + bf16_lo(w.x); a.y = a.y + bf16_hi(w.x);
+    a.z = a.z + bf16_lo(w.y); a.w = a.w + bf16_hi(w.y);
+    b.x = b.x + bf16_lo(w.z); b.y = b.y + bf16_hi(w.z);
+    b.z = b.z + bf16_lo(w.w); b.w = b.w + bf16_hi(w.w);
     st<true>(reinterpret_cast<f32x4*>(acc + i), a);
     st<true>(reinterpret_cast<f32x4*>(acc + i + 4), b);
   }
   for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * kThreads)
-    acc[i] = __fadd_rn(acc[i], bf16_at(micro, i));
+    acc[i] = acc[i] + bf16_at(micro, i);
 }
 
 __global__ __launch_bounds__(kThreads) void cast_bf16_kernel(uint16_t* __restrict__ dst,
