@@ -47,7 +47,38 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--also", default="qwen3-0.6b",
                     help="comma list of extra configs reported under 'extra' (empty = none)")
+    ap.add_argument("--mode", choices=("bench", "kernels"), default="bench",
+                    help="kernels: only the norm and update launches, --reps times each, plus a "
+                         "2 GiB device copy for calibrating HBM byte counters (for rocprofv3 --pmc)")
+    ap.add_argument("--reps", type=int, default=3)
     return ap.parse_args()
+
+
+def run_kernels_only(config: str, reps: int, chunk_elems, dev):
+    """Launch sequence profiled by rocprofv3 --pmc: `reps` x (norm, update), then a
+    plain copy of 2 GiB (512 Mi fp32) whose FETCH_SIZE/WRITE_SIZE calibrate the counters."""
+    import torch
+
+    from torchure_amd.core.grad_helper import NormLaunch
+
+    params, work, opt, n_params = build_state(config, chunk_elems, dev)
+    norm_l = NormLaunch([w.grad for w in work], 1.0)
+    norm_l()
+    upd = opt.plan_step(norm_l.coef, {id(p) for p in params})
+    for _ in range(reps):
+        norm_l()
+        upd[0]()
+    torch.cuda.synchronize()
+    del params, work, opt, upd
+    torch.cuda.empty_cache()
+    a = torch.ones(512 * 1024 * 1024, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"mode": "kernels", "config": config, "params": n_params, "reps": reps,
+                      "update_algorithmic_bytes": n_params * UPDATE_BYTES_PER_PARAM,
+                      "norm_algorithmic_bytes": n_params * NORM_BYTES_PER_PARAM,
+                      "copy_bytes_each_way": a.numel() * 4}), flush=True)
 
 
 def build_state(config: str, chunk_elems, dev):
@@ -127,6 +158,20 @@ def run_gpu(config: str, steps: int, warmup: int, chunk_elems, dev):
     torch.cuda.synchronize()
     norm_ms = [a.elapsed_time(b) / reps]
     upd_ms = [b.elapsed_time(c) / reps]
+    del upd, norm_l
+    # Ceiling reference for a 1:1 read/write stream on this device: torch's own
+    # device-to-device copy of 2 GiB (reads 2 GiB, writes 2 GiB), same event timing.
+    src = torch.ones(512 * 1024 * 1024, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(5):
+        dst.copy_(src)
+    b.record(stream)
+    torch.cuda.synchronize()
+    copy_gbps = 2 * src.numel() * 4 / (a.elapsed_time(b) / 5 * 1e-3) / 1e9
+    del src, dst
     out = dict(
         config=config,
         n_params=n_params,
@@ -136,6 +181,7 @@ def run_gpu(config: str, steps: int, warmup: int, chunk_elems, dev):
         norm_ms_mean=statistics.fmean(norm_ms),
         update_ms_mean=statistics.fmean(upd_ms),
         kernel_reps=reps,
+        copy_GBps=round(copy_gbps, 1),
     )
     del params, work, opt
     torch.cuda.empty_cache()
@@ -207,6 +253,9 @@ def main():
     import torchure_amd
 
     torchure_amd._native.lib()
+    if args.mode == "kernels":
+        run_kernels_only(args.config, args.reps, args.chunk_elems, dev)
+        return
 
     main_res = run_gpu(args.config, args.steps, args.warmup, args.chunk_elems, dev)
     print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
@@ -253,6 +302,8 @@ def main():
             "traffic": load_traffic(args.config),
             "launch_ms_mean": round(main_res["update_ms_mean"], 4),
             "norm_ms_mean": round(main_res["norm_ms_mean"], 4),
+            "device_copy_GBps": main_res["copy_GBps"],
+            "frac_of_device_copy": round(upd_gbs / main_res["copy_GBps"], 4),
         },
         "cpu_baseline": cpu,
         "extra": extra,

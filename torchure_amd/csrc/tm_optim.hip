@@ -129,6 +129,7 @@ __device__ __forceinline__ void adamw_elem(float& p, float& m, float& v, float g
 }
 
 __device__ __forceinline__ bool aligned16(uint64_t a) { return (a & 15u) == 0; }
+__device__ __forceinline__ bool aligned8(uint64_t a) { return (a & 7u) == 0; }
 
 // ------------------------------------------------------------------- reductions
 
@@ -316,61 +317,102 @@ __global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
 
 // ------------------------------------------------------------------- AdamW update
 
-template <bool kGradF32, bool kOut, bool kNT>
-__device__ __forceinline__ void update_vector(const tm_tensor_t& d, int64_t start, int64_t vend,
-                                              const TensorScal& c, bool clip, float coef) {
-  float* __restrict__ P = reinterpret_cast<float*>(d.master);
-  float* __restrict__ M = reinterpret_cast<float*>(d.exp_avg);
-  float* __restrict__ V = reinterpret_cast<float*>(d.exp_avg_sq);
-  uint16_t* __restrict__ O = reinterpret_cast<uint16_t*>(d.param_bf16);
-#pragma unroll 2
-  for (int64_t i = start + threadIdx.x * kVec; i < vend; i += kThreads * kVec) {
-    float g[kVec];
-    if constexpr (kGradF32) {
-      const float* G = reinterpret_cast<const float*>(d.grad);
-      const f32x4 a = ld<kNT>(reinterpret_cast<const f32x4*>(G + i));
-      const f32x4 b = ld<kNT>(reinterpret_cast<const f32x4*>(G + i + 4));
-      g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w;
-      g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
-    } else {
-      const uint16_t* G = reinterpret_cast<const uint16_t*>(d.grad);
-      const u32x4 w = ld<kNT>(reinterpret_cast<const u32x4*>(G + i));
-      g[0] = bf16_lo(w.x); g[1] = bf16_hi(w.x); g[2] = bf16_lo(w.y); g[3] = bf16_hi(w.y);
-      g[4] = bf16_lo(w.z); g[5] = bf16_hi(w.z); g[6] = bf16_lo(w.w); g[7] = bf16_hi(w.w);
-    }
-    const f32x4 p0 = ld<kNT>(reinterpret_cast<const f32x4*>(P + i));
-    const f32x4 p1 = ld<kNT>(reinterpret_cast<const f32x4*>(P + i + 4));
-    const f32x4 m0 = ld<kNT>(reinterpret_cast<const f32x4*>(M + i));
-    const f32x4 m1 = ld<kNT>(reinterpret_cast<const f32x4*>(M + i + 4));
-    const f32x4 v0 = ld<kNT>(reinterpret_cast<const f32x4*>(V + i));
-    const f32x4 v1 = ld<kNT>(reinterpret_cast<const f32x4*>(V + i + 4));
-    float p[kVec] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-    float m[kVec] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
-    float v[kVec] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+// Vector path. A thread works on groups of 4 consecutive elements; in a block
+// iteration starting at `base`, group k of thread t covers
+//   [base + k * kThreads * 4 + t * 4, +4).
+// Every load/store instruction of a wave therefore touches one contiguous span
+// (1 KiB of an fp32 array, 512 B of a bf16 array): whole cache lines, so the
+// stores never leave partially written lines behind. kUpdateGroups groups are
+// loaded before any is computed, to keep that many 16-byte loads per array in
+// flight per thread.
+#ifndef TM_UPDATE_GROUPS
+#define TM_UPDATE_GROUPS 2
+#endif
+#ifndef TM_UPDATE_NT
+#define TM_UPDATE_NT 1
+#endif
+constexpr int kUpdateGroups = TM_UPDATE_GROUPS;
+constexpr bool kUpdateNT = TM_UPDATE_NT != 0;  // non-temporal (streaming) loads and stores
+constexpr int kGroupSpan = kThreads * 4;                 // elements per group slot
+constexpr int kUpdateIter = kGroupSpan * kUpdateGroups;  // elements per block iteration
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct Group4 {
+  f32x4 p, m, v;
+  float g[4];
+};
+
+template <bool kGradF32, bool kNT>
+__device__ __forceinline__ void load_group(Group4& r, const tm_tensor_t& d, int64_t e) {
+  if constexpr (kGradF32) {
+    const f32x4 a = ld<kNT>(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(d.grad) + e));
+    r.g[0] = a.x; r.g[1] = a.y; r.g[2] = a.z; r.g[3] = a.w;
+  } else {
+    const u32x2 w =
+        ld<kNT>(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(d.grad) + e));
+    r.g[0] = bf16_lo(w.x); r.g[1] = bf16_hi(w.x); r.g[2] = bf16_lo(w.y); r.g[3] = bf16_hi(w.y);
+  }
+  r.p = ld<kNT>(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(d.master) + e));
+  r.m = ld<kNT>(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(d.exp_avg) + e));
+  r.v = ld<kNT>(reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(d.exp_avg_sq) + e));
+}
+
+__device__ __forceinline__ void compute_group(Group4& r, const TensorScal& c, bool clip, float coef) {
+  float p[4] = {r.p.x, r.p.y, r.p.z, r.p.w};
+  float m[4] = {r.m.x, r.m.y, r.m.z, r.m.w};
+  float v[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
 #pragma unroll
-    for (int j = 0; j < kVec; ++j) {
-      const float gj = clip ? g[j] * coef : g[j];
-      adamw_elem(p[j], m[j], v[j], gj, c);
-    }
-    st<kNT>(reinterpret_cast<f32x4*>(P + i), f32x4{p[0], p[1], p[2], p[3]});
-    st<kNT>(reinterpret_cast<f32x4*>(P + i + 4), f32x4{p[4], p[5], p[6], p[7]});
-    st<kNT>(reinterpret_cast<f32x4*>(M + i), f32x4{m[0], m[1], m[2], m[3]});
-    st<kNT>(reinterpret_cast<f32x4*>(M + i + 4), f32x4{m[4], m[5], m[6], m[7]});
-    st<kNT>(reinterpret_cast<f32x4*>(V + i), f32x4{v[0], v[1], v[2], v[3]});
-    st<kNT>(reinterpret_cast<f32x4*>(V + i + 4), f32x4{v[4], v[5], v[6], v[7]});
-    if constexpr (kOut) {
-      u32x4 o;
-      o.x = bf16_rne(p[0]) | (bf16_rne(p[1]) << 16);
-      o.y = bf16_rne(p[2]) | (bf16_rne(p[3]) << 16);
-      o.z = bf16_rne(p[4]) | (bf16_rne(p[5]) << 16);
-      o.w = bf16_rne(p[6]) | (bf16_rne(p[7]) << 16);
-      st<kNT>(reinterpret_cast<u32x4*>(O + i), o);
-    }
+  for (int j = 0; j < 4; ++j) {
+    const float gj = clip ? r.g[j] * coef : r.g[j];
+    adamw_elem(p[j], m[j], v[j], gj, c);
+  }
+  r.p = f32x4{p[0], p[1], p[2], p[3]};
+  r.m = f32x4{m[0], m[1], m[2], m[3]};
+  r.v = f32x4{v[0], v[1], v[2], v[3]};
+}
+
+template <bool kOut, bool kNT>
+__device__ __forceinline__ void store_group(const Group4& r, const tm_tensor_t& d, int64_t e) {
+  st<kNT>(reinterpret_cast<f32x4*>(reinterpret_cast<float*>(d.master) + e), r.p);
+  st<kNT>(reinterpret_cast<f32x4*>(reinterpret_cast<float*>(d.exp_avg) + e), r.m);
+  st<kNT>(reinterpret_cast<f32x4*>(reinterpret_cast<float*>(d.exp_avg_sq) + e), r.v);
+  if constexpr (kOut) {
+    u32x2 o;
+    o.x = bf16_rne(r.p.x) | (bf16_rne(r.p.y) << 16);
+    o.y = bf16_rne(r.p.z) | (bf16_rne(r.p.w) << 16);
+    st<kNT>(reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(d.param_bf16) + e), o);
   }
 }
 
-// Element-at-a-time path: the tail of a tensor whose length is not a multiple of 8,
-// and whole tensors whose pointers are not 16-byte aligned.
+// Elements [start, vend) with (vend - start) % 4 == 0 and start % 4 == 0.
+template <bool kGradF32, bool kOut, bool kNT>
+__device__ __forceinline__ void update_vector(const tm_tensor_t& d, int64_t start, int64_t vend,
+                                              const TensorScal& c, bool clip, float coef) {
+  const int64_t lane4 = static_cast<int64_t>(threadIdx.x) * 4;
+  int64_t base = start;
+  for (; base + kUpdateIter <= vend; base += kUpdateIter) {
+    Group4 r[kUpdateGroups];
+#pragma unroll
+    for (int k = 0; k < kUpdateGroups; ++k)
+      load_group<kGradF32, kNT>(r[k], d, base + k * kGroupSpan + lane4);
+#pragma unroll
+    for (int k = 0; k < kUpdateGroups; ++k) compute_group(r[k], c, clip, coef);
+#pragma unroll
+    for (int k = 0; k < kUpdateGroups; ++k)
+      store_group<kOut, kNT>(r[k], d, base + k * kGroupSpan + lane4);
+  }
+  for (int64_t e = base + lane4; e < vend; e += kGroupSpan) {
+    Group4 r;
+    load_group<kGradF32, kNT>(r, d, e);
+    compute_group(r, c, clip, coef);
+    store_group<kOut, kNT>(r, d, e);
+  }
+}
+
+// Element-at-a-time path: the tail of a tensor whose length is not a multiple of 4,
+// and whole tensors whose fp32 pointers are not 16-byte aligned (or bf16 pointers
+// not 8-byte aligned).
 __device__ __forceinline__ void update_scalar(const tm_tensor_t& d, int64_t start, int64_t end,
                                               const TensorScal& c, bool clip, float coef) {
   float* P = reinterpret_cast<float*>(d.master);
@@ -406,11 +448,12 @@ __global__ __launch_bounds__(kThreads) void adamw_update_kernel(
   const bool clip = (d.flags & TM_FLAG_CLIP) != 0;
   const float coef = clip ? *coef_p : 1.0f;
   const bool out = d.param_bf16 != 0;
+  const bool grad_ok = (d.flags & TM_GRAD_F32) ? aligned16(d.grad) : aligned8(d.grad);
   const bool vec = aligned16(d.master) && aligned16(d.exp_avg) && aligned16(d.exp_avg_sq) &&
-                   aligned16(d.grad) && (!out || aligned16(d.param_bf16));
+                   grad_ok && (!out || aligned8(d.param_bf16));
   int64_t vend = start;
   if (vec) {
-    vend = start + ((end - start) & ~int64_t(kVec - 1));
+    vend = start + ((end - start) & ~int64_t(3));
     if (d.flags & TM_GRAD_F32) {
       if (out) update_vector<true, true, kNT>(d, start, vend, c, clip, coef);
       else update_vector<true, false, kNT>(d, start, vend, c, clip, coef);
@@ -575,7 +618,7 @@ int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
   // d_coef may be null only when no tensor asks for the clip; the kernel reads it
   // only for TM_FLAG_CLIP tensors, so point it at the workspace otherwise.
   const float* coef = d_coef ? d_coef : reinterpret_cast<const float*>(d_ws);
-  hipLaunchKernelGGL(adamw_update_kernel<true>, dim3(static_cast<uint32_t>(n_chunks)), dim3(kThreads),
+  hipLaunchKernelGGL(adamw_update_kernel<kUpdateNT>, dim3(static_cast<uint32_t>(n_chunks)), dim3(kThreads),
                      0, s, d_tensors, n_tensors, d_chunks, chunk_elems, scal, coef);
   return check_launch("adamw_update_kernel");
 }
