@@ -221,3 +221,22 @@ def test_param_group_split(name, dec, nod, dec_el, nod_el):
     assert (len(d), len(n)) == (dec, nod)
     assert sum(numel(shapes[i]) for i in d) == dec_el
     assert sum(numel(shapes[i]) for i in n) == nod_el
+
+
+def test_bf16_update_equals_widened_update():
+    """adamw_update_bf16 (bf16 grad bits, fused clip multiply and bf16 refresh) equals
+    adamw_update on the widened, coefficient-scaled fp32 grads."""
+    r = H.rng(8)
+    n = 3001
+    p = (r.standard_normal(n) * 0.02).astype(np.float32)
+    m = (r.standard_normal(n) * 1e-4).astype(np.float32)
+    v = (np.abs(r.standard_normal(n)) * 1e-8).astype(np.float32)
+    g = oracle.bf16_rne((r.standard_normal(n) * 1e-3).astype(np.float32))
+    coef = np.float32(0.37)
+    p2, m2, v2 = p.copy(), m.copy(), v.copy()
+    out = np.zeros(n, np.uint16)
+    oracle.adamw_update_bf16(p, m, v, g, out, coef, 1, 1001.0, 3e-4, 0.9, 0.95, 0.1, 1e-8)
+    gw = (oracle.bf16_to_f32(g) * coef).astype(np.float32)
+    oracle.adamw_update(p2, m2, v2, gw, 1001.0, 3e-4, 0.9, 0.95, 0.1, 1e-8)
+    assert np.array_equal(p, p2) and np.array_equal(m, m2) and np.array_equal(v, v2)
+    assert np.array_equal(out, oracle.bf16_rne(p))
