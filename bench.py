@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--cpu-sample-blocks", type=int, default=2,
                     help="transformer blocks of the config timed for the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-steps", type=int, default=3)
-    ap.add_argument("--also", default="qwen3-0.6b",
+    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-fp32acc",
                     help="comma list of extra configs reported under 'extra' (empty = none)")
     ap.add_argument("--mode", choices=("bench", "kernels"), default="bench",
                     help="kernels: only the norm and update launches, --reps times each, plus a "
@@ -188,6 +188,62 @@ def run_gpu(config: str, steps: int, warmup: int, chunk_elems, dev):
     return out
 
 
+def run_gpu_fp32acc(config: str, steps: int, warmup: int, chunk_elems, dev):
+    """Config-3 style step: bf16 micro-grads accumulated into fp32 .grad; the last
+    micro-step's accumulation also yields the global norm (fused), clip_grad_norm
+    reuses it, and the step reads fp32 grads. Per iteration: last micro-step
+    accumulate+norm (10 B/param), then clip (no grad read) + step (32 B/param)."""
+    import torch
+
+    import torchure_amd as ta
+    from torchure_amd.optimizer.working import accumulate_grads_
+
+    params, work, opt, n_params = build_state(config, chunk_elems, dev)
+    g = torch.Generator(device=dev).manual_seed(77)
+    micro = [w.grad for w in work]
+    for p in params:
+        p.grad = torch.randn(p.shape, device=dev, generator=g) * 3e-3
+    stream = torch.cuda.current_stream(dev)
+
+    def one(ev=None):
+        for w, m in zip(work, micro):
+            w.grad = m
+        if ev is not None:
+            ev[0].record(stream)
+        accumulate_grads_(params, last=True)
+        if ev is not None:
+            ev[1].record(stream)
+        ta.clip_grad_norm(params, None, 1.0)
+        opt.step()
+        if ev is not None:
+            ev[2].record(stream)
+
+    for _ in range(warmup):
+        one()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        one(evs[k])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    acc_ms = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+    step_ms = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+    out = dict(
+        config=config + "-fp32acc",
+        n_params=n_params,
+        ms_per_iteration=wall * 1e3 / steps,
+        last_microstep_accumulate_norm_ms=round(acc_ms, 4),
+        accumulate_GBps=round(10 * n_params / (acc_ms * 1e-3) / 1e9, 1),
+        step_ms=round(step_ms, 4),
+        step_bytes_per_param=32,
+        step_GBps=round(32 * n_params / (step_ms * 1e-3) / 1e9, 1),
+    )
+    del params, work, opt, micro
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_cpu_baseline(config: str, blocks: int, steps: int):
     """Reference composition on torch CPU over the first ``blocks`` transformer
     blocks of ``config`` (the sample), bf16 grads widened to fp32."""
@@ -261,6 +317,11 @@ def main():
     print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
     extra = {}
     for cfg in [c for c in args.also.split(",") if c and c != args.config]:
+        if cfg.endswith("-fp32acc"):
+            r = run_gpu_fp32acc(cfg[: -len("-fp32acc")], args.steps, args.warmup, args.chunk_elems, dev)
+            extra[cfg] = r
+            print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
+            continue
         r = run_gpu(cfg, args.steps, args.warmup, args.chunk_elems, dev)
         r["GBps"] = round(r["n_params"] * STEP_BYTES_PER_PARAM / (r["ms_per_step"] * 1e-3) / 1e9, 1)
         r["frac_of_peak"] = round(r["GBps"] / PEAK_HBM_GBS, 4)

@@ -87,6 +87,16 @@ typedef struct tm_chunk {
   uint32_t chunk;
 } tm_chunk_t;
 
+/* One tensor of a micro-step accumulation list (32 bytes, device memory):
+ * acc (fp32, updated in place) += micro (bf16), numel elements. micro may be 0:
+ * the accumulator is then left as is and only enters the norm. */
+typedef struct tm_accum {
+  uint64_t acc;
+  uint64_t micro;
+  int64_t numel;
+  int64_t reserved;
+} tm_accum_t;
+
 /* Hyper-parameters of one param group, as torch.optim.AdamW holds them
  * (python floats = double): torch/optim/adam.py:35-113, fused_adam_utils.cuh:110-121. */
 typedef struct tm_hyper {
@@ -158,6 +168,23 @@ int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
  * builds in p.grad across micro-batches (torchure/train/trainer.py:383-390).
  */
 int tm_grad_accumulate_bf16(float* d_acc, const uint16_t* d_micro, int64_t numel, void* stream);
+
+/*
+ * Micro-step accumulation over a list of tensors, one launch: acc += micro for every
+ * entry (the fp32 .grad accumulation of torchure/train/trainer.py:383-390).
+ * With with_norm != 0 (the last micro-step) the same pass also produces the global
+ * L2 norm of the accumulated grads into d_norm, bit-identical to tm_grad_norm on the
+ * resulting fp32 buffers with the same chunk table -- the separate norm read pass of
+ * torch._foreach_norm (torchure/core/grad_helper.py:17-18) disappears.
+ *   d_ws  at least tm_workspace_bytes(0) bytes when with_norm != 0
+ */
+int tm_grad_accumulate_list(const tm_accum_t* d_list, int64_t n_list, const tm_chunk_t* d_chunks,
+                            int64_t n_chunks, int64_t chunk_elems, int with_norm, void* d_ws,
+                            float* d_norm, void* stream);
+
+/* Clip coefficient from a norm already on the device:
+ * clamp(max_norm / (norm + 1e-6), max=1.0) as in tm_grad_norm (grad_helper.py:32). */
+int tm_clip_coef(const float* d_norm, float max_norm, float* d_coef, void* stream);
 
 /* Writes RNE(src) into dst (bf16 working-copy refresh without an update).
  * Rounding rule of torch/headeronly/util/BFloat16.h:100-114 (NaN -> 0x7FC0). */

@@ -402,3 +402,64 @@ def test_full_size_0p6b_properties():
         got = params[i].detach().cpu().numpy().reshape(-1)
         assert int(H.ulp_diff(got, t[0]["p"]).max()) == 0, i
         assert np.array_equal(opt.state[params[i]]["exp_avg"].cpu().numpy().reshape(-1), t[0]["m"])
+
+
+def test_accumulate_list_fused_norm_and_reuse():
+    """Row (f)1: 4 bf16 micro-steps accumulated into fp32 .grad in one launch each;
+    the last also yields the global norm, bit-identical to the standalone norm pass,
+    and clip_grad_norm reuses it; the step then matches the oracle bit for bit."""
+    import torchure_amd as ta
+    from torchure_amd.core.grad_helper import grad_norm_launch
+    from torchure_amd.optimizer.working import accumulate_grads_, cached_norm
+
+    shapes = shapes_for("tiny") + [(1001,), (3, 333)]  # odd lengths exercise the tail
+    host = H.make_host_set(shapes, seed=21)
+    params, work, opt = H.device_setup(host, DEV)
+    for w in work:
+        w.grad = None
+    r = H.rng(22)
+    acc_ref = [np.zeros(numel(s), np.float32) for s in shapes]
+    for k in range(4):
+        for i, (s, w) in enumerate(zip(shapes, work)):
+            if k == 3 and i == 5:
+                continue  # no micro-grad for this param in the last step: still in the norm
+            mg = oracle.bf16_rne((r.standard_normal(numel(s)) * 2e-3).astype(np.float32))
+            acc_ref[i] = (acc_ref[i] + oracle.bf16_to_f32(mg)).astype(np.float32)
+            w.grad = H.to_dev_bf16(mg, s, DEV)
+        norm = accumulate_grads_(params, last=(k == 3))
+    torch.cuda.synchronize()
+    for i, p in enumerate(params):
+        assert np.array_equal(p.grad.cpu().numpy().reshape(-1), acc_ref[i]), i
+        assert work[i].grad is None
+    ref_norm, _ = grad_norm_launch([p.grad for p in params], None)
+    assert norm.view(torch.int32).item() == ref_norm.view(torch.int32).item()
+    exact = np.sqrt(sum(oracle.sumsq(a) for a in acc_ref))
+    assert abs(norm.item() - exact) <= 1e-6 * exact
+    assert cached_norm([p.grad for p in params]) is norm
+    got = ta.clip_grad_norm(params, None, 1.0)
+    assert got is norm
+    coef = opt._pending[0].clone()
+    assert float(coef.item()) == float(oracle.clip_coef(norm.item(), 1.0))
+    opt.step()
+    torch.cuda.synchronize()
+    for i, h in enumerate(host):
+        h["g"] = acc_ref[i]
+    tens = H.oracle_tensors(host)
+    oracle.reference_step(tens, H.HYPER, 1.0, clip_override=float(coef.item()))
+    w = H.compare_state(params, work, opt, tens)
+    assert w == {"p": 0, "m": 0, "v": 0, "bf16": 0, "step": 0}, w
+
+
+def test_cached_norm_invalidated_by_inplace_change():
+    import torchure_amd as ta
+    from torchure_amd.optimizer.working import accumulate_grads_
+
+    host = H.make_host_set([(64, 32), (100,)], seed=23)
+    params, work, opt = H.device_setup(host, DEV)
+    n1 = accumulate_grads_(params, last=True).item()
+    params[0].grad.mul_(2.0)  # torch in-place op bumps the version: cache must not be used
+    n2 = ta.clip_grad_norm(params, None, None).item()
+    g0 = params[0].grad.double()
+    g1 = params[1].grad.double()
+    want = float(torch.sqrt((g0 * g0).sum() + (g1 * g1).sum()).item())
+    assert abs(n2 - want) <= 1e-6 * want and abs(n2 - n1) > 1e-3 * n1

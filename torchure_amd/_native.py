@@ -47,6 +47,10 @@ TENSOR_DTYPE = np.dtype(
 )
 assert TENSOR_DTYPE.itemsize == 64
 
+# tm_accum_t, 32 bytes.
+ACCUM_DTYPE = np.dtype([("acc", "<u8"), ("micro", "<u8"), ("numel", "<i8"), ("reserved", "<i8")])
+assert ACCUM_DTYPE.itemsize == 32
+
 # tm_chunk_t, 8 bytes.
 CHUNK_DTYPE = np.dtype([("tensor", "<u4"), ("chunk", "<u4")])
 
@@ -79,6 +83,8 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _i64, ctypes.POINTER(TmHyper), ctypes.c_int32, _vp, _vp, _vp],
     ),
+    "tm_grad_accumulate_list": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]),
+    "tm_clip_coef": (ctypes.c_int, [_vp, ctypes.c_float, _vp, _vp]),
     "tm_grad_accumulate_bf16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "tm_cast_bf16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
 }

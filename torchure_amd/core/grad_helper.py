@@ -123,6 +123,8 @@ def scale_grads_(
         _native.stream_handle(device),
     )
     _native.check(rc, "tm_grad_scale")
+    for g in grads:
+        torch.autograd.graph.increment_version(g)
 
 
 def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
@@ -147,7 +149,19 @@ def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
 
     materialize_pending_for(holders)
 
-    norm, coef = grad_norm_launch(grads, max_norm)
+    from torchure_amd.optimizer.working import cached_norm
+
+    norm = cached_norm(grads)
+    if norm is not None:
+        # the last micro-step's fused accumulate+norm already measured exactly these grads
+        coef = None
+        if max_norm is not None:
+            coef = torch.empty((), dtype=torch.float32, device=norm.device)
+            rc = _native.lib().tm_clip_coef(norm.data_ptr(), float(max_norm), coef.data_ptr(),
+                                            _native.stream_handle(norm.device))
+            _native.check(rc, "tm_clip_coef")
+    else:
+        norm, coef = grad_norm_launch(grads, max_norm)
     if max_norm is None:
         return norm
 

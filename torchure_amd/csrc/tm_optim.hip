@@ -40,9 +40,11 @@ namespace {
 constexpr int kThreads = 256;  // 4 wave64 per block
 constexpr int kVec = 8;        // elements per thread per iteration (16 B of bf16)
 constexpr int kWaves = kThreads / 64;
+constexpr int kGroupSpan0 = kThreads * 4;  // elements covered by one 4-element group per thread
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 thread_local char g_err[512] = "";
 
@@ -155,6 +157,79 @@ __device__ __forceinline__ double block_sum(double x) {
   return s;
 }
 
+// ------------------------------------------------- fp32 sum-of-squares skeleton
+//
+// Every fp32 sum of squares (the norm of fp32 grads, and the norm fused into the
+// last micro-step of grad accumulation) visits a chunk's elements in this one
+// fixed order, so the fused and the standalone norm give identical bits:
+//   vector part: per 2048-element block iteration, thread t takes the groups
+//     [base + 4t, +4) and [base + 1024 + 4t, +4) (each wave instruction is one
+//     contiguous 1 KiB span) and adds their 8 squares, fma-chained in fp64, to its
+//     accumulator; a last partial iteration takes single groups of 4;
+//   tail (and unaligned tensors): element by element, stride kThreads.
+// Policy::group(e) produces the 4 fp32 values at e (and may store them);
+// Policy::one(i) produces one value.
+
+__device__ __forceinline__ double sumsq4(const f32x4 a, double s) {
+  s = fma((double)a.x, (double)a.x, s);
+  s = fma((double)a.y, (double)a.y, s);
+  s = fma((double)a.z, (double)a.z, s);
+  s = fma((double)a.w, (double)a.w, s);
+  return s;
+}
+
+template <class Policy>
+__device__ __forceinline__ double sumsq_range_f32(const Policy& pol, int64_t start, int64_t end,
+                                                  bool vec) {
+  double acc = 0.0;
+  int64_t vend = start;
+  if (vec) {
+    vend = start + ((end - start) & ~int64_t(3));
+    const int64_t lane4 = static_cast<int64_t>(threadIdx.x) * 4;
+    int64_t base = start;
+    for (; base + 2 * kGroupSpan0 <= vend; base += 2 * kGroupSpan0) {
+      const f32x4 a = pol.group(base + lane4);
+      const f32x4 b = pol.group(base + kGroupSpan0 + lane4);
+      acc += sumsq4(b, sumsq4(a, 0.0));
+    }
+    for (int64_t e = base + lane4; e < vend; e += kGroupSpan0) acc += sumsq4(pol.group(e), 0.0);
+  }
+  for (int64_t i = vend + threadIdx.x; i < end; i += kThreads) {
+    const double x = pol.one(i);
+    acc = fma(x, x, acc);
+  }
+  return acc;
+}
+
+struct ReadF32 {
+  const float* g;
+  __device__ __forceinline__ f32x4 group(int64_t e) const {
+    return ld<true>(reinterpret_cast<const f32x4*>(g + e));
+  }
+  __device__ __forceinline__ float one(int64_t i) const { return g[i]; }
+};
+
+// acc (fp32) += micro (bf16), stored back; yields the new accumulator values.
+struct AccumBf16 {
+  float* acc;
+  const uint16_t* micro;
+  __device__ __forceinline__ f32x4 group(int64_t e) const {
+    f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(acc + e));
+    const u32x2 w = ld<true>(reinterpret_cast<const u32x2*>(micro + e));
+    a.x = a.x + bf16_lo(w.x);
+    a.y = a.y + bf16_hi(w.x);
+    a.z = a.z + bf16_lo(w.y);
+    a.w = a.w + bf16_hi(w.y);
+    st<true>(reinterpret_cast<f32x4*>(acc + e), a);
+    return a;
+  }
+  __device__ __forceinline__ float one(int64_t i) const {
+    const float a = acc[i] + bf16_at(micro, i);
+    acc[i] = a;
+    return a;
+  }
+};
+
 // ------------------------------------------------------------------- norm pass 1
 
 __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
@@ -170,29 +245,8 @@ __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
     if (start >= d.numel) continue;
     const int64_t end = min(start + chunk_elems, d.numel);
     if (d.flags & TM_GRAD_F32) {
-      const float* __restrict__ g = reinterpret_cast<const float*>(d.grad);
-      if (aligned16(d.grad)) {
-        const int64_t vend = start + ((end - start) & ~int64_t(kVec - 1));
-        for (int64_t i = start + threadIdx.x * kVec; i < vend; i += kThreads * kVec) {
-          const f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(g + i));
-          const f32x4 b = ld<true>(reinterpret_cast<const f32x4*>(g + i + 4));
-          double s = 0.0;
-          s = fma((double)a.x, (double)a.x, s);
-          s = fma((double)a.y, (double)a.y, s);
-          s = fma((double)a.z, (double)a.z, s);
-          s = fma((double)a.w, (double)a.w, s);
-          s = fma((double)b.x, (double)b.x, s);
-          s = fma((double)b.y, (double)b.y, s);
-          s = fma((double)b.z, (double)b.z, s);
-          s = fma((double)b.w, (double)b.w, s);
-          acc += s;
-        }
-        for (int64_t i = vend + threadIdx.x; i < end; i += kThreads)
-          acc = fma((double)g[i], (double)g[i], acc);
-      } else {
-        for (int64_t i = start + threadIdx.x; i < end; i += kThreads)
-          acc = fma((double)g[i], (double)g[i], acc);
-      }
+      acc += sumsq_range_f32(ReadF32{reinterpret_cast<const float*>(d.grad)}, start, end,
+                             aligned16(d.grad));
     } else {
       const uint16_t* __restrict__ g = reinterpret_cast<const uint16_t*>(d.grad);
       if (aligned16(d.grad)) {
@@ -235,6 +289,12 @@ __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
 // `max_norm / (total + 1e-6)` on a 0-d fp32 tensor: fp32 add of 1e-6f, fp32
 // reciprocal, fp32 multiply by float(max_norm), then clamp(max=1) with NaN passing
 // through (torch/_tensor.py:1119-1122).
+__device__ __forceinline__ float clip_coef(float norm, float max_norm) {
+  const float r = 1.0f / (norm + 1e-6f);
+  const float c = r * max_norm;
+  return (c > 1.0f) ? 1.0f : c;
+}
+
 __global__ __launch_bounds__(kThreads) void norm_finalize_kernel(
     const double* __restrict__ partials, float max_norm, int clip, float* __restrict__ norm_out,
     float* __restrict__ coef_out) {
@@ -244,12 +304,13 @@ __global__ __launch_bounds__(kThreads) void norm_finalize_kernel(
   if (threadIdx.x == 0) {
     const float norm = static_cast<float>(sqrt(total));
     *norm_out = norm;
-    if (clip) {
-      const float r = 1.0f / (norm + 1e-6f);
-      const float c = r * max_norm;
-      *coef_out = (c > 1.0f) ? 1.0f : c;
-    }
+    if (clip) *coef_out = clip_coef(norm, max_norm);
   }
+}
+
+__global__ void clip_coef_kernel(const float* __restrict__ norm, float max_norm,
+                                 float* __restrict__ coef_out) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *coef_out = clip_coef(*norm, max_norm);
 }
 
 // ------------------------------------------------------------------- grad scale
@@ -335,8 +396,6 @@ constexpr int kUpdateGroups = TM_UPDATE_GROUPS;
 constexpr bool kUpdateNT = TM_UPDATE_NT != 0;  // non-temporal (streaming) loads and stores
 constexpr int kGroupSpan = kThreads * 4;                 // elements per group slot
 constexpr int kUpdateIter = kGroupSpan * kUpdateGroups;  // elements per block iteration
-
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct Group4 {
   f32x4 p, m, v;
@@ -463,6 +522,42 @@ __global__ __launch_bounds__(kThreads) void adamw_update_kernel(
     }
   }
   if (vend < end) update_scalar(d, vend, end, c, clip, coef);
+}
+
+// ------------------------------------------------------- micro-step accumulation
+
+// acc += micro over a list of tensors. kNorm: fixed grid of TM_NORM_PARTIALS blocks,
+// block b owns chunks b, b+G, ... (the partition of norm_partials_kernel) and writes
+// the fp64 partial sum of squares of the new accumulator values; otherwise one block
+// per chunk.
+template <bool kNorm>
+__global__ __launch_bounds__(kThreads) void accumulate_list_kernel(
+    const tm_accum_t* __restrict__ list, int64_t n_list, const tm_chunk_t* __restrict__ chunks,
+    int64_t n_chunks, int64_t chunk_elems, double* __restrict__ partials) {
+  double acc = 0.0;
+  const int64_t first = blockIdx.x;
+  const int64_t step = kNorm ? static_cast<int64_t>(gridDim.x) : n_chunks;
+  for (int64_t c = first; c < n_chunks; c += step) {
+    const tm_chunk_t ck = chunks[c];
+    if (ck.tensor >= n_list) continue;
+    const tm_accum_t d = list[ck.tensor];
+    const int64_t start = static_cast<int64_t>(ck.chunk) * chunk_elems;
+    if (start >= d.numel) continue;
+    const int64_t end = min(start + chunk_elems, d.numel);
+    if (d.micro) {
+      const bool vec = aligned16(d.acc) && aligned8(d.micro);
+      acc += sumsq_range_f32(AccumBf16{reinterpret_cast<float*>(d.acc),
+                                       reinterpret_cast<const uint16_t*>(d.micro)},
+                             start, end, vec);
+    } else if (kNorm) {  // no micro-grad this step: the accumulator only enters the norm
+      acc += sumsq_range_f32(ReadF32{reinterpret_cast<const float*>(d.acc)}, start, end,
+                             aligned16(d.acc));
+    }
+  }
+  if constexpr (kNorm) {
+    const double s = block_sum(acc);
+    if (threadIdx.x == 0) partials[blockIdx.x] = s;
+  }
 }
 
 // ------------------------------------------------------------------- elementwise
@@ -621,6 +716,36 @@ int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
   hipLaunchKernelGGL(adamw_update_kernel<kUpdateNT>, dim3(static_cast<uint32_t>(n_chunks)), dim3(kThreads),
                      0, s, d_tensors, n_tensors, d_chunks, chunk_elems, scal, coef);
   return check_launch("adamw_update_kernel");
+}
+
+int tm_grad_accumulate_list(const tm_accum_t* d_list, int64_t n_list, const tm_chunk_t* d_chunks,
+                            int64_t n_chunks, int64_t chunk_elems, int with_norm, void* d_ws,
+                            float* d_norm, void* stream) {
+  int rc = check_table(d_list, n_list, d_chunks, n_chunks, chunk_elems, "tm_grad_accumulate_list");
+  if (rc) return rc;
+  if (with_norm && (!d_ws || !d_norm))
+    return fail(TM_EINVAL, "tm_grad_accumulate_list: norm requested with null workspace or output");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (with_norm) {
+    double* partials = static_cast<double*>(d_ws);
+    hipLaunchKernelGGL(accumulate_list_kernel<true>, dim3(TM_NORM_PARTIALS), dim3(kThreads), 0, s,
+                       d_list, n_list, d_chunks, n_chunks, chunk_elems, partials);
+    if ((rc = check_launch("accumulate_list_kernel<norm>"))) return rc;
+    hipLaunchKernelGGL(norm_finalize_kernel, dim3(1), dim3(kThreads), 0, s, partials, 0.0f, 0,
+                       d_norm, static_cast<float*>(nullptr));
+    return check_launch("norm_finalize_kernel");
+  }
+  if (n_chunks == 0) return TM_OK;
+  hipLaunchKernelGGL(accumulate_list_kernel<false>, dim3(static_cast<uint32_t>(n_chunks)), dim3(kThreads),
+                     0, s, d_list, n_list, d_chunks, n_chunks, chunk_elems, static_cast<double*>(nullptr));
+  return check_launch("accumulate_list_kernel");
+}
+
+int tm_clip_coef(const float* d_norm, float max_norm, float* d_coef, void* stream) {
+  if (!d_norm || !d_coef) return fail(TM_EINVAL, "tm_clip_coef: null pointer");
+  hipLaunchKernelGGL(clip_coef_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), d_norm,
+                     max_norm, d_coef);
+  return check_launch("clip_coef_kernel");
 }
 
 int tm_grad_accumulate_bf16(float* d_acc, const uint16_t* d_micro, int64_t numel, void* stream) {

@@ -11,7 +11,7 @@ from torchure_amd.optimizer.scheduler import (
     WarmupStableDecaySchedulder,
     wsd_scale,
 )
-from torchure_amd.optimizer.working import accumulate_grad_, attach_bf16_working_params
+from torchure_amd.optimizer.working import accumulate_grad_, accumulate_grads_, attach_bf16_working_params
 
 __all__ = [
     "AdamW",
@@ -24,5 +24,6 @@ __all__ = [
     "WarmupStableDecaySchedulder",
     "wsd_scale",
     "accumulate_grad_",
+    "accumulate_grads_",
     "attach_bf16_working_params",
 ]

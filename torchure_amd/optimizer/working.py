@@ -13,6 +13,9 @@ copy is a separate autograd leaf aliasing its slice.
 
 from __future__ import annotations
 
+import weakref
+
+import numpy as np
 import torch
 
 from torchure_amd import _native
@@ -64,3 +67,107 @@ def accumulate_grad_(acc: torch.Tensor, micro: torch.Tensor) -> None:
         acc.data_ptr(), micro.data_ptr(), acc.numel(), _native.stream_handle(acc.device)
     )
     _native.check(rc, "tm_grad_accumulate_bf16")
+    torch.autograd.graph.increment_version(acc)
+
+
+# device -> (norm tensor, [(weakref(grad), grad._version), ...]) of the last fused
+# accumulate+norm call; clip_grad_norm reuses it when it sees exactly those grads,
+# unmodified (torch bumps _version on every in-place op; this package's own kernels
+# that write grads call increment_version or drop the entry).
+_NORM_CACHE: dict = {}
+
+
+def _stamp(grads):
+    return [(weakref.ref(g), g._version) for g in grads]
+
+
+def cached_norm(grads: list[torch.Tensor]):
+    """The fused norm of exactly ``grads`` (same tensors, same order, unmodified), or None."""
+    if not grads:
+        return None
+    hit = _NORM_CACHE.get(grads[0].device)
+    if hit is None:
+        return None
+    norm, stamp = hit
+    if len(stamp) != len(grads):
+        return None
+    for (ref, ver), g in zip(stamp, grads):
+        if ref() is not g or g._version != ver:
+            return None
+    return norm
+
+
+def drop_cached_norm(device=None) -> None:
+    if device is None:
+        _NORM_CACHE.clear()
+    else:
+        _NORM_CACHE.pop(device, None)
+
+
+def accumulate_grads_(params, *, last: bool = False,
+                      chunk_elems: int = tables.DEFAULT_CHUNK_ELEMS) -> torch.Tensor | None:
+    """One micro-step of gradient accumulation for fp32 masters with bf16 working copies.
+
+    For every param whose working copy carries a bf16 grad: ``p.grad`` (fp32, created
+    as zeros on first use) += that grad, in one launch over the whole list; the bf16
+    grad is then released. This is the fp32 ``.grad`` accumulation autograd performs
+    across micro-batches in torchure/train/trainer.py:383-390.
+
+    With ``last=True`` the same pass also computes the global L2 norm of the
+    accumulated fp32 grads of all ``params`` (returned as a 0-d fp32 device tensor).
+    A following ``clip_grad_norm`` over the same params reuses it instead of reading
+    every grad again; the value is bit-identical to what it would compute.
+    """
+    who = "accumulate_grads_"
+    params = list(params)
+    accs, micros = [], []
+    for p in params:
+        w = getattr(p, "_tm_working", None)
+        mg = w.grad if w is not None else None
+        if mg is None and (not last or p.grad is None):
+            continue
+        tables.require_device_tensor(p, who, "param")
+        if p.grad is None:
+            p.grad = torch.zeros_like(p, memory_format=torch.contiguous_format)
+        g = p.grad
+        tables.require_device_tensor(g, who, "fp32 accumulator")
+        if g.dtype != torch.float32:
+            raise RuntimeError(f"{who}: the accumulator (p.grad) must be float32, got {g.dtype}")
+        if mg is not None:
+            tables.require_device_tensor(mg, who, "bf16 micro-step grad")
+            if mg.dtype != torch.bfloat16 or mg.numel() != g.numel() or mg.device != g.device:
+                raise RuntimeError(f"{who}: micro-step grad must be bf16 of the param's size and device")
+        accs.append(g)
+        micros.append(mg)
+    if not accs:
+        if last:
+            raise AssertionError(f"{who}: no grads to accumulate or measure")
+        return None
+    device = accs[0].device
+    if any(a.device != device for a in accs):
+        raise RuntimeError(f"{who}: all params must be on one device")
+    drop_cached_norm(device)
+    rows = np.zeros(len(accs), dtype=_native.ACCUM_DTYPE)
+    rows["acc"] = np.asarray([a.data_ptr() for a in accs], dtype=np.uint64)
+    rows["micro"] = np.asarray([m.data_ptr() if m is not None else 0 for m in micros], dtype=np.uint64)
+    rows["numel"] = np.asarray([a.numel() for a in accs], dtype=np.int64)
+    chunk_elems = tables.check_chunk_elems(chunk_elems)
+    chunks, n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]), chunk_elems, device)
+    d_rows = tables.upload(rows, device)
+    norm = torch.empty((), dtype=torch.float32, device=device) if last else None
+    ws = torch.empty(_native.workspace_bytes(0), dtype=torch.uint8, device=device) if last else None
+    rc = _native.lib().tm_grad_accumulate_list(
+        d_rows.data_ptr(), len(accs), chunks.data_ptr(), n_chunks, chunk_elems, int(last),
+        ws.data_ptr() if last else None, norm.data_ptr() if last else None,
+        _native.stream_handle(device))
+    _native.check(rc, "tm_grad_accumulate_list")
+    for a, m in zip(accs, micros):
+        if m is not None:
+            torch.autograd.graph.increment_version(a)
+    for p in params:
+        w = getattr(p, "_tm_working", None)
+        if w is not None and w.grad is not None:
+            w.grad = None
+    if last:
+        _NORM_CACHE[device] = (norm, _stamp(accs))
+    return norm
