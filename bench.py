@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--cpu-sample-blocks", type=int, default=2,
                     help="transformer blocks of the config timed for the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-steps", type=int, default=3)
-    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-fp32acc",
+    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,ragged",
                     help="comma list of extra configs reported under 'extra' (empty = none)")
     ap.add_argument("--mode", choices=("bench", "kernels"), default="bench",
                     help="kernels: only the norm and update launches, --reps times each, plus a "

@@ -463,3 +463,74 @@ def test_cached_norm_invalidated_by_inplace_change():
     g1 = params[1].grad.double()
     want = float(torch.sqrt((g0 * g0).sum() + (g1 * g1).sum()).item())
     assert abs(n2 - want) <= 1e-6 * want and abs(n2 - n1) > 1e-3 * n1
+
+
+def test_ragged_full_size_three_chained_steps():
+    """Config 5 at full size: 10,000 tensors, ~1.02e10 elements (~163 GB resident),
+    ~30% odd lengths, 40% 1-D (no decay), 1% all-zero grads; three chained steps.
+    Size-independent checks on every tensor (norm vs fp64, bf16 copy = torch's cast
+    of the master, step counters) and bit-exact oracle checks on a sample that covers
+    the largest, odd-length, 1-D and all-zero tensors, carried across the steps."""
+    import torchure_amd as ta
+
+    shapes = ragged_shapes()
+    n_total = sum(numel(s) for s in shapes)
+    assert len(shapes) == 10000 and n_total > 1e10
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV, generator=gen) * 0.02) for s in shapes]
+    work = ta.attach_bf16_working_params(params)
+    opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
+                             {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True})
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=DEV)
+        st["exp_avg"] = torch.randn(p.shape, device=DEV, generator=gen) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, device=DEV, generator=gen).abs_() * 1e-8
+    zero = set(range(0, 10000, 100))
+    sizes = [numel(s) for s in shapes]
+    order = sorted(range(10000), key=lambda i: sizes[i])
+    sample = sorted({order[-1], order[-2], order[0], 100, 200}
+                    | {i for i in order[5000:5100] if sizes[i] % 8 and len(shapes[i]) == 1}
+                    | {i for i in order[5000:5100] if sizes[i] % 4 == 1 and len(shapes[i]) == 2})
+    held = {i: None for i in sample}
+    for k in range(3):
+        for i, w in enumerate(work):
+            if w.grad is None:
+                w.grad = torch.empty(w.shape, dtype=torch.bfloat16, device=DEV)
+            if i in zero:
+                w.grad.zero_()
+            else:
+                w.grad.normal_(0.0, 1e-3, generator=gen)
+        for i in sample:
+            st = opt.state[params[i]]
+            held[i] = dict(p=params[i].detach().cpu().numpy().reshape(-1).copy(),
+                           m=st["exp_avg"].cpu().numpy().reshape(-1).copy(),
+                           v=st["exp_avg_sq"].cpu().numpy().reshape(-1).copy(),
+                           g=H.from_dev_bf16(work[i].grad).copy())
+        sq = torch.zeros((), dtype=torch.float64, device=DEV)
+        for w in work:
+            sq += torch.sum(w.grad.double() ** 2)
+        norm = ta.clip_grad_norm(params, None, 1.0)
+        coef = opt._pending[0].clone()
+        opt.step()
+        torch.cuda.synchronize()
+        exact = float(sq.sqrt().item())
+        print(f"ragged step {k}: norm {norm.item():.6f} (fp64 {exact:.6f}), coef {coef.item():.6f}", flush=True)
+        assert abs(norm.item() - exact) <= 1e-6 * exact
+        for p, w in zip(params, work):
+            assert torch.equal(w, p.detach().to(torch.bfloat16))
+        steps = torch.stack([opt.state[p]["step"] for p in params])
+        assert bool(torch.all(steps == 1001.0 + k).item())
+        for i in sample:
+            h = held[i]
+            wd = 0.1 if len(shapes[i]) >= 2 else 0.0
+            out = np.zeros(h["p"].size, np.uint16)
+            oracle.adamw_update_bf16(h["p"], h["m"], h["v"], h["g"], out, float(coef.item()), 1,
+                                     1001.0 + k, 3e-4, 0.9, 0.95, wd, 1e-8)
+            st = opt.state[params[i]]
+            assert int(H.ulp_diff(params[i].detach().cpu().numpy().reshape(-1), h["p"]).max()) == 0, (k, i)
+            assert np.array_equal(st["exp_avg"].cpu().numpy().reshape(-1), h["m"]), (k, i)
+            assert np.array_equal(st["exp_avg_sq"].cpu().numpy().reshape(-1), h["v"]), (k, i)
+            assert np.array_equal(H.from_dev_bf16(work[i]), out), (k, i)
+    del params, work, opt
+    torch.cuda.empty_cache()

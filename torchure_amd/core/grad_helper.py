@@ -49,6 +49,10 @@ def grads_of(params) -> tuple[list[torch.Tensor], list[torch.nn.Parameter]]:
     return grads, holders
 
 
+_NORM_UPLOAD = tables.TableUploader()
+_SCALE_UPLOAD = tables.TableUploader()
+
+
 class NormLaunch:
     """One ``tm_grad_norm`` call with its device tables kept alive; calling it
     enqueues both passes on the device's current stream and writes ``norm``
@@ -67,7 +71,7 @@ class NormLaunch:
         self.chunk_elems = chunk_elems
         self.chunks, self.n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]),
                                                        chunk_elems, device)
-        self.d_rows = tables.upload(rows, device)
+        self.d_rows = _NORM_UPLOAD(rows, device)
         self.ws = torch.empty(_native.workspace_bytes(len(grads)), dtype=torch.uint8, device=device)
         self.norm = torch.empty((), dtype=torch.float32, device=device)
         self.clip = max_norm is not None
@@ -112,7 +116,7 @@ def scale_grads_(
     device = grads[0].device
     rows = tables.grad_table(grads, who)
     chunks, n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]), chunk_elems, device)
-    d_rows = tables.upload(rows, device)
+    d_rows = _SCALE_UPLOAD(rows, device)
     rc = _native.lib().tm_grad_scale(
         d_rows.data_ptr(),
         len(grads),
@@ -145,9 +149,10 @@ def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
         assert grads, "clip_grad_norm got no grads; backward didn't run, or all params are frozen"
 
     # A clip pending from an earlier call must land before these grads are measured.
-    from torchure_amd.optimizer.adamw import owner_of, materialize_pending_for
+    from torchure_amd.optimizer.adamw import materialize_pending_for, owners_of
 
-    materialize_pending_for(holders)
+    owners = owners_of(holders)
+    materialize_pending_for(holders, owners)
 
     from torchure_amd.optimizer.working import cached_norm
 
@@ -165,9 +170,8 @@ def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
     if max_norm is None:
         return norm
 
-    owners = {id(owner_of(p)) for p in holders}
-    opt = owner_of(holders[0])
-    if len(owners) == 1 and opt is not None and opt.defer_clip:
+    opt = next(iter(owners)) if len(owners) == 1 else None
+    if opt is not None and opt.defer_clip:
         opt._set_pending_clip(coef, holders)
     else:
         scale_grads_(grads, coef)

@@ -34,28 +34,31 @@ from __future__ import annotations
 
 import numpy as np
 import torch
-from torch.utils.weak import WeakIdKeyDictionary
+import weakref
 
 from torchure_amd import _native
 from torchure_amd.core import tables
 
-# param -> owning AdamW (weak on both sides' lifetimes via the param key).
-_OWNERS: WeakIdKeyDictionary = WeakIdKeyDictionary()
-
-
 def owner_of(p: torch.Tensor):
-    return _OWNERS.get(p)
+    """The torchure_amd AdamW that owns ``p`` (a weak reference set by add_param_group), or None."""
+    ref = getattr(p, "_tm_owner", None)
+    return ref() if ref is not None else None
 
 
-def materialize_pending_for(params) -> None:
-    """Apply any deferred clip pending on the optimizers that own ``params``."""
-    seen = set()
+def owners_of(params) -> set:
+    """Set of owners (AdamW objects, or None for unowned params) of ``params``."""
+    out = set()
     for p in params:
-        opt = _OWNERS.get(p)
-        if opt is not None and id(opt) not in seen:
-            seen.add(id(opt))
-            if opt._pending is not None:
-                opt.materialize_clip()
+        ref = getattr(p, "_tm_owner", None)
+        out.add(ref() if ref is not None else None)
+    return out
+
+
+def materialize_pending_for(params, owners=None) -> None:
+    """Apply any deferred clip pending on the optimizers that own ``params``."""
+    for opt in owners if owners is not None else owners_of(params):
+        if opt is not None and opt._pending is not None:
+            opt.materialize_clip()
 
 
 class AdamW(torch.optim.Optimizer):
@@ -116,6 +119,8 @@ class AdamW(torch.optim.Optimizer):
         self.chunk_elems = tables.check_chunk_elems(chunk_elems)
         self.defer_clip = bool(defer_clip)
         self._pending = None  # (coef device tensor, set of ids of params it applies to)
+        self._uploader = tables.TableUploader()
+        self._verified: dict = {}  # id(param) -> _ParamEntry
         super().__init__(params, defaults)
         if len(self.param_groups) > _native.TM_MAX_GROUPS:
             raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
@@ -124,8 +129,9 @@ class AdamW(torch.optim.Optimizer):
         super().add_param_group(param_group)
         if len(self.param_groups) > _native.TM_MAX_GROUPS:
             raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
+        ref = weakref.ref(self)
         for p in self.param_groups[-1]["params"]:
-            _OWNERS[p] = self
+            p._tm_owner = ref
 
     def __setstate__(self, state):
         super().__setstate__(state)
@@ -134,6 +140,8 @@ class AdamW(torch.optim.Optimizer):
         self.__dict__.setdefault("chunk_elems", tables.DEFAULT_CHUNK_ELEMS)
         self.__dict__.setdefault("defer_clip", True)
         self.__dict__.setdefault("_pending", None)
+        self.__dict__.setdefault("_uploader", tables.TableUploader())
+        self.__dict__.setdefault("_verified", {})
 
     # ------------------------------------------------------------ deferred clip
 
@@ -176,6 +184,10 @@ class AdamW(torch.optim.Optimizer):
         tensors and grads (bench.py uses this to time the kernels back to back)."""
         per_dev: dict = {}
         hyper = []
+        state_map = self.state
+        verified = self._verified
+        clip_flag = _native.TM_FLAG_CLIP
+        bf16, f32 = torch.bfloat16, torch.float32
         for gi, group in enumerate(self.param_groups):
             lr = group["lr"]
             if isinstance(lr, torch.Tensor):
@@ -188,58 +200,83 @@ class AdamW(torch.optim.Optimizer):
             for p in group["params"]:
                 g = p.grad
                 work = getattr(p, "_tm_working", None)
-                if g is None and work is not None:
-                    g = work.grad
                 if g is None:
-                    continue
-                self._check_param(p, g, work)
-                state = self.state[p]
-                if len(state) == 0:
-                    state["step"] = torch.zeros((), dtype=torch.float32, device=p.device)
-                    state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
-                    state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                    if work is None:
+                        continue
+                    g = work.grad
+                    if g is None:
+                        continue
+                state = state_map[p]
+                ent = verified.get(id(p))
+                if (ent is None or ent.param is not p or ent.work is not work
+                        or state.get("step") is not ent.step or state.get("exp_avg") is not ent.m
+                        or state.get("exp_avg_sq") is not ent.v or p.data_ptr() != ent.p_ptr):
+                    ent = self._verify_param(p, state, work)
+                    verified[id(p)] = ent
+                gdt = g.dtype
+                if gdt is bf16:
+                    flags = _native.TM_GRAD_BF16
+                elif gdt is f32:
+                    flags = _native.TM_GRAD_F32
                 else:
-                    st = state["step"]
-                    if st.device != p.device or st.dtype != torch.float32:
-                        state["step"] = st.to(dtype=torch.float32, device=p.device)
-                    for k in ("exp_avg", "exp_avg_sq"):
-                        t = state[k]
-                        if t.device != p.device or t.dtype != torch.float32 or not t.is_contiguous():
-                            state[k] = t.to(dtype=torch.float32, device=p.device).contiguous()
-                flags = tables.grad_flags(g, "torchure_amd.AdamW")
+                    flags = tables.grad_flags(g, "torchure_amd.AdamW")  # raises
+                if (not g.is_cuda or g.get_device() != ent.dev_index or g.numel() != ent.numel
+                        or not g.is_contiguous() or g.is_sparse):
+                    self._check_param(p, g, work)  # raises with a precise message
                 if id(p) in clip_ids:
-                    flags |= _native.TM_FLAG_CLIP
-                cols = per_dev.setdefault(p.device, ([], [], [], [], [], [], [], [], []))
-                cols[0].append(p.data_ptr())
-                cols[1].append(state["exp_avg"].data_ptr())
-                cols[2].append(state["exp_avg_sq"].data_ptr())
-                cols[3].append(g.data_ptr())
-                cols[4].append(work.data_ptr() if work is not None else 0)
-                cols[5].append(state["step"].data_ptr())
-                cols[6].append(p.numel())
-                cols[7].append(gi)
-                cols[8].append(flags)
+                    flags |= clip_flag
+                rows = per_dev.get(ent.device)
+                if rows is None:
+                    rows = per_dev[ent.device] = []
+                rows.append((ent.p_ptr, ent.m_ptr, ent.v_ptr, g.data_ptr(), ent.w_ptr, ent.s_ptr,
+                             ent.numel, gi, flags))
 
         if not per_dev:
             return []
         return self._plan_launches(per_dev, hyper, coef)
 
+    def _verify_param(self, p: torch.Tensor, state: dict, work) -> "_ParamEntry":
+        """Full checks of a param, its working copy and its state (created lazily,
+        moved to fp32 on the param's device when loaded from elsewhere); cached
+        until any of those objects changes."""
+        who = "torchure_amd.AdamW"
+        tables.require_device_tensor(p, who, "param")
+        if p.dtype != torch.float32:
+            raise RuntimeError(f"{who}: params (fp32 masters) must be float32, got {p.dtype}")
+        if work is not None:
+            tables.require_device_tensor(work, who, "bf16 working copy")
+            if work.dtype != torch.bfloat16 or work.numel() != p.numel() or work.device != p.device:
+                raise RuntimeError(f"{who}: working copy must be bf16 of the param's size and device")
+        if len(state) == 0:
+            state["step"] = torch.zeros((), dtype=torch.float32, device=p.device)
+            state["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+            state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+        else:
+            st = state["step"]
+            if st.device != p.device or st.dtype != torch.float32:
+                state["step"] = st.to(dtype=torch.float32, device=p.device)
+            for k in ("exp_avg", "exp_avg_sq"):
+                t = state[k]
+                if t.numel() != p.numel():
+                    raise RuntimeError(f"{who}: state['{k}'] has {t.numel()} elements, param {p.numel()}")
+                if t.device != p.device or t.dtype != torch.float32 or not t.is_contiguous():
+                    state[k] = t.to(dtype=torch.float32, device=p.device).contiguous()
+        return _ParamEntry(p, work, state["step"], state["exp_avg"], state["exp_avg_sq"])
+
+    def load_state_dict(self, state_dict) -> None:
+        self._verified.clear()
+        super().load_state_dict(state_dict)
+
     def _plan_launches(self, per_dev, hyper, coef) -> list["StepLaunch"]:
         groups_c = _native.hyper_array(hyper)
         out = []
-        for device, cols in per_dev.items():
-            n = len(cols[0])
-            rows = np.zeros(n, dtype=_native.TENSOR_DTYPE)
-            for name, col, dt in zip(
-                _native.TENSOR_DTYPE.names,
-                cols,
-                (np.uint64,) * 6 + (np.int64, np.int32, np.uint32),
-            ):
-                rows[name] = np.asarray(col, dtype=dt)
+        for device, recs in per_dev.items():
+            n = len(recs)
+            rows = np.array(recs, dtype=_native.TENSOR_DTYPE)
             if coef is not None and coef.device != device:
                 raise RuntimeError("torchure_amd.AdamW: clip coefficient on another device")
-            chunks, n_chunks = tables.CHUNKS.get(tuple(cols[6]), self.chunk_elems, device)
-            out.append(StepLaunch(device, tables.upload(rows, device), n, chunks, n_chunks,
+            chunks, n_chunks = tables.CHUNKS.get(tuple(r[6] for r in recs), self.chunk_elems, device)
+            out.append(StepLaunch(device, self._uploader(rows, device), n, chunks, n_chunks,
                                   self.chunk_elems, groups_c, len(hyper), coef))
         return out
 
@@ -271,6 +308,24 @@ class AdamW(torch.optim.Optimizer):
                         w.grad = None
                     else:
                         w.grad.zero_()
+
+
+class _ParamEntry:
+    """Verified per-param record: the objects it was built from and their pointers."""
+
+    __slots__ = ("param", "work", "step", "m", "v", "p_ptr", "m_ptr", "v_ptr", "s_ptr", "w_ptr",
+                 "numel", "device", "dev_index")
+
+    def __init__(self, p, work, step, m, v):
+        self.param, self.work, self.step, self.m, self.v = p, work, step, m, v
+        self.p_ptr = p.data_ptr()
+        self.m_ptr = m.data_ptr()
+        self.v_ptr = v.data_ptr()
+        self.s_ptr = step.data_ptr()
+        self.w_ptr = work.data_ptr() if work is not None else 0
+        self.numel = p.numel()
+        self.device = p.device
+        self.dev_index = p.get_device()
 
 
 class StepLaunch:
@@ -315,4 +370,4 @@ def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out:
     return upd + (grad_bytes if with_norm else 0)
 
 
-__all__ = ["AdamW", "owner_of", "materialize_pending_for", "step_bytes_per_param"]
+__all__ = ["AdamW", "owner_of", "owners_of", "materialize_pending_for", "step_bytes_per_param"]

@@ -75,6 +75,7 @@ def accumulate_grad_(acc: torch.Tensor, micro: torch.Tensor) -> None:
 # unmodified (torch bumps _version on every in-place op; this package's own kernels
 # that write grads call increment_version or drop the entry).
 _NORM_CACHE: dict = {}
+_ACC_UPLOAD = tables.TableUploader()
 
 
 def _stamp(grads):
@@ -153,7 +154,7 @@ def accumulate_grads_(params, *, last: bool = False,
     rows["numel"] = np.asarray([a.numel() for a in accs], dtype=np.int64)
     chunk_elems = tables.check_chunk_elems(chunk_elems)
     chunks, n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]), chunk_elems, device)
-    d_rows = tables.upload(rows, device)
+    d_rows = _ACC_UPLOAD(rows, device)
     norm = torch.empty((), dtype=torch.float32, device=device) if last else None
     ws = torch.empty(_native.workspace_bytes(0), dtype=torch.uint8, device=device) if last else None
     rc = _native.lib().tm_grad_accumulate_list(

@@ -50,6 +50,10 @@ CONFIGS = {
 
 
 def shapes_for(name: str) -> list[tuple[int, ...]]:
+    """Shapes of a named configuration: a Qwen3 set from CONFIGS, or "ragged"
+    (the 10,000-tensor stress list of ragged_shapes)."""
+    if name == "ragged":
+        return ragged_shapes()
     return qwen3_param_shapes(**CONFIGS[name])
 
 
