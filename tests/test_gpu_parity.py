@@ -534,3 +534,188 @@ def test_ragged_full_size_three_chained_steps():
             assert np.array_equal(H.from_dev_bf16(work[i]), out), (k, i)
     del params, work, opt
     torch.cuda.empty_cache()
+
+
+def test_fresh_grads_each_step_two_optimizers_interleaved():
+    """Grad tensors reallocated every step (set_to_none) on two interleaved optimizers,
+    more steps than the uploader's pinned slots: every step matches the oracle, so no
+    stale or foreign tensor table is ever used."""
+    import torchure_amd as ta
+
+    sets = []
+    for seed in (31, 32):
+        host = H.make_host_set([(96, 40), (257,), (1024, 3), (13,)], seed=seed)
+        params, work, opt = H.device_setup(host, DEV)
+        sets.append([host, params, work, opt, H.oracle_tensors(host)])
+    r = H.rng(33)
+    for k in range(6):
+        for host, params, work, opt, tens in sets:
+            opt.zero_grad()
+            for i, h in enumerate(host):
+                gb = oracle.bf16_rne((r.standard_normal(h["p"].size) * 1e-3).astype(np.float32))
+                tens[i]["g"] = gb
+                work[i].grad = H.to_dev_bf16(gb, h["shape"], DEV)
+            ta.clip_grad_norm(params, None, 1.0)
+            coef = opt._pending[0].clone()
+            opt.step()
+            torch.cuda.synchronize()
+            oracle.reference_step(tens, H.HYPER, 1.0, clip_override=float(coef.item()))
+            w = H.compare_state(params, work, opt, tens)
+            assert w == {"p": 0, "m": 0, "v": 0, "bf16": 0, "step": 0}, (k, w)
+
+
+def test_groups_with_different_hyperparameters():
+    """Three param groups with different lr / weight decay / betas / eps in one launch."""
+    import torchure_amd as ta
+
+    host = H.make_host_set([(64, 16), (33,), (128, 8), (7, 7)], seed=34)
+    params = [torch.nn.Parameter(torch.from_numpy(h["p"].copy()).view(h["shape"]).to(DEV)) for h in host]
+    for p, h in zip(params, host):
+        p.grad = torch.from_numpy(oracle.bf16_to_f32(h["g"]).copy()).view(h["shape"]).to(DEV)
+    hp = [dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01),
+          dict(lr=0.0, betas=(0.8, 0.9), eps=1e-6, weight_decay=0.5),
+          dict(lr=5e-2, betas=(0.5, 0.75), eps=0.0, weight_decay=0.0)]
+    groups = [dict(params=[params[0], params[1]], **hp[0]), dict(params=[params[2]], **hp[1]),
+              dict(params=[params[3]], **hp[2])]
+    opt = ta.AdamW(groups, fused=True)
+    for p, h in zip(params, host):
+        st = opt.state[p]
+        st["step"] = torch.tensor(h["step"], dtype=torch.float32, device=DEV)
+        st["exp_avg"] = torch.from_numpy(h["m"].copy()).view(h["shape"]).to(DEV)
+        st["exp_avg_sq"] = torch.from_numpy(h["v"].copy()).view(h["shape"]).to(DEV)
+    opt.step()
+    torch.cuda.synchronize()
+    gi_of = [0, 0, 1, 2]
+    for i, (p, h) in enumerate(zip(params, host)):
+        q = hp[gi_of[i]]
+        t = dict(p=h["p"].copy(), m=h["m"].copy(), v=h["v"].copy())
+        oracle.adamw_update(t["p"], t["m"], t["v"], oracle.bf16_to_f32(h["g"]).copy(), h["step"] + 1,
+                            q["lr"], q["betas"][0], q["betas"][1], q["weight_decay"], q["eps"])
+        st = opt.state[p]
+        assert np.array_equal(p.detach().cpu().numpy().reshape(-1).view(np.int32), t["p"].view(np.int32)), i
+        assert np.array_equal(st["exp_avg"].cpu().numpy().reshape(-1), t["m"]), i
+        assert np.array_equal(st["exp_avg_sq"].cpu().numpy().reshape(-1), t["v"]), i
+
+
+def test_nonfinite_grads_propagate_like_torch():
+    """inf / NaN grads: same finiteness pattern and same finite values as torch-ROCm's
+    fused AdamW on the same inputs (no clip, so the coefficient does not spread NaN)."""
+    import torchure_amd as ta
+
+    n = 4096
+    r = H.rng(35)
+    p0 = (r.standard_normal(n) * 0.02).astype(np.float32)
+    g = (r.standard_normal(n) * 1e-3).astype(np.float32)
+    g[::97] = np.inf
+    g[5::101] = -np.inf
+    g[7::103] = np.nan
+    mine = torch.nn.Parameter(torch.from_numpy(p0.copy()).to(DEV))
+    ref = torch.nn.Parameter(torch.from_numpy(p0.copy()).to(DEV))
+    mine.grad = torch.from_numpy(g.copy()).to(DEV)
+    ref.grad = torch.from_numpy(g.copy()).to(DEV)
+    o1 = ta.AdamW([mine], lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, fused=True)
+    o2 = torch.optim.AdamW([ref], lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, fused=True)
+    o1.step()
+    o2.step()
+    torch.cuda.synchronize()
+    for a, b in ((mine.detach(), ref.detach()),
+                 (o1.state[mine]["exp_avg"], o2.state[ref]["exp_avg"]),
+                 (o1.state[mine]["exp_avg_sq"], o2.state[ref]["exp_avg_sq"])):
+        a, b = a.cpu().numpy(), b.cpu().numpy()
+        assert np.array_equal(np.isnan(a), np.isnan(b))
+        fin = np.isfinite(b)
+        assert np.array_equal(np.isfinite(a), fin)
+        assert np.array_equal(a[fin], b[fin])
+        assert np.array_equal(a[np.isinf(b)], b[np.isinf(b)])
+
+
+def test_checkpoint_file_roundtrip_continues_bit_exact(tmp_path):
+    """torchure's Checkpointer flow (torch.save(optimizer.state_dict()); later
+    torch.load(map_location="cpu", weights_only=True) + load_state_dict,
+    torchure/checkpoint/checkpointer.py:43-60,81-82): a resumed optimizer continues
+    exactly like the uninterrupted one."""
+    import torchure_amd as ta
+
+    host = H.make_host_set(shapes_for("tiny")[:6], seed=36)
+    pa, wa, oa = H.device_setup(host, DEV)
+    ta.clip_grad_norm(pa, None, 1.0)
+    oa.step()
+    torch.save(oa.state_dict(), tmp_path / "optimizer.pt")
+    torch.save({"p": [p.detach().cpu() for p in pa]}, tmp_path / "model.pt")
+    # uninterrupted second step
+    ta.clip_grad_norm(pa, None, 1.0)
+    oa.step()
+    torch.cuda.synchronize()
+    # resume from the files into fresh objects
+    model = torch.load(tmp_path / "model.pt", map_location="cpu", weights_only=True)
+    pb = [torch.nn.Parameter(t.to(DEV)) for t in model["p"]]
+    wb = ta.attach_bf16_working_params(pb)
+    for w, w0 in zip(wb, wa):
+        w.grad = w0.grad.clone()
+    ob = ta.build_optimizer(torch.nn.ParameterList(pb), "adamw",
+                            {"lr": H.HYPER["lr"], "weight_decay": H.WD,
+                             "betas": (H.HYPER["beta1"], H.HYPER["beta2"]), "fused": True})
+    ob.load_state_dict(torch.load(tmp_path / "optimizer.pt", map_location="cpu", weights_only=True))
+    ta.clip_grad_norm(pb, None, 1.0)
+    ob.step()
+    torch.cuda.synchronize()
+    for a, b in zip(pa, pb):
+        assert torch.equal(a, b)
+        for k in ("step", "exp_avg", "exp_avg_sq"):
+            assert torch.equal(oa.state[a][k], ob.state[b][k])
+            assert ob.state[b][k].device == b.device
+
+
+def test_grads_as_views_into_flat_buckets():
+    """DDP-style flat grad buckets (torchure/parallelism/data_parallel.py:53-66): grads
+    are views into one flat fp32 buffer at arbitrary offsets, including ones that
+    break 16-byte alignment; the tables alias them directly."""
+    import torchure_amd as ta
+
+    shapes = [(64, 32), (17,), (100, 3), (5,), (8, 8)]
+    host = H.make_host_set(shapes, seed=37, grad_dtype="f32")
+    params = [torch.nn.Parameter(torch.from_numpy(h["p"].copy()).view(h["shape"]).to(DEV)) for h in host]
+    total = sum(h["p"].size for h in host)
+    bucket = torch.zeros(total + 3, device=DEV)
+    off = 0
+    for p, h in zip(params, host):
+        view = bucket[off:off + h["p"].size].view(h["shape"])
+        view.copy_(torch.from_numpy(h["g"]).view(h["shape"]))
+        p.grad = view
+        off += h["p"].size
+    opt = ta.AdamW(params, lr=H.HYPER["lr"], betas=(H.HYPER["beta1"], H.HYPER["beta2"]),
+                   weight_decay=H.WD, fused=True)
+    for p, h in zip(params, host):
+        st = opt.state[p]
+        st["step"] = torch.tensor(h["step"], dtype=torch.float32, device=DEV)
+        st["exp_avg"] = torch.from_numpy(h["m"].copy()).view(h["shape"]).to(DEV)
+        st["exp_avg_sq"] = torch.from_numpy(h["v"].copy()).view(h["shape"]).to(DEV)
+        h["wd"] = H.WD
+    norm = ta.clip_grad_norm(params, None, 1.0)
+    coef = opt._pending[0].clone()
+    opt.step()
+    torch.cuda.synchronize()
+    tens = H.oracle_tensors(host)
+    for t in tens:
+        t["out"] = None
+    ref_norm, _ = oracle.reference_step(tens, H.HYPER, 1.0, clip_override=float(coef.item()))
+    assert abs(norm.item() - float(ref_norm)) <= 1e-6 * float(ref_norm)
+    w = H.compare_state(params, None, opt, tens)
+    assert w == {"p": 0, "m": 0, "v": 0, "bf16": 0, "step": 0}, w
+
+
+def test_materialize_clip_equals_eager_clip():
+    import torchure_amd as ta
+
+    host = H.make_host_set([(64, 64), (50,)], seed=38, grad_std=0.1, grad_dtype="f32")
+    pa, _, oa = H.device_setup(host, DEV, working=False)
+    pb, _, ob = H.device_setup(host, DEV, working=False)
+    ob.defer_clip = False
+    ta.clip_grad_norm(pa, None, 1.0)
+    assert oa._pending is not None
+    oa.materialize_clip()
+    ta.clip_grad_norm(pb, None, 1.0)
+    assert ob._pending is None
+    torch.cuda.synchronize()
+    for a, b in zip(pa, pb):
+        assert torch.equal(a.grad, b.grad)
