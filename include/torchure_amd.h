@@ -155,7 +155,8 @@ int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
  * the deferred clip scale (tensors with TM_FLAG_CLIP read *d_coef) and the bf16
  * working-copy refresh (param_bf16 != 0).
  *   h_groups  n_groups (1..TM_MAX_GROUPS) host records; tm_tensor_t.group indexes them
- *   d_coef    clip coefficient (device fp32), required if any tensor has TM_FLAG_CLIP
+ *   d_coef    clip coefficient (device fp32) applied to TM_FLAG_CLIP tensors; NULL means
+ *             no tensor is scaled (TM_FLAG_CLIP is then ignored)
  *   d_ws      at least tm_workspace_bytes(n_tensors) bytes
  */
 int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,

@@ -504,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void adamw_update_kernel(
   if (start >= d.numel) return;
   const int64_t end = min(start + chunk_elems, d.numel);
   const TensorScal c = scal[ck.tensor];
-  const bool clip = (d.flags & TM_FLAG_CLIP) != 0;
+  const bool clip = (d.flags & TM_FLAG_CLIP) != 0 && coef_p != nullptr;
   const float coef = clip ? *coef_p : 1.0f;
   const bool out = d.param_bf16 != 0;
   const bool grad_ok = (d.flags & TM_GRAD_F32) ? aligned16(d.grad) : aligned8(d.grad);
@@ -710,11 +710,9 @@ int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
                      dim3(kThreads), 0, s, d_tensors, n_tensors, hyper, scal);
   if ((rc = check_launch("adamw_prep_kernel"))) return rc;
   if (n_chunks == 0) return TM_OK;
-  // d_coef may be null only when no tensor asks for the clip; the kernel reads it
-  // only for TM_FLAG_CLIP tensors, so point it at the workspace otherwise.
-  const float* coef = d_coef ? d_coef : reinterpret_cast<const float*>(d_ws);
+  // d_coef == NULL: TM_FLAG_CLIP is ignored (every grad is used unscaled).
   hipLaunchKernelGGL(adamw_update_kernel<kUpdateNT>, dim3(static_cast<uint32_t>(n_chunks)), dim3(kThreads),
-                     0, s, d_tensors, n_tensors, d_chunks, chunk_elems, scal, coef);
+                     0, s, d_tensors, n_tensors, d_chunks, chunk_elems, scal, d_coef);
   return check_launch("adamw_update_kernel");
 }
 
