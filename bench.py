@@ -51,6 +51,9 @@ def parse():
                     help="kernels: only the norm and update launches, --reps times each, plus a "
                          "2 GiB device copy for calibrating HBM byte counters (for rocprofv3 --pmc)")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--torch-reference", type=int, default=1,
+                    help="also time torch-ROCm's own GPU path (foreach clip + fused AdamW) on the "
+                         "same config and device (1 = yes)")
     return ap.parse_args()
 
 
@@ -244,6 +247,58 @@ def run_gpu_fp32acc(config: str, steps: int, warmup: int, chunk_elems, dev):
     return out
 
 
+def run_torch_gpu_reference(config: str, steps: int, warmup: int, dev):
+    """The reference's own GPU path on the same device, for comparison: fp32 grads
+    (the reference trains with fp32 .grad), torch._foreach_norm + stack + vector_norm,
+    clamp(max_norm / (total + 1e-6), max=1), torch._foreach_mul_
+    (torchure/core/grad_helper.py:17-33), torch.optim.AdamW(fused=True) with the two
+    groups of torchure/optimizer/builder.py:37-43, then the bf16 cast autocast performs
+    (torchure/train/trainer.py:374). Same synthetic steady state as the main leg."""
+    import torch
+
+    from torchure_amd.workloads import shapes_for
+
+    shapes = shapes_for(config)
+    g = torch.Generator(device=dev).manual_seed(4321)
+    params = [torch.nn.Parameter(torch.randn(s, device=dev, generator=g) * 0.02) for s in shapes]
+    for p in params:
+        p.grad = (torch.randn(p.shape, device=dev, generator=g) * 1e-3).to(torch.bfloat16).float()
+    groups = [{"params": [p for p in params if p.dim() >= 2], "weight_decay": 0.1},
+              {"params": [p for p in params if p.dim() < 2], "weight_decay": 0.0}]
+    opt = torch.optim.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, fused=True)
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=dev)
+        st["exp_avg"] = torch.randn(p.shape, device=dev, generator=g) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, device=dev, generator=g).abs_() * 1e-8
+    bf16 = [torch.empty(p.shape, dtype=torch.bfloat16, device=dev) for p in params]
+    grads = [p.grad for p in params]
+
+    def one():
+        norms = torch._foreach_norm(grads, 2.0)
+        total = torch.linalg.vector_norm(torch.stack(norms), 2.0)
+        coef = torch.clamp(1.0 / (total + 1e-6), max=1.0)
+        torch._foreach_mul_(grads, coef)
+        opt.step()
+        torch._foreach_copy_(bf16, params)
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    n = sum(p.numel() for p in params)
+    del params, grads, opt, bf16
+    torch.cuda.empty_cache()
+    return dict(config=config, ms_per_step=round(ms, 4), n_params=n,
+                GBps_on_30B_basis=round(STEP_BYTES_PER_PARAM * n / (ms * 1e-3) / 1e9, 1),
+                path="torch-ROCm: fp32 grads, _foreach_norm clip + _foreach_mul_, "
+                     "AdamW(fused=True), bf16 cast (46 B/param moved)")
+
+
 def run_cpu_baseline(config: str, blocks: int, steps: int):
     """Reference composition on torch CPU over the first ``blocks`` transformer
     blocks of ``config`` (the sample), bf16 grads widened to fp32."""
@@ -327,6 +382,12 @@ def main():
         r["frac_of_peak"] = round(r["GBps"] / PEAK_HBM_GBS, 4)
         extra[cfg] = r
         print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
+
+    if args.torch_reference:
+        ref = run_torch_gpu_reference(args.config, max(5, min(args.steps, 20)), 2, dev)
+        ref["speedup_of_this_build"] = round(ref["ms_per_step"] / main_res["ms_per_step"], 3)
+        extra["torch_rocm_reference_" + args.config] = ref
+        print(f"[bench] torch-ROCm reference: {ref}", file=sys.stderr, flush=True)
 
     n = main_res["n_params"]
     ms = main_res["ms_per_step"]
