@@ -719,3 +719,21 @@ def test_materialize_clip_equals_eager_clip():
     torch.cuda.synchronize()
     for a, b in zip(pa, pb):
         assert torch.equal(a.grad, b.grad)
+
+
+def test_step_bumps_autograd_versions():
+    """The kernels write through raw pointers; the step bumps the version counters of
+    everything it wrote, as torch's in-place fused AdamW does, so autograd still
+    detects a param modified between forward and backward."""
+    import torchure_amd as ta
+
+    host = H.make_host_set([(32, 16), (9,)], seed=39)
+    params, work, opt = H.device_setup(host, DEV)
+    before = [(p._version, w._version, opt.state[p]["exp_avg"]._version) for p, w in zip(params, work)]
+    x = torch.randn(4, 32, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    y = (x @ work[0]).sum()  # saves work[0] (for x's grad) for backward
+    opt.step()
+    for (pv, wv, mv), p, w in zip(before, params, work):
+        assert p._version > pv and w._version > wv and opt.state[p]["exp_avg"]._version > mv
+    with pytest.raises(RuntimeError, match="modified by an inplace operation"):
+        y.backward()

@@ -225,11 +225,12 @@ class AdamW(torch.optim.Optimizer):
                     self._check_param(p, g, work)  # raises with a precise message
                 if id(p) in clip_ids:
                     flags |= clip_flag
-                rows = per_dev.get(ent.device)
-                if rows is None:
-                    rows = per_dev[ent.device] = []
-                rows.append((ent.p_ptr, ent.m_ptr, ent.v_ptr, g.data_ptr(), ent.w_ptr, ent.s_ptr,
-                             ent.numel, gi, flags))
+                bucket = per_dev.get(ent.device)
+                if bucket is None:
+                    bucket = per_dev[ent.device] = ([], [])
+                bucket[0].append((ent.p_ptr, ent.m_ptr, ent.v_ptr, g.data_ptr(), ent.w_ptr, ent.s_ptr,
+                                  ent.numel, gi, flags))
+                bucket[1].extend(ent.written)
 
         if not per_dev:
             return []
@@ -270,14 +271,14 @@ class AdamW(torch.optim.Optimizer):
     def _plan_launches(self, per_dev, hyper, coef) -> list["StepLaunch"]:
         groups_c = _native.hyper_array(hyper)
         out = []
-        for device, recs in per_dev.items():
+        for device, (recs, written) in per_dev.items():
             n = len(recs)
             rows = np.array(recs, dtype=_native.TENSOR_DTYPE)
             if coef is not None and coef.device != device:
                 raise RuntimeError("torchure_amd.AdamW: clip coefficient on another device")
             chunks, n_chunks = tables.CHUNKS.get(tuple(r[6] for r in recs), self.chunk_elems, device)
             out.append(StepLaunch(device, self._uploader(rows, device), n, chunks, n_chunks,
-                                  self.chunk_elems, groups_c, len(hyper), coef))
+                                  self.chunk_elems, groups_c, len(hyper), coef, written))
         return out
 
     @staticmethod
@@ -314,10 +315,13 @@ class _ParamEntry:
     """Verified per-param record: the objects it was built from and their pointers."""
 
     __slots__ = ("param", "work", "step", "m", "v", "p_ptr", "m_ptr", "v_ptr", "s_ptr", "w_ptr",
-                 "numel", "device", "dev_index")
+                 "numel", "device", "dev_index", "written")
 
     def __init__(self, p, work, step, m, v):
         self.param, self.work, self.step, self.m, self.v = p, work, step, m, v
+        # tensors the step writes through raw pointers; their autograd version counters
+        # are bumped after each launch, as an in-place torch op would do
+        self.written = (p, m, v, step) if work is None else (p, m, v, step, work)
         self.p_ptr = p.data_ptr()
         self.m_ptr = m.data_ptr()
         self.v_ptr = v.data_ptr()
@@ -336,7 +340,9 @@ class StepLaunch:
     tensors with the same grads (used to time the kernels back to back).
     """
 
-    def __init__(self, device, d_rows, n, chunks, n_chunks, chunk_elems, groups_c, n_groups, coef):
+    def __init__(self, device, d_rows, n, chunks, n_chunks, chunk_elems, groups_c, n_groups, coef,
+                 written=()):
+        self.written = list(written)
         self.device = device
         self.d_rows = d_rows
         self.n = n
@@ -362,6 +368,8 @@ class StepLaunch:
             _native.stream_handle(self.device),
         )
         _native.check(rc, "tm_adamw_step")
+        if self.written:
+            torch.autograd.graph.increment_version(self.written)
 
 
 def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out: bool = True) -> int:
