@@ -94,12 +94,14 @@ def adamw_scalars(step_after: float, lr: float, beta1: float, beta2: float) -> t
     return float(out[0]), float(out[1])
 
 
-def adamw_update(p, m, v, g, step_after, lr, beta1, beta2, weight_decay, eps) -> None:
-    """In-place AdamW on float32 numpy arrays; ``g`` is the fp32 (clipped) grad."""
+def adamw_update(p, m, v, g, step_after, lr, beta1, beta2, weight_decay, eps,
+                 threaded: bool = False) -> None:
+    """In-place AdamW on float32 numpy arrays; ``g`` is the fp32 (clipped) grad.
+    ``threaded`` runs the same element-wise code on OpenMP threads (same results)."""
     for a in (p, m, v, g):
         assert a.dtype == np.float32 and a.flags.c_contiguous
     assert p.size == m.size == v.size == g.size
-    lib().orc_adamw_update(_ptr(p), _ptr(m), _ptr(v), _ptr(g), p.size, float(step_after),
+    lib(threaded).orc_adamw_update(_ptr(p), _ptr(m), _ptr(v), _ptr(g), p.size, float(step_after),
                            lr, beta1, beta2, weight_decay, eps)
 
 

@@ -25,7 +25,8 @@
  *   orc_clip_coef      clamp(max_norm / (total + 1e-6), max=1.0), grad_helper.py:32,
  *                      evaluated as reciprocal-then-multiply in fp32
  *                      (torch/_tensor.py:1119-1122).
- *   orc_adamw_update_mt  the same update split over threads (for timing only).
+ * The element loops carry OpenMP pragmas: the liborc_mt.so build splits them over
+ * threads (same per-element results), liborc.so runs them serially.
  */
 #include <math.h>
 #include <stdint.h>
@@ -95,6 +96,7 @@ void orc_adamw_update(float* p, float* m, float* v, const float* g, int64_t n, f
   orc_adamw_scalars(step_after, lr, beta1, beta2, sc);
   const double neg_lrwd = -(lr * weight_decay);
   const int decay = weight_decay != 0.0;
+#pragma omp parallel for schedule(static)
   for (int64_t i = 0; i < n; ++i)
     adamw_elem(p + i, m + i, v + i, g[i], neg_lrwd, decay, beta1, beta2, eps, sc[0], sc[1]);
 }

@@ -362,12 +362,14 @@ def test_state_dict_roundtrip_with_torch_adamw():
         assert opt2.state[p]["step"].device == p.device
 
 
-def test_full_size_0p6b_properties():
-    """Config 2 at full size (596M params): norm vs fp64 over every grad, the bf16
-    copy is RNE(master) everywhere, and sampled tensors match the oracle bit for bit."""
+@pytest.mark.parametrize("config", ["qwen3-0.6b", "qwen3-4b"])
+def test_full_size_properties(config):
+    """Configs 2 and 4 at full size (596M / 4.02B params): norm vs fp64 over every
+    grad, the bf16 copy is RNE(master) everywhere, and sampled tensors -- including
+    the tied embedding, the largest tensor -- match the oracle bit for bit."""
     import torchure_amd as ta
 
-    shapes = shapes_for("qwen3-0.6b")
+    shapes = shapes_for(config)
     g = torch.Generator(device=DEV).manual_seed(0)
     params, grads = [], []
     for s in shapes:
@@ -398,7 +400,7 @@ def test_full_size_0p6b_properties():
         t = [dict(p=p0.copy(), m=np.zeros(n, np.float32), v=np.zeros(n, np.float32), g=gb, step=0.0,
                   wd=0.1 if len(shapes[i]) >= 2 else 0.0, out=np.zeros(n, np.uint16))]
         oracle.adamw_update_bf16(t[0]["p"], t[0]["m"], t[0]["v"], gb, t[0]["out"], float(coef.item()), 1,
-                                 1.0, 3e-4, 0.9, 0.95, t[0]["wd"], 1e-8)
+                                 1.0, 3e-4, 0.9, 0.95, t[0]["wd"], 1e-8, threaded=True)
         got = params[i].detach().cpu().numpy().reshape(-1)
         assert int(H.ulp_diff(got, t[0]["p"]).max()) == 0, i
         assert np.array_equal(opt.state[params[i]]["exp_avg"].cpu().numpy().reshape(-1), t[0]["m"])
@@ -737,3 +739,77 @@ def test_step_bumps_autograd_versions():
         assert p._version > pv and w._version > wv and opt.state[p]["exp_avg"]._version > mv
     with pytest.raises(RuntimeError, match="modified by an inplace operation"):
         y.backward()
+
+
+def test_full_size_config3_fp32_accumulation():
+    """Config 3 at full size (Qwen3-0.6B shapes, 596M params): four bf16 micro-steps
+    accumulated into fp32 .grad (the last one also measuring the norm), grads scaled
+    so the global norm is ~5 and the clip triggers, WSD lr at decay step 9800. The
+    fused norm equals the standalone norm pass bit for bit and fp64 within 1e-6;
+    sampled tensors match the oracle bit for bit."""
+    import torchure_amd as ta
+    from torchure_amd.core.grad_helper import grad_norm_launch
+    from torchure_amd.optimizer.working import accumulate_grads_
+
+    shapes = shapes_for("qwen3-0.6b")
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV, generator=gen) * 0.02) for s in shapes]
+    work = ta.attach_bf16_working_params(params)
+    opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
+                             {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True})
+    sched = ta.build_scheduler(opt, {"type": "wsd", "total_steps": 10000, "warmup_ratio": 0.001,
+                                     "decay_ratio": 0.2})
+    sched.last_epoch = 9799
+    sched.step()
+    lr = opt.param_groups[0]["lr"]
+    assert lr == 3e-4 * oracle.wsd_scale(9800, 10000, 0.001, 0.2)
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(9799.0, dtype=torch.float32, device=DEV)
+        st["exp_avg"] = torch.randn(p.shape, device=DEV, generator=gen) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, device=DEV, generator=gen).abs_() * 1e-8
+    # sigma so that 4 summed micro-grads have global norm ~5: 5 / sqrt(4 * N)
+    sigma = 5.0 / np.sqrt(4.0 * sum(numel(s) for s in shapes))
+    sample = [0, 3, 5, 6, len(shapes) - 1]
+    micro_host = {i: [] for i in sample}
+    for k in range(4):
+        for i, w in enumerate(work):
+            w.grad = (torch.randn(w.shape, device=DEV, generator=gen) * sigma).to(torch.bfloat16)
+            if i in micro_host:
+                micro_host[i].append(H.from_dev_bf16(w.grad).copy())
+        if k == 3:
+            before = {i: (params[i].detach().cpu().numpy().reshape(-1).copy(),
+                          opt.state[params[i]]["exp_avg"].cpu().numpy().reshape(-1).copy(),
+                          opt.state[params[i]]["exp_avg_sq"].cpu().numpy().reshape(-1).copy())
+                      for i in sample}
+        norm = accumulate_grads_(params, last=(k == 3))
+    grads = [p.grad for p in params]
+    standalone, _ = grad_norm_launch(grads, None)
+    exact_sq = sum(float(torch.sum(g.double() ** 2).item()) for g in grads)
+    torch.cuda.synchronize()
+    assert norm.view(torch.int32).item() == standalone.view(torch.int32).item()
+    assert abs(norm.item() - np.sqrt(exact_sq)) <= 1e-6 * np.sqrt(exact_sq)
+    assert 4.0 < norm.item() < 6.0
+    acc = {i: params[i].grad.cpu().numpy().reshape(-1).copy() for i in sample}
+    got = ta.clip_grad_norm(params, None, 1.0)
+    assert got is norm
+    coef = opt._pending[0].clone()
+    opt.step()
+    torch.cuda.synchronize()
+    assert float(coef.item()) < 0.25
+    for i in sample:
+        want = np.zeros_like(acc[i])
+        for mg in micro_host[i]:
+            want = (want + oracle.bf16_to_f32(mg)).astype(np.float32)
+        assert np.array_equal(acc[i], want), i
+        p0, m0, v0 = before[i]
+        gclip = (acc[i] * np.float32(coef.item())).astype(np.float32)
+        wd = 0.1 if len(shapes[i]) >= 2 else 0.0
+        oracle.adamw_update(p0, m0, v0, gclip, 9800.0, lr, 0.9, 0.95, wd, 1e-8, threaded=True)
+        st = opt.state[params[i]]
+        assert int(H.ulp_diff(params[i].detach().cpu().numpy().reshape(-1), p0).max()) == 0, i
+        assert np.array_equal(st["exp_avg"].cpu().numpy().reshape(-1), m0), i
+        assert np.array_equal(st["exp_avg_sq"].cpu().numpy().reshape(-1), v0), i
+        assert torch.equal(work[i], params[i].detach().to(torch.bfloat16))
+    del params, work, opt, grads
+    torch.cuda.empty_cache()
