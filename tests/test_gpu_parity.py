@@ -813,3 +813,48 @@ def test_full_size_config3_fp32_accumulation():
         assert torch.equal(work[i], params[i].detach().to(torch.bfloat16))
     del params, work, opt, grads
     torch.cuda.empty_cache()
+
+
+class _TiedLM(torch.nn.Module):
+    """A small language model with a tied embedding / output head: the parameter
+    reached through two modules must count once (model.parameters() yields it once)."""
+
+    def __init__(self, vocab=64, dim=32):
+        super().__init__()
+        self.emb = torch.nn.Embedding(vocab, dim)
+        self.norm1 = torch.nn.RMSNorm(dim)
+        self.up = torch.nn.Linear(dim, 3 * dim, bias=False)
+        self.down = torch.nn.Linear(3 * dim, dim, bias=False)
+        self.norm2 = torch.nn.RMSNorm(dim)
+        self.head = torch.nn.Linear(dim, vocab, bias=False)
+        self.head.weight = self.emb.weight
+
+    def forward(self, ids):
+        x = self.emb(ids)
+        x = x + self.down(torch.nn.functional.silu(self.up(self.norm1(x))))
+        return self.head(self.norm2(x))
+
+
+@pytest.mark.parametrize("max_norm", [0.1, 1.0, 5.0])
+def test_clip_matches_torch_on_tied_model(max_norm):
+    """torchure tests/grad_helper.py:83-102 restated: clip_grad_norm on a real model
+    with a tied embedding vs torch.nn.utils.clip_grad_norm_ (rtol 1e-5, atol 1e-7)."""
+    import torchure_amd as ta
+
+    def build():
+        torch.manual_seed(0)
+        return _TiedLM().to(DEV)
+
+    mine, ref = build(), build()
+    g = torch.Generator().manual_seed(1234)
+    ids = torch.randint(0, 64, (2, 16), generator=g).to(DEV)
+    for m in (mine, ref):
+        logits = m(ids)
+        loss = torch.nn.functional.cross_entropy(logits[:, :-1].reshape(-1, 64), ids[:, 1:].reshape(-1))
+        (loss * 50.0).backward()  # norms large enough that every max_norm clips
+    got = ta.clip_grad_norm(mine.parameters(), None, max_norm)
+    want = torch.nn.utils.clip_grad_norm_(ref.parameters(), max_norm)
+    torch.testing.assert_close(got, want)
+    assert len(list(mine.parameters())) == 5  # tied weight counted once
+    for (name, p), (_, q) in zip(mine.named_parameters(), ref.named_parameters()):
+        torch.testing.assert_close(p.grad, q.grad, rtol=1e-5, atol=1e-7, msg=name)
