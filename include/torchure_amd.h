@@ -191,6 +191,33 @@ int tm_clip_coef(const float* d_norm, float max_norm, float* d_coef, void* strea
  * Rounding rule of torch/headeronly/util/BFloat16.h:100-114 (NaN -> 0x7FC0). */
 int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* stream);
 
+/* ---- chunked fused linear + cross-entropy (torchure/loss/fused_linear_ce.py) ---- */
+
+/*
+ * One fused pass over a chunk of bf16 logits (rows x vocab, row stride ld elements),
+ * replacing the per-chunk softmax math of torchure/loss/fused_linear_ce.py:40-52:
+ *   lse = logsumexp(float(logits)), row_loss = lse - logits[label] (0 on ignored rows),
+ *   logits <- bf16(exp(logits - lse) - onehot(label)) on valid rows, 0 on ignored rows.
+ * Labels are int64; a row is ignored when label == ignore_index.
+ */
+int tm_ce_rows_bf16(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows,
+                    int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream);
+
+/*
+ * Deterministic loss reduction (fused_linear_ce.py:76-90): d_out3[0] = sum of row
+ * losses, d_out3[1] = n_valid = max(1, count(label != ignore_index)),
+ * d_out3[2] = d_out3[0] / d_out3[1] (the mean loss).
+ */
+int tm_ce_loss(const float* d_row_loss, const int64_t* d_labels, int64_t rows, int64_t ignore_index,
+               float* d_out3, void* stream);
+
+/*
+ * Backward scaling in place (fused_linear_ce.py:117-126): scale = *d_grad_out / *d_n_valid;
+ * grad_h (bf16) *= bf16(scale), grad_w (fp32, may be NULL with nw = 0) *= scale.
+ */
+int tm_ce_scale_grads(uint16_t* d_grad_h, int64_t nh, float* d_grad_w, int64_t nw,
+                      const float* d_grad_out, const float* d_n_valid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,3 +45,43 @@ def reference_step(params, opt, max_norm=1.0, bf16_out=None) -> torch.Tensor:
         for p, w in zip(params, bf16_out):
             w.copy_(p.detach().to(torch.bfloat16))
     return total
+
+
+def chunk_fwd_reference(hidden, weight, labels, ignore_index):
+    """Per-chunk math of torchure/loss/fused_linear_ce.py:31-59 with the same torch
+    calls (without torch.compile): returns (loss_sum, grad_hidden, grad_weight)."""
+    logits = (hidden @ weight.t()).float()
+    valid = labels != ignore_index
+    safe = torch.where(valid, labels, 0).unsqueeze(1)
+    lse = torch.logsumexp(logits, dim=-1)
+    target = logits.gather(1, safe).squeeze(1)
+    loss_sum = ((lse - target) * valid).sum()
+    probs = torch.exp(logits - lse.unsqueeze(1))
+    probs = probs * valid.unsqueeze(1)
+    probs.scatter_add_(1, safe, -valid.float().unsqueeze(1))
+    grad_logits = probs.to(hidden.dtype)
+    grad_hidden = grad_logits @ weight
+    grad_weight = grad_logits.t() @ hidden
+    return loss_sum, grad_hidden, grad_weight
+
+
+def fused_linear_ce_reference(hidden, weight, labels, ignore_index=-100, chunk_size=1024,
+                              chunk_fn=chunk_fwd_reference):
+    """Forward + backward (grad_out = 1) of the reference op, fused_linear_ce.py:62-127.
+    Returns (mean loss, grad_hidden, grad_weight fp32)."""
+    n = hidden.shape[0]
+    w = weight.to(hidden.dtype)
+    loss_sum = torch.zeros((), dtype=torch.float32, device=hidden.device)
+    grad_hidden = torch.empty_like(hidden)
+    grad_weight = torch.zeros_like(weight, dtype=torch.float32)
+    for s in range(0, n, chunk_size):
+        e = min(s + chunk_size, n)
+        chunk_loss, gh, gw = chunk_fn(hidden[s:e], w, labels[s:e], ignore_index)
+        loss_sum += chunk_loss
+        grad_hidden[s:e] = gh
+        grad_weight += gw
+    n_valid = (labels != ignore_index).sum().clamp_min(1)
+    scale = 1.0 / n_valid
+    grad_hidden.mul_(scale.to(grad_hidden.dtype))
+    grad_weight.mul_(scale)
+    return loss_sum / n_valid, grad_hidden, grad_weight

@@ -87,6 +87,9 @@ _SIGNATURES = {
     "tm_clip_coef": (ctypes.c_int, [_vp, ctypes.c_float, _vp, _vp]),
     "tm_grad_accumulate_bf16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "tm_cast_bf16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "tm_ce_rows_bf16": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "tm_ce_loss": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "tm_ce_scale_grads": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

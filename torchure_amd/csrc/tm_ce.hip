@@ -1,0 +1,283 @@
+// tm_ce.hip -- gfx950 kernels of the chunked fused linear + cross-entropy.
+//
+// The reference (torchure/loss/fused_linear_ce.py:31-59) computes, per chunk of rows,
+//   logits = h @ W^T (bf16 GEMM), lse = logsumexp(float(logits)), loss = lse - target,
+//   grad_logits = bf16(softmax - onehot) on valid rows (0 on ignored rows),
+//   grad_h = grad_logits @ W, grad_W += grad_logits^T @ h,
+// and scales both grads by grad_out / n_valid in backward (:94-127).
+// The GEMMs are plain library GEMMs (hipBLASLt). These kernels do the rest:
+//   ce_rows_kernel        one workgroup per row: online max / sum-exp over the bf16
+//                         logits row, target logit, per-row loss, then softmax - onehot
+//                         written back over the logits as bf16 (RNE). A row of up to
+//                         kRegCols vectors per thread stays in registers (one HBM read);
+//                         longer rows are read twice.
+//   ce_loss_kernel        one workgroup: fixed-order sum of the per-row losses and of
+//                         the valid-row count -> loss_sum, n_valid, mean loss.
+//   ce_scale_kernel       backward: grad_h (bf16) *= bf16(g / n_valid),
+//                         grad_W (fp32) *= g / n_valid.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "torchure_amd.h"
+#include "tm_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kCeThreads = 1024;  // 16 wave64 per row
+constexpr int kCeWaves = kCeThreads / 64;
+constexpr int kRegCols = 20;  // 8-element vectors per thread kept in registers (V <= 163,840)
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename... A>
+int ce_fail(int code, const char* fmt, A... args) {
+  return tm_internal_fail(code, fmt, args...);
+}
+
+__device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+__device__ __forceinline__ uint32_t rne16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (f != f) ? 0x7FC0u : r;
+}
+
+// (max, sum of exp(x - max)) pairs combine associatively.
+__device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
+  if (m2 > m) {
+    s = s * expf(m - m2) + s2;
+    m = m2;
+  } else if (m2 == m) {
+    s = s + s2;
+  } else {
+    s = s + s2 * expf(m2 - m);
+  }
+}
+
+__device__ __forceinline__ void ms_add(float& m, float& s, float x) {
+  if (x == -INFINITY) return;  // exp(-inf - m) = 0 contributes nothing
+  if (x > m) {
+    s = s * expf(m - x) + 1.0f;
+    m = x;
+  } else {
+    s = s + expf(x - m);
+  }
+}
+
+// Block-wide (max, sumexp) in a fixed order; every thread receives the result.
+__device__ __forceinline__ void block_ms(float& m, float& s) {
+  __shared__ float lm[kCeWaves], ls[kCeWaves];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, 64);
+    const float s2 = __shfl_xor(s, off, 64);
+    ms_merge(m, s, m2, s2);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    lm[wave] = m;
+    ls[wave] = s;
+  }
+  __syncthreads();
+  m = lm[0];
+  s = ls[0];
+  for (int w = 1; w < kCeWaves; ++w) ms_merge(m, s, lm[w], ls[w]);
+  __syncthreads();
+}
+
+// logits: rows x vocab bf16 (row-major, row stride ld elements), overwritten with
+// grad_logits. labels: int64 per row. row_loss: fp32 per row (0 for ignored rows).
+template <bool kInRegs>
+__global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restrict__ logits,
+                                                             int64_t ld,
+                                                             const int64_t* __restrict__ labels,
+                                                             int64_t vocab, int64_t ignore_index,
+                                                             float* __restrict__ row_loss) {
+  const int64_t r = blockIdx.x;
+  uint16_t* row = logits + r * ld;
+  const int64_t label = labels[r];
+  const bool valid = label != ignore_index;
+  const int64_t nvec = vocab >> 3;  // full 8-element vectors (16 B)
+  const bool vec = ((reinterpret_cast<uint64_t>(row) & 15u) == 0);
+  const int64_t vend = vec ? nvec * 8 : 0;
+
+  float m = -INFINITY, s = 0.0f;
+  auto add8 = [&](const u32x4 w) {
+    ms_add(m, s, lo16(w.x)); ms_add(m, s, hi16(w.x));
+    ms_add(m, s, lo16(w.y)); ms_add(m, s, hi16(w.y));
+    ms_add(m, s, lo16(w.z)); ms_add(m, s, hi16(w.z));
+    ms_add(m, s, lo16(w.w)); ms_add(m, s, hi16(w.w));
+  };
+  u32x4 keep[kInRegs ? kRegCols : 1];
+  if (vec) {
+    if constexpr (kInRegs) {
+      // fully unrolled with compile-time indices so that `keep` stays in VGPRs
+#pragma unroll
+      for (int k = 0; k < kRegCols; ++k) {
+        const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
+        if (v < nvec) {
+          keep[k] = *reinterpret_cast<const u32x4*>(row + v * 8);
+          add8(keep[k]);
+        }
+      }
+    } else {
+      for (int64_t v = threadIdx.x; v < nvec; v += kCeThreads)
+        add8(*reinterpret_cast<const u32x4*>(row + v * 8));
+    }
+  }
+  for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
+    ms_add(m, s, __uint_as_float(static_cast<uint32_t>(row[i]) << 16));
+  block_ms(m, s);
+  const float lse = m + logf(s);
+
+  // every thread has the same lse; the target logit is read before any write
+  const float target = (valid && label >= 0 && label < vocab)
+                           ? __uint_as_float(static_cast<uint32_t>(row[label]) << 16)
+                           : 0.0f;
+  __syncthreads();
+  if (threadIdx.x == 0) row_loss[r] = valid ? (lse - target) : 0.0f;
+
+  // grad = exp(x - lse) on valid rows (0 on ignored rows), minus 1 at the label
+  auto g_of = [&](float x, int64_t idx) -> float {
+    if (!valid) return 0.0f;
+    float p = expf(x - lse);
+    if (idx == label) p = p - 1.0f;
+    return p;
+  };
+  auto put8 = [&](const u32x4 w, int64_t v) {
+    const int64_t b = v * 8;
+    u32x4 o;
+    o.x = rne16(g_of(lo16(w.x), b + 0)) | (rne16(g_of(hi16(w.x), b + 1)) << 16);
+    o.y = rne16(g_of(lo16(w.y), b + 2)) | (rne16(g_of(hi16(w.y), b + 3)) << 16);
+    o.z = rne16(g_of(lo16(w.z), b + 4)) | (rne16(g_of(hi16(w.z), b + 5)) << 16);
+    o.w = rne16(g_of(lo16(w.w), b + 6)) | (rne16(g_of(hi16(w.w), b + 7)) << 16);
+    *reinterpret_cast<u32x4*>(row + b) = o;
+  };
+  if (vec) {
+    if constexpr (kInRegs) {
+#pragma unroll
+      for (int k = 0; k < kRegCols; ++k) {
+        const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
+        if (v < nvec) put8(keep[k], v);
+      }
+    } else {
+      for (int64_t v = threadIdx.x; v < nvec; v += kCeThreads)
+        put8(*reinterpret_cast<const u32x4*>(row + v * 8), v);
+    }
+  }
+  for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
+    row[i] = static_cast<uint16_t>(rne16(g_of(__uint_as_float(static_cast<uint32_t>(row[i]) << 16), i)));
+}
+
+// Fixed-order sums over rows: loss_sum, n_valid (count of label != ignore), mean.
+__global__ __launch_bounds__(256) void ce_loss_kernel(const float* __restrict__ row_loss,
+                                                      const int64_t* __restrict__ labels,
+                                                      int64_t rows, int64_t ignore_index,
+                                                      float* __restrict__ out3) {
+  __shared__ double sl[4];
+  __shared__ long long sn[4];
+  double acc = 0.0;
+  long long cnt = 0;
+  for (int64_t i = threadIdx.x; i < rows; i += 256) {
+    acc += static_cast<double>(row_loss[i]);
+    cnt += labels[i] != ignore_index;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    acc += __shfl_xor(acc, off, 64);
+    cnt += __shfl_xor(cnt, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sl[threadIdx.x >> 6] = acc;
+    sn[threadIdx.x >> 6] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double total = sl[0] + sl[1] + sl[2] + sl[3];
+    long long n = sn[0] + sn[1] + sn[2] + sn[3];
+    const float loss_sum = static_cast<float>(total);
+    const float n_valid = static_cast<float>(n < 1 ? 1 : n);  // clamp_min(1)
+    out3[0] = loss_sum;
+    out3[1] = n_valid;
+    out3[2] = loss_sum / n_valid;
+  }
+}
+
+// Backward scaling, fused_linear_ce.py:117-126: grad_h (bf16) *= bf16(g / n_valid)
+// (the scale is cast to the grad's dtype, then a bf16 multiply), grad_W *= g / n_valid.
+__global__ __launch_bounds__(256) void ce_scale_kernel(uint16_t* __restrict__ gh, int64_t nh,
+                                                       float* __restrict__ gw, int64_t nw,
+                                                       const float* __restrict__ grad_out,
+                                                       const float* __restrict__ n_valid) {
+  const float scale = *grad_out / *n_valid;
+  const float scale_b = __uint_as_float(rne16(scale) << 16);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < nh; i += stride)
+    gh[i] = static_cast<uint16_t>(rne16(__uint_as_float(static_cast<uint32_t>(gh[i]) << 16) * scale_b));
+  if (gw)
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < nw; i += stride)
+      gw[i] = gw[i] * scale;
+}
+
+int ce_check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return ce_fail(TM_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return TM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tm_ce_rows_bf16(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows,
+                    int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream) {
+  if (rows < 0 || vocab <= 0 || ld < vocab)
+    return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: bad sizes rows=%lld vocab=%lld ld=%lld",
+                   (long long)rows, (long long)vocab, (long long)ld);
+  if (rows == 0) return TM_OK;
+  if (!d_logits || !d_labels || !d_row_loss) return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: null pointer");
+  if (rows > 0x7FFFFFFFll) return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: too many rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool regs = (vocab >> 3) <= static_cast<int64_t>(kCeThreads) * kRegCols;
+  if (regs)
+    hipLaunchKernelGGL(ce_rows_kernel<true>, dim3(static_cast<uint32_t>(rows)), dim3(kCeThreads), 0, s,
+                       d_logits, ld, d_labels, vocab, ignore_index, d_row_loss);
+  else
+    hipLaunchKernelGGL(ce_rows_kernel<false>, dim3(static_cast<uint32_t>(rows)), dim3(kCeThreads), 0, s,
+                       d_logits, ld, d_labels, vocab, ignore_index, d_row_loss);
+  return ce_check_launch("ce_rows_kernel");
+}
+
+int tm_ce_loss(const float* d_row_loss, const int64_t* d_labels, int64_t rows, int64_t ignore_index,
+               float* d_out3, void* stream) {
+  if (rows < 0) return ce_fail(TM_EINVAL, "tm_ce_loss: negative rows");
+  if (!d_out3 || (rows > 0 && (!d_row_loss || !d_labels)))
+    return ce_fail(TM_EINVAL, "tm_ce_loss: null pointer");
+  hipLaunchKernelGGL(ce_loss_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     d_row_loss, d_labels, rows, ignore_index, d_out3);
+  return ce_check_launch("ce_loss_kernel");
+}
+
+int tm_ce_scale_grads(uint16_t* d_grad_h, int64_t nh, float* d_grad_w, int64_t nw,
+                      const float* d_grad_out, const float* d_n_valid, void* stream) {
+  if (nh < 0 || nw < 0) return ce_fail(TM_EINVAL, "tm_ce_scale_grads: negative size");
+  if ((nh > 0 && !d_grad_h) || (nw > 0 && !d_grad_w) || !d_grad_out || !d_n_valid)
+    return ce_fail(TM_EINVAL, "tm_ce_scale_grads: null pointer");
+  int64_t n = nh > nw ? nh : nw;
+  int64_t blocks = (n + 256 * 8 - 1) / (256 * 8);
+  if (blocks < 1) blocks = 1;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(ce_scale_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), d_grad_h, nh, nw > 0 ? d_grad_w : nullptr, nw,
+                     d_grad_out, d_n_valid);
+  return ce_check_launch("ce_scale_kernel");
+}
+
+}  // extern "C"

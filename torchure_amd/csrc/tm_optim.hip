@@ -32,8 +32,21 @@
 #include <string.h>
 
 #include "torchure_amd.h"
+#include "tm_internal.h"
 
 #pragma clang fp contract(off)
+
+namespace {
+thread_local char g_err[512] = "";
+}  // namespace
+
+int tm_internal_fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
 
 namespace {
 
@@ -46,14 +59,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-thread_local char g_err[512] = "";
-
-int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
-  va_end(ap);
-  return code;
+template <typename... A>
+int fail(int code, const char* fmt, A... args) {
+  return tm_internal_fail(code, fmt, args...);
 }
 
 int check_launch(const char* what) {

@@ -1,0 +1,111 @@
+"""Chunked fused linear + cross-entropy on gfx950.
+
+Same function, arguments and semantics as torchure/loss/fused_linear_ce.py:130-136:
+``fused_linear_cross_entropy(hidden, weight, labels, ignore_index=-100, chunk_size=...)``
+returns the mean loss over non-ignored tokens (F.cross_entropy(reduction="mean")
+semantics, :22-24), computes grad_hidden and grad_weight during the forward pass
+(:42-58) and scales them in place by grad_out / n_valid in backward (:94-127).
+
+Per chunk of rows:
+  logits = h @ W^T                  bf16 GEMM (hipBLASLt, through torch.matmul)
+  tm_ce_rows_bf16                   one fused kernel: logsumexp, per-row loss and
+                                    grad_logits = bf16(softmax - onehot), in place
+  grad_h = grad_logits @ W          bf16 GEMM
+  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_grad_accumulate_bf16 into fp32
+then tm_ce_loss sums the per-row losses in a fixed order (deterministic).
+
+MI355X sizing: the chunk is chosen so that the bf16 logits of a chunk take up to
+``logits_bytes`` (4 GiB by default) instead of 1024 rows: with 288 GB of HBM the
+whole Qwen3 vocabulary for 8K-16K tokens fits in one chunk, so the fp32 grad_W
+accumulation (a full read+write of V x D fp32 per chunk) runs once or twice
+instead of once per 1024 rows, and the GEMMs get large M.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from torchure_amd import _native
+from torchure_amd.core import tables
+
+DEFAULT_LOGITS_BYTES = 4 << 30
+
+
+def auto_chunk_rows(n_rows: int, vocab: int, logits_bytes: int = DEFAULT_LOGITS_BYTES) -> int:
+    rows = max(256, logits_bytes // (2 * vocab) // 256 * 256)
+    return max(1, min(n_rows, rows))
+
+
+class _FusedLinearCE(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, weight, labels, ignore_index, chunk_size):
+        who = "fused_linear_cross_entropy"
+        for t, what in ((hidden, "hidden"), (weight, "weight"), (labels, "labels")):
+            tables.require_device_tensor(t, who, what)
+        if hidden.dtype != torch.bfloat16:
+            raise NotImplementedError(f"{who}: hidden must be bfloat16 (the autocast activation dtype)")
+        if labels.dtype != torch.int64:
+            raise RuntimeError(f"{who}: labels must be int64")
+        n, d = hidden.shape
+        v = weight.shape[0]
+        if weight.shape[1] != d or labels.shape[0] != n:
+            raise RuntimeError(f"{who}: shapes hidden {tuple(hidden.shape)}, weight {tuple(weight.shape)}, "
+                               f"labels {tuple(labels.shape)} do not match")
+        lib = _native.lib()
+        stream = _native.stream_handle(hidden.device)
+        w = weight.to(hidden.dtype).contiguous()  # cast once, not per chunk
+        chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
+        grad_hidden = torch.empty_like(hidden)
+        grad_weight = torch.zeros_like(weight, dtype=torch.float32) if weight.requires_grad else None
+        row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
+        for s in range(0, n, chunk):
+            e = min(s + chunk, n)
+            h = hidden[s:e]
+            logits = torch.matmul(h, w.t())  # (C, V) bf16
+            _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
+                                              int(ignore_index), row_loss[s:].data_ptr(), stream),
+                          "tm_ce_rows_bf16")
+            torch.matmul(logits, w, out=grad_hidden[s:e])
+            if grad_weight is not None:
+                gw = torch.matmul(logits.t(), h)  # (V, D) bf16
+                _native.check(lib.tm_grad_accumulate_bf16(grad_weight.data_ptr(), gw.data_ptr(),
+                                                          gw.numel(), stream), "tm_grad_accumulate_bf16")
+                del gw
+            del logits
+        out3 = torch.empty(3, dtype=torch.float32, device=hidden.device)
+        _native.check(lib.tm_ce_loss(row_loss.data_ptr(), labels.data_ptr(), n, int(ignore_index),
+                                     out3.data_ptr(), stream), "tm_ce_loss")
+        ctx.n_valid = out3[1:2]
+        ctx.grad_hidden = grad_hidden
+        ctx.grad_weight = grad_weight
+        return out3[2].clone()
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        if ctx.n_valid is None:
+            raise RuntimeError(
+                "fused_linear_cross_entropy: backward called twice. the stashed grads are "
+                "consumed in place on the first call, so retain_graph does not work through this op")
+        grad_hidden, grad_weight, n_valid = ctx.grad_hidden, ctx.grad_weight, ctx.n_valid
+        ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = None
+        g = grad_out.detach().to(torch.float32).contiguous()
+        rc = _native.lib().tm_ce_scale_grads(
+            grad_hidden.data_ptr(), grad_hidden.numel(),
+            grad_weight.data_ptr() if grad_weight is not None else None,
+            grad_weight.numel() if grad_weight is not None else 0,
+            g.data_ptr(), n_valid.data_ptr(), _native.stream_handle(grad_hidden.device))
+        _native.check(rc, "tm_ce_scale_grads")
+        return grad_hidden, grad_weight, None, None, None
+
+
+def fused_linear_cross_entropy(
+    hidden: torch.Tensor,  # (B, S, D) or (N, D), bf16
+    weight: torch.Tensor,  # (V, D) lm_head weight
+    labels: torch.Tensor,  # (B, S) or (N,), already shifted, int64
+    ignore_index: int = -100,
+    chunk_size: int | None = None,
+) -> torch.Tensor:
+    if hidden.dim() == 3:
+        hidden = hidden.reshape(-1, hidden.shape[-1])
+        labels = labels.reshape(-1)
+    return _FusedLinearCE.apply(hidden.contiguous(), weight, labels.contiguous(), ignore_index, chunk_size)
