@@ -47,10 +47,12 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,ragged",
                     help="comma list of extra configs reported under 'extra' (empty = none)")
-    ap.add_argument("--mode", choices=("bench", "kernels"), default="bench",
+    ap.add_argument("--mode", choices=("bench", "kernels", "ce"), default="bench",
                     help="kernels: only the norm and update launches, --reps times each, plus a "
                          "2 GiB device copy for calibrating HBM byte counters (for rocprofv3 --pmc)")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--fused-ce", type=int, default=1,
+                    help="also time the chunked fused linear + CE on the Qwen3-0.6B head (1 = yes)")
     ap.add_argument("--torch-reference", type=int, default=1,
                     help="also time torch-ROCm's own GPU path (foreach clip + fused AdamW) on the "
                          "same config and device (1 = yes)")
@@ -299,6 +301,86 @@ def run_torch_gpu_reference(config: str, steps: int, warmup: int, dev):
                      "AdamW(fused=True), bf16 cast (46 B/param moved)")
 
 
+def _ce_chunk_reference(hidden, weight, labels, ignore_index):
+    """Per-chunk math of the reference's fused linear CE (torchure/loss/fused_linear_ce.py:31-59),
+    the same torch calls; compiled with torch.compile as the reference does."""
+    import torch
+
+    logits = (hidden @ weight.t()).float()
+    valid = labels != ignore_index
+    safe = torch.where(valid, labels, 0).unsqueeze(1)
+    lse = torch.logsumexp(logits, dim=-1)
+    target = logits.gather(1, safe).squeeze(1)
+    loss_sum = ((lse - target) * valid).sum()
+    probs = torch.exp(logits - lse.unsqueeze(1))
+    probs = probs * valid.unsqueeze(1)
+    probs.scatter_add_(1, safe, -valid.float().unsqueeze(1))
+    grad_logits = probs.to(hidden.dtype)
+    return loss_sum, grad_logits @ weight, grad_logits.t() @ hidden
+
+
+def run_fused_ce(reps: int, dev, with_reference: bool = True):
+    """Chunked fused linear + CE on the Qwen3-0.6B head: 8192 tokens (2 x 4096),
+    hidden 1024, vocab 151936 (tied embedding), bf16 activations, fp32 weight,
+    forward + backward. Roofline: the three GEMMs, 6 * N * D * V flops, bf16 MFMA."""
+    import torch
+
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    n, d, v = 8192, 1024, 151936
+    g = torch.Generator(device=dev).manual_seed(0)
+    hidden = torch.randn(n, d, device=dev, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=dev, generator=g) * 0.02
+    labels = torch.randint(0, v, (n,), device=dev, generator=g)
+    labels[::50] = -100
+    flops = 6.0 * n * d * v
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / reps
+
+    def ours():
+        h = hidden.detach().requires_grad_(True)
+        w = weight.detach().requires_grad_(True)
+        fused_linear_cross_entropy(h, w, labels).backward()
+
+    out = {"workload": "qwen3-0.6b lm_head: N 8192, D 1024, V 151936, fwd+bwd",
+           "flops": flops, "ms": round(timed(ours), 4)}
+    out["TFLOPs"] = round(flops / (out["ms"] * 1e-3) / 1e12, 1)
+    out["frac_of_bf16_mfma_peak"] = round(out["TFLOPs"] / 2500.0, 4)
+    if with_reference:
+        comp = torch.compile(_ce_chunk_reference, dynamic=False)
+
+        def ref():
+            w = weight.to(hidden.dtype)
+            loss_sum = torch.zeros((), dtype=torch.float32, device=dev)
+            gh_all = torch.empty_like(hidden)
+            gw_all = torch.zeros_like(weight)
+            for s in range(0, n, 1024):
+                e = min(s + 1024, n)
+                cl, gh, gw = comp(hidden[s:e], w, labels[s:e], -100)
+                loss_sum += cl
+                gh_all[s:e] = gh
+                gw_all += gw
+            nv = (labels != -100).sum().clamp_min(1)
+            gh_all.mul_((1.0 / nv).to(gh_all.dtype))
+            gw_all.mul_(1.0 / nv)
+
+        try:
+            out["reference_compiled_ms"] = round(timed(ref), 4)
+            out["speedup_vs_reference_compiled"] = round(out["reference_compiled_ms"] / out["ms"], 3)
+        except Exception as e:  # torch.compile unavailable: report, do not fail the bench
+            out["reference_compiled_error"] = repr(e)[:200]
+    del hidden, weight, labels
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_cpu_baseline(config: str, blocks: int, steps: int):
     """Reference composition on torch CPU over the first ``blocks`` transformer
     blocks of ``config`` (the sample), bf16 grads widened to fp32."""
@@ -367,6 +449,9 @@ def main():
     if args.mode == "kernels":
         run_kernels_only(args.config, args.reps, args.chunk_elems, dev)
         return
+    if args.mode == "ce":  # fused linear CE only (for rocprofv3)
+        print(json.dumps(run_fused_ce(args.reps, dev, with_reference=False)), flush=True)
+        return
 
     main_res = run_gpu(args.config, args.steps, args.warmup, args.chunk_elems, dev)
     print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
@@ -382,6 +467,11 @@ def main():
         r["frac_of_peak"] = round(r["GBps"] / PEAK_HBM_GBS, 4)
         extra[cfg] = r
         print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
+
+    if args.fused_ce:
+        ce = run_fused_ce(5, dev, with_reference=bool(args.torch_reference))
+        extra["fused_linear_ce_qwen3-0.6b"] = ce
+        print(f"[bench] fused linear CE: {ce}", file=sys.stderr, flush=True)
 
     if args.torch_reference:
         ref = run_torch_gpu_reference(args.config, max(5, min(args.steps, 20)), 2, dev)

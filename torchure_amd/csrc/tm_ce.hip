@@ -6,11 +6,12 @@
 //   grad_h = grad_logits @ W, grad_W += grad_logits^T @ h,
 // and scales both grads by grad_out / n_valid in backward (:94-127).
 // The GEMMs are plain library GEMMs (hipBLASLt). These kernels do the rest:
-//   ce_rows_kernel        one workgroup per row: online max / sum-exp over the bf16
-//                         logits row, target logit, per-row loss, then softmax - onehot
-//                         written back over the logits as bf16 (RNE). A row of up to
-//                         kRegCols vectors per thread stays in registers (one HBM read);
-//                         longer rows are read twice.
+//   ce_rows_kernel        one workgroup per row: row max, sum of exp, target logit,
+//                         per-row loss, then softmax - onehot written back over the
+//                         logits as bf16 (RNE). A row of up to kRegCols vectors per
+//                         thread stays in registers (one HBM read, one write); longer
+//                         rows use an online (max, sum-of-exp) read, then a second
+//                         read for the write pass. exp is the hardware base-2 exp.
 //   ce_loss_kernel        one workgroup: fixed-order sum of the per-row losses and of
 //                         the valid-row count -> loss_sum, n_valid, mean loss.
 //   ce_scale_kernel       backward: grad_h (bf16) *= bf16(g / n_valid),
@@ -30,9 +31,22 @@
 
 namespace {
 
-constexpr int kCeThreads = 1024;  // 16 wave64 per row
-constexpr int kCeWaves = kCeThreads / 64;
+constexpr int kRowThreadsRegs = 1024;  // 16 wave64 per row when the row stays in registers
+#ifndef TM_CE_STREAM_THREADS
+#define TM_CE_STREAM_THREADS 256
+#endif
+#ifndef TM_CE_STREAM_LDS
+#define TM_CE_STREAM_LDS 0
+#endif
+// Streaming path: threads per row, and dynamic LDS per workgroup used only to cap how
+// many rows are in flight per CU (so the second read of a row can hit the MALL).
+constexpr int kRowThreadsStream = TM_CE_STREAM_THREADS;
+constexpr int kStreamLds = TM_CE_STREAM_LDS;
+#ifndef TM_CE_REG_ROWS
+#define TM_CE_REG_ROWS 1
+#endif
 constexpr int kRegCols = 20;  // 8-element vectors per thread kept in registers (V <= 163,840)
+constexpr int kMaxWaves = (kRowThreadsRegs > TM_CE_STREAM_THREADS ? kRowThreadsRegs : TM_CE_STREAM_THREADS) / 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -49,31 +63,39 @@ __device__ __forceinline__ uint32_t rne16(float f) {
   return (f != f) ? 0x7FC0u : r;
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+
+// exp(x - c) through the hardware base-2 exponential: exp2((x - c) * log2(e)).
+__device__ __forceinline__ float exp_shift(float x, float c) { return exp2f((x - c) * kLog2e); }
+
 // (max, sum of exp(x - max)) pairs combine associatively.
 __device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
+  if (m2 == -INFINITY) return;
   if (m2 > m) {
-    s = s * expf(m - m2) + s2;
+    s = s * exp_shift(m, m2) + s2;
     m = m2;
   } else if (m2 == m) {
     s = s + s2;
   } else {
-    s = s + s2 * expf(m2 - m);
+    s = s + s2 * exp_shift(m2, m);
   }
 }
 
 __device__ __forceinline__ void ms_add(float& m, float& s, float x) {
   if (x == -INFINITY) return;  // exp(-inf - m) = 0 contributes nothing
   if (x > m) {
-    s = s * expf(m - x) + 1.0f;
+    s = s * exp_shift(m, x) + 1.0f;
     m = x;
   } else {
-    s = s + expf(x - m);
+    s = s + exp_shift(x, m);
   }
 }
 
 // Block-wide (max, sumexp) in a fixed order; every thread receives the result.
+template <int kCeThreads>
 __device__ __forceinline__ void block_ms(float& m, float& s) {
-  __shared__ float lm[kCeWaves], ls[kCeWaves];
+  constexpr int kCeWaves = kCeThreads / 64;
+  __shared__ float lm[kMaxWaves], ls[kMaxWaves];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float m2 = __shfl_xor(m, off, 64);
@@ -92,9 +114,37 @@ __device__ __forceinline__ void block_ms(float& m, float& s) {
   __syncthreads();
 }
 
+template <int kCeThreads>
+__device__ __forceinline__ float block_max(float m) {
+  constexpr int kCeWaves = kCeThreads / 64;
+  __shared__ float lm[kMaxWaves];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) lm[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = lm[0];
+  for (int w = 1; w < kCeWaves; ++w) m = fmaxf(m, lm[w]);
+  __syncthreads();
+  return m;
+}
+
+template <int kCeThreads>
+__device__ __forceinline__ float block_sum_f(float s) {
+  constexpr int kCeWaves = kCeThreads / 64;
+  __shared__ float ls[kMaxWaves];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if ((threadIdx.x & 63) == 0) ls[threadIdx.x >> 6] = s;
+  __syncthreads();
+  s = ls[0];
+  for (int w = 1; w < kCeWaves; ++w) s += ls[w];
+  __syncthreads();
+  return s;
+}
+
 // logits: rows x vocab bf16 (row-major, row stride ld elements), overwritten with
 // grad_logits. labels: int64 per row. row_loss: fp32 per row (0 for ignored rows).
-template <bool kInRegs>
+template <bool kInRegs, int kCeThreads>
 __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restrict__ logits,
                                                              int64_t ld,
                                                              const int64_t* __restrict__ labels,
@@ -108,34 +158,70 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
   const bool vec = ((reinterpret_cast<uint64_t>(row) & 15u) == 0);
   const int64_t vend = vec ? nvec * 8 : 0;
 
-  float m = -INFINITY, s = 0.0f;
-  auto add8 = [&](const u32x4 w) {
-    ms_add(m, s, lo16(w.x)); ms_add(m, s, hi16(w.x));
-    ms_add(m, s, lo16(w.y)); ms_add(m, s, hi16(w.y));
-    ms_add(m, s, lo16(w.z)); ms_add(m, s, hi16(w.z));
-    ms_add(m, s, lo16(w.w)); ms_add(m, s, hi16(w.w));
-  };
   u32x4 keep[kInRegs ? kRegCols : 1];
-  if (vec) {
-    if constexpr (kInRegs) {
+  float lse;
+  if constexpr (kInRegs) {
+    // The row stays in registers: max pass, then sum-of-exp pass, no second read.
+    float m = -INFINITY;
+    if (vec) {
       // fully unrolled with compile-time indices so that `keep` stays in VGPRs
 #pragma unroll
       for (int k = 0; k < kRegCols; ++k) {
         const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
         if (v < nvec) {
-          keep[k] = *reinterpret_cast<const u32x4*>(row + v * 8);
-          add8(keep[k]);
+          const u32x4 w = *reinterpret_cast<const u32x4*>(row + v * 8);
+          keep[k] = w;
+          m = fmaxf(m, fmaxf(fmaxf(fmaxf(lo16(w.x), hi16(w.x)), fmaxf(lo16(w.y), hi16(w.y))),
+                             fmaxf(fmaxf(lo16(w.z), hi16(w.z)), fmaxf(lo16(w.w), hi16(w.w)))));
         }
       }
-    } else {
-      for (int64_t v = threadIdx.x; v < nvec; v += kCeThreads)
-        add8(*reinterpret_cast<const u32x4*>(row + v * 8));
     }
+    for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
+      m = fmaxf(m, __uint_as_float(static_cast<uint32_t>(row[i]) << 16));
+    m = block_max<kCeThreads>(m);
+    float s = 0.0f;
+    if (vec) {
+#pragma unroll
+      for (int k = 0; k < kRegCols; ++k) {
+        const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
+        if (v < nvec) {
+          const u32x4 w = keep[k];
+          s += exp_shift(lo16(w.x), m) + exp_shift(hi16(w.x), m) + exp_shift(lo16(w.y), m) +
+               exp_shift(hi16(w.y), m) + exp_shift(lo16(w.z), m) + exp_shift(hi16(w.z), m) +
+               exp_shift(lo16(w.w), m) + exp_shift(hi16(w.w), m);
+        }
+      }
+    }
+    for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
+      s += exp_shift(__uint_as_float(static_cast<uint32_t>(row[i]) << 16), m);
+    s = block_sum_f<kCeThreads>(s);
+    lse = m + logf(s);
+  } else {
+    // Row too long for registers: one online (max, sum-of-exp) read, one write pass.
+    float m = -INFINITY, s = 0.0f;
+    if (vec) {
+      // 8 independent (max, sum) pairs per thread (one per vector lane) for ILP
+      float mm[8], ss[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mm[j] = -INFINITY;
+        ss[j] = 0.0f;
+      }
+      for (int64_t v = threadIdx.x; v < nvec; v += kCeThreads) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(row + v * 8);
+        ms_add(mm[0], ss[0], lo16(w.x)); ms_add(mm[1], ss[1], hi16(w.x));
+        ms_add(mm[2], ss[2], lo16(w.y)); ms_add(mm[3], ss[3], hi16(w.y));
+        ms_add(mm[4], ss[4], lo16(w.z)); ms_add(mm[5], ss[5], hi16(w.z));
+        ms_add(mm[6], ss[6], lo16(w.w)); ms_add(mm[7], ss[7], hi16(w.w));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ms_merge(m, s, mm[j], ss[j]);
+    }
+    for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
+      ms_add(m, s, __uint_as_float(static_cast<uint32_t>(row[i]) << 16));
+    block_ms<kCeThreads>(m, s);
+    lse = m + logf(s);
   }
-  for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
-    ms_add(m, s, __uint_as_float(static_cast<uint32_t>(row[i]) << 16));
-  block_ms(m, s);
-  const float lse = m + logf(s);
 
   // every thread has the same lse; the target logit is read before any write
   const float target = (valid && label >= 0 && label < vocab)
@@ -147,7 +233,7 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
   // grad = exp(x - lse) on valid rows (0 on ignored rows), minus 1 at the label
   auto g_of = [&](float x, int64_t idx) -> float {
     if (!valid) return 0.0f;
-    float p = expf(x - lse);
+    float p = exp_shift(x, lse);
     if (idx == label) p = p - 1.0f;
     return p;
   };
@@ -245,13 +331,15 @@ int tm_ce_rows_bf16(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int
   if (!d_logits || !d_labels || !d_row_loss) return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: null pointer");
   if (rows > 0x7FFFFFFFll) return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool regs = (vocab >> 3) <= static_cast<int64_t>(kCeThreads) * kRegCols;
+  const bool regs = TM_CE_REG_ROWS && (vocab >> 3) <= static_cast<int64_t>(kRowThreadsRegs) * kRegCols;
   if (regs)
-    hipLaunchKernelGGL(ce_rows_kernel<true>, dim3(static_cast<uint32_t>(rows)), dim3(kCeThreads), 0, s,
-                       d_logits, ld, d_labels, vocab, ignore_index, d_row_loss);
+    hipLaunchKernelGGL((ce_rows_kernel<true, kRowThreadsRegs>), dim3(static_cast<uint32_t>(rows)),
+                       dim3(kRowThreadsRegs), 0, s, d_logits, ld, d_labels, vocab, ignore_index,
+                       d_row_loss);
   else
-    hipLaunchKernelGGL(ce_rows_kernel<false>, dim3(static_cast<uint32_t>(rows)), dim3(kCeThreads), 0, s,
-                       d_logits, ld, d_labels, vocab, ignore_index, d_row_loss);
+    hipLaunchKernelGGL((ce_rows_kernel<false, kRowThreadsStream>), dim3(static_cast<uint32_t>(rows)),
+                       dim3(kRowThreadsStream), kStreamLds, s, d_logits, ld, d_labels, vocab,
+                       ignore_index, d_row_loss);
   return ce_check_launch("ce_rows_kernel");
 }
 
