@@ -11,7 +11,9 @@
 //                         logits as bf16 (RNE). A row of up to kRegCols vectors per
 //                         thread stays in registers (one HBM read, one write); longer
 //                         rows use an online (max, sum-of-exp) read, then a second
-//                         read for the write pass. exp is the hardware base-2 exp.
+//                         read for the write pass. exp is the hardware base-2 exp
+//                         (full-range exp2f wherever a result would be denormal), and
+//                         the bf16 rounding is the hardware RNE convert.
 //   ce_loss_kernel        one workgroup: fixed-order sum of the per-row losses and of
 //                         the valid-row count -> loss_sum, n_valid, mean loss.
 //   ce_scale_kernel       backward: grad_h (bf16) *= bf16(g / n_valid),
@@ -65,8 +67,21 @@ __device__ __forceinline__ uint32_t rne16(float f) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// exp(x - c) through the hardware base-2 exponential: exp2((x - c) * log2(e)).
+// exp(x - c) through the base-2 exponential: exp2((x - c) * log2(e)), full range
+// (denormal results included).
 __device__ __forceinline__ float exp_shift(float x, float c) { return exp2f((x - c) * kLog2e); }
+
+// The bare v_exp_f32: identical to exp2f for results >= 2^-126, flushes smaller ones.
+__device__ __forceinline__ float exp2_hw(float t) { return __builtin_amdgcn_exp2f(t); }
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 (round to nearest even) in one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2 h = __builtin_convertvector(f32x2{a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
 
 // (max, sum of exp(x - max)) pairs combine associatively.
 __device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
@@ -186,9 +201,11 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
         const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
         if (v < nvec) {
           const u32x4 w = keep[k];
-          s += exp_shift(lo16(w.x), m) + exp_shift(hi16(w.x), m) + exp_shift(lo16(w.y), m) +
-               exp_shift(hi16(w.y), m) + exp_shift(lo16(w.z), m) + exp_shift(hi16(w.z), m) +
-               exp_shift(lo16(w.w), m) + exp_shift(hi16(w.w), m);
+          // terms below 2^-126 (flushed by the bare exp) cannot move a sum that is >= 1
+          s += exp2_hw((lo16(w.x) - m) * kLog2e) + exp2_hw((hi16(w.x) - m) * kLog2e) +
+               exp2_hw((lo16(w.y) - m) * kLog2e) + exp2_hw((hi16(w.y) - m) * kLog2e) +
+               exp2_hw((lo16(w.z) - m) * kLog2e) + exp2_hw((hi16(w.z) - m) * kLog2e) +
+               exp2_hw((lo16(w.w) - m) * kLog2e) + exp2_hw((hi16(w.w) - m) * kLog2e);
         }
       }
     }
@@ -230,20 +247,40 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
   __syncthreads();
   if (threadIdx.x == 0) row_loss[r] = valid ? (lse - target) : 0.0f;
 
-  // grad = exp(x - lse) on valid rows (0 on ignored rows), minus 1 at the label
+  // grad = exp(x - lse) on valid rows (0 on ignored rows), minus 1 at the label.
   auto g_of = [&](float x, int64_t idx) -> float {
     if (!valid) return 0.0f;
     float p = exp_shift(x, lse);
     if (idx == label) p = p - 1.0f;
     return p;
   };
+  const int64_t label_vec = (valid && label >= 0) ? (label >> 3) : -1;
   auto put8 = [&](const u32x4 w, int64_t v) {
     const int64_t b = v * 8;
     u32x4 o;
-    o.x = rne16(g_of(lo16(w.x), b + 0)) | (rne16(g_of(hi16(w.x), b + 1)) << 16);
-    o.y = rne16(g_of(lo16(w.y), b + 2)) | (rne16(g_of(hi16(w.y), b + 3)) << 16);
-    o.z = rne16(g_of(lo16(w.z), b + 4)) | (rne16(g_of(hi16(w.z), b + 5)) << 16);
-    o.w = rne16(g_of(lo16(w.w), b + 6)) | (rne16(g_of(hi16(w.w), b + 7)) << 16);
+    if (!valid) {
+      o = u32x4{0u, 0u, 0u, 0u};
+    } else {
+      float t[8] = {(lo16(w.x) - lse) * kLog2e, (hi16(w.x) - lse) * kLog2e,
+                    (lo16(w.y) - lse) * kLog2e, (hi16(w.y) - lse) * kLog2e,
+                    (lo16(w.z) - lse) * kLog2e, (hi16(w.z) - lse) * kLog2e,
+                    (lo16(w.w) - lse) * kLog2e, (hi16(w.w) - lse) * kLog2e};
+      float p[8];
+      const float tmin = fminf(fminf(fminf(t[0], t[1]), fminf(t[2], t[3])),
+                               fminf(fminf(t[4], t[5]), fminf(t[6], t[7])));
+      if (tmin >= -126.0f) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = exp2_hw(t[j]);
+      } else {  // some result is a denormal: the full-range exp2
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = exp2f(t[j]);
+      }
+      if (v == label_vec) p[label & 7] = p[label & 7] - 1.0f;
+      o.x = pack_bf16x2(p[0], p[1]);
+      o.y = pack_bf16x2(p[2], p[3]);
+      o.z = pack_bf16x2(p[4], p[5]);
+      o.w = pack_bf16x2(p[6], p[7]);
+    }
     *reinterpret_cast<u32x4*>(row + b) = o;
   };
   if (vec) {
