@@ -125,3 +125,23 @@ def test_cosine_is_refused():
 def test_sgd_registry_entry_passes_through():
     opt = build_optimizer(_model(), "sgd", {"lr": 0.1, "weight_decay": 0.0})
     assert isinstance(opt, torch.optim.SGD)
+
+
+def test_fused_linear_ce_fails_loudly_without_gpu():
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    hidden = torch.randn(8, 4).to(torch.bfloat16)
+    weight = torch.randn(16, 4)
+    labels = torch.zeros(8, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        fused_linear_cross_entropy(hidden, weight, labels)
+
+
+def test_fused_linear_ce_chunk_sizing():
+    from torchure_amd.loss.fused_linear_ce import auto_chunk_rows
+
+    # 4 GiB of bf16 logits for the Qwen3 vocabulary: 14,080 rows (a multiple of 256)
+    assert auto_chunk_rows(100000, 151936) == 14080
+    assert auto_chunk_rows(8192, 151936) == 8192  # 8K tokens fit in one chunk
+    assert auto_chunk_rows(10, 151936) == 10
+    assert auto_chunk_rows(100000, 10 ** 9) == 256  # never below 256 rows
