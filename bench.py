@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--cpu-sample-blocks", type=int, default=2,
                     help="transformer blocks of the config timed for the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-steps", type=int, default=3)
-    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,ragged",
+    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,qwen3-4b-dropin,ragged",
                     help="comma list of extra configs reported under 'extra' (empty = none)")
     ap.add_argument("--mode", choices=("bench", "kernels", "ce"), default="bench",
                     help="kernels: only the norm and update launches, --reps times each, plus a "
@@ -193,6 +193,52 @@ def run_gpu(config: str, steps: int, warmup: int, chunk_elems, dev):
     return out
 
 
+def run_gpu_dropin(config: str, steps: int, warmup: int, chunk_elems, dev):
+    """The plain drop-in configuration: fp32 masters with fp32 .grad (what autograd
+    leaves when the model trains on fp32 params under autocast, as the reference's
+    trainer does), no bf16 working copies. One step = clip_grad_norm (norm pass,
+    4 B/param) + AdamW.step() with the clip fused (28 B/param: read g/p/m/v, write
+    p/m/v) = 32 B/param."""
+    import torch
+
+    import torchure_amd as ta
+    from torchure_amd.core import tables
+    from torchure_amd.workloads import shapes_for
+
+    shapes = shapes_for(config)
+    g = torch.Generator(device=dev).manual_seed(2468)
+    params = [torch.nn.Parameter(torch.randn(s, device=dev, generator=g) * 0.02) for s in shapes]
+    for p in params:
+        p.grad = torch.randn(p.shape, device=dev, generator=g) * 1e-3
+    opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
+                             {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True,
+                              "chunk_elems": chunk_elems or tables.DEFAULT_CHUNK_ELEMS})
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=dev)
+        st["exp_avg"] = torch.randn(p.shape, device=dev, generator=g) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, device=dev, generator=g).abs_() * 1e-8
+
+    def one():
+        ta.clip_grad_norm(params, None, 1.0)
+        opt.step()
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    n = sum(p.numel() for p in params)
+    del params, opt
+    torch.cuda.empty_cache()
+    return dict(config=config + "-dropin-fp32grads", n_params=n, ms_per_step=round(ms, 4),
+                bytes_per_param=32, GBps=round(32 * n / (ms * 1e-3) / 1e9, 1),
+                frac_of_peak=round(32 * n / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+
+
 def run_gpu_fp32acc(config: str, steps: int, warmup: int, chunk_elems, dev):
     """Config-3 style step: bf16 micro-grads accumulated into fp32 .grad; the last
     micro-step's accumulation also yields the global norm (fused), clip_grad_norm
@@ -276,29 +322,35 @@ def run_torch_gpu_reference(config: str, steps: int, warmup: int, dev):
     bf16 = [torch.empty(p.shape, dtype=torch.bfloat16, device=dev) for p in params]
     grads = [p.grad for p in params]
 
-    def one():
+    def one(cast=True):
         norms = torch._foreach_norm(grads, 2.0)
         total = torch.linalg.vector_norm(torch.stack(norms), 2.0)
         coef = torch.clamp(1.0 / (total + 1e-6), max=1.0)
         torch._foreach_mul_(grads, coef)
         opt.step()
-        torch._foreach_copy_(bf16, params)
+        if cast:
+            torch._foreach_copy_(bf16, params)
 
-    for _ in range(warmup):
-        one()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        one()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+    def timed(cast):
+        for _ in range(warmup):
+            one(cast)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            one(cast)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    ms = timed(True)
+    ms_nocast = timed(False)
     n = sum(p.numel() for p in params)
     del params, grads, opt, bf16
     torch.cuda.empty_cache()
     return dict(config=config, ms_per_step=round(ms, 4), n_params=n,
                 GBps_on_30B_basis=round(STEP_BYTES_PER_PARAM * n / (ms * 1e-3) / 1e9, 1),
                 path="torch-ROCm: fp32 grads, _foreach_norm clip + _foreach_mul_, "
-                     "AdamW(fused=True), bf16 cast (46 B/param moved)")
+                     "AdamW(fused=True), bf16 cast (46 B/param moved)",
+                ms_per_step_without_bf16_cast=round(ms_nocast, 4))
 
 
 def _ce_chunk_reference(hidden, weight, labels, ignore_index):
@@ -457,6 +509,11 @@ def main():
     print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
     extra = {}
     for cfg in [c for c in args.also.split(",") if c and c != args.config]:
+        if cfg.endswith("-dropin"):
+            r = run_gpu_dropin(cfg[: -len("-dropin")], args.steps, args.warmup, args.chunk_elems, dev)
+            extra[cfg] = r
+            print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
+            continue
         if cfg.endswith("-fp32acc"):
             r = run_gpu_fp32acc(cfg[: -len("-fp32acc")], args.steps, args.warmup, args.chunk_elems, dev)
             extra[cfg] = r
@@ -476,6 +533,11 @@ def main():
     if args.torch_reference:
         ref = run_torch_gpu_reference(args.config, max(5, min(args.steps, 20)), 2, dev)
         ref["speedup_of_this_build"] = round(ref["ms_per_step"] / main_res["ms_per_step"], 3)
+        dropin = extra.get(args.config + "-dropin")
+        if dropin:
+            # same fp32-grad inputs as the reference path, no bf16 working copies
+            ref["speedup_of_dropin_fp32grads"] = round(ref["ms_per_step_without_bf16_cast"] /
+                                                       dropin["ms_per_step"], 3)
         extra["torch_rocm_reference_" + args.config] = ref
         print(f"[bench] torch-ROCm reference: {ref}", file=sys.stderr, flush=True)
 

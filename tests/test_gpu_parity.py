@@ -858,3 +858,126 @@ def test_clip_matches_torch_on_tied_model(max_norm):
     assert len(list(mine.parameters())) == 5  # tied weight counted once
     for (name, p), (_, q) in zip(mine.named_parameters(), ref.named_parameters()):
         torch.testing.assert_close(p.grad, q.grad, rtol=1e-5, atol=1e-7, msg=name)
+
+
+class _MLPBlockLM(torch.nn.Module):
+    """A small pre-norm MLP block with an output head (no embedding, whose backward
+    accumulates with atomics and is not bit-reproducible)."""
+
+    def __init__(self, dim=64, vocab=96):
+        super().__init__()
+        self.norm1 = torch.nn.RMSNorm(dim)
+        self.up = torch.nn.Linear(dim, 4 * dim, bias=True)
+        self.down = torch.nn.Linear(4 * dim, dim, bias=False)
+        self.norm2 = torch.nn.RMSNorm(dim)
+        self.head = torch.nn.Linear(dim, vocab, bias=False)
+
+    def forward(self, x):
+        h = x + self.down(torch.nn.functional.silu(self.up(self.norm1(x))))
+        return self.head(self.norm2(h))
+
+
+def _train_loop(model, batches, opt, sched, clip, max_norm, micro):
+    """torchure/train/trainer.py:370-397 restated: bf16 autocast forward, loss / micro,
+    backward (fp32 .grad accumulates over the micro-batches), clip, step, zero_grad,
+    scheduler step. Returns the per-step losses and pre-clip norms."""
+    losses, norms = [], []
+    for step_batches in batches:
+        loss = torch.zeros((), device=DEV)
+        for x, y in step_batches[:micro]:
+            with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                logits = model(x)
+                part = torch.nn.functional.cross_entropy(logits.float().reshape(-1, logits.shape[-1]),
+                                                         y.reshape(-1)) / micro
+            part.backward()
+            loss += part.detach()
+        norms.append(clip(model, max_norm).detach().clone())
+        opt.step()
+        opt.zero_grad()
+        sched.step()
+        losses.append(loss)
+    return torch.stack(losses), torch.stack(norms)
+
+
+def _run_training(max_norm, steps=6, micro=2, total_steps=6):
+    """Runs the same training twice from the same init and data: once through
+    torchure_amd (clip_grad_norm + AdamW + WSD schedule), once through the
+    reference's torch composition (grad_helper clip, AdamW(fused=True), the WSD
+    multiplier through LambdaLR)."""
+    import torchure_amd as ta
+    from oracle.torch_composition import clip_grad_norm_reference
+
+    g = torch.Generator().manual_seed(99)
+    batches = [[(torch.randn(4, 32, 64, generator=g).to(DEV),
+                 torch.randint(0, 96, (4, 32), generator=g).to(DEV)) for _ in range(micro)]
+               for _ in range(steps)]
+    sched_cfg = {"type": "wsd", "total_steps": total_steps, "warmup_ratio": 0.34, "decay_ratio": 0.34}
+    hyper = {"lr": 2e-3, "betas": (0.9, 0.95), "eps": 1e-8, "weight_decay": 0.1}
+
+    def build():
+        torch.manual_seed(0)
+        return _MLPBlockLM().to(DEV)
+
+    def ours():
+        model = build()
+        opt = ta.build_optimizer(model, "adamw", dict(hyper, fused=True))
+        sched = ta.build_scheduler(opt, sched_cfg)
+        out = _train_loop(model, batches, opt, sched,
+                          lambda m, mn: ta.clip_grad_norm(m.parameters(), None, mn), max_norm, micro)
+        return model, opt, out
+
+    def reference():
+        model = build()
+        params = [p for p in model.parameters() if p.requires_grad]
+        groups = [{"params": [p for p in params if p.dim() >= 2], "weight_decay": hyper["weight_decay"]},
+                  {"params": [p for p in params if p.dim() < 2], "weight_decay": 0.0}]
+        opt = torch.optim.AdamW(groups, lr=hyper["lr"], betas=hyper["betas"], eps=hyper["eps"], fused=True)
+        sched = torch.optim.lr_scheduler.LambdaLR(
+            opt, lambda s: oracle.wsd_scale(s, total_steps, 0.34, 0.34))
+        out = _train_loop(model, batches, opt, sched,
+                          lambda m, mn: clip_grad_norm_reference([p.grad for p in m.parameters()], mn),
+                          max_norm, micro)
+        return model, opt, out
+
+    return ours(), reference(), reference
+
+
+def _assert_reference_reproducible(ref, rerun):
+    m2, _, (l2, _) = rerun()
+    same = torch.equal(ref[2][0], l2) and all(torch.equal(p, q) for p, q in
+                                               zip(ref[0].parameters(), m2.parameters()))
+    if not same:
+        pytest.skip("torch's own training loop is not bit-reproducible on this box")
+
+
+def test_training_loop_no_clip_bit_exact_vs_torch():
+    """Full loop with a max_norm no step reaches (coefficient 1.0): losses, masters,
+    moments and step counters equal torch's fused AdamW loop bit for bit over six
+    steps through the whole WSD curve (warmup, stable, decay)."""
+    (mine, opt, (loss_a, norm_a)), ref, rerun = _run_training(max_norm=1e9)
+    _assert_reference_reproducible(ref, rerun)
+    model_r, opt_r, (loss_b, norm_b) = ref
+    assert torch.equal(loss_a, loss_b)
+    torch.testing.assert_close(norm_a, norm_b, rtol=1e-6, atol=0)
+    assert [gr["lr"] for gr in opt.param_groups] == [gr["lr"] for gr in opt_r.param_groups]
+    for (name, p), q in zip(mine.named_parameters(), model_r.parameters()):
+        assert torch.equal(p, q), name
+        sa, sb = opt.state[p], opt_r.state[q]
+        assert torch.equal(sa["exp_avg"], sb["exp_avg"]), name
+        assert torch.equal(sa["exp_avg_sq"], sb["exp_avg_sq"]), name
+        assert float(sa["step"]) == float(sb["step"]) == 6.0
+        assert p.grad is None
+
+
+def test_training_loop_with_clip_tracks_torch():
+    """Same loop with clipping active on every step. The coefficient comes from this
+    library's fp64-accumulated norm and torch's fp32 one, which may differ in the
+    last bits, so the trajectories are compared within tolerance: norms to 1e-6
+    relative, losses to 1e-5, parameters to rtol 1e-4 / atol 2e-6."""
+    (mine, opt, (loss_a, norm_a)), ref, _ = _run_training(max_norm=0.05)
+    model_r, opt_r, (loss_b, norm_b) = ref
+    assert bool((norm_a > 0.05).all()), norm_a  # every step clipped
+    torch.testing.assert_close(norm_a, norm_b, rtol=1e-6, atol=0)
+    torch.testing.assert_close(loss_a, loss_b, rtol=1e-5, atol=0)
+    for (name, p), q in zip(mine.named_parameters(), model_r.parameters()):
+        torch.testing.assert_close(p, q, rtol=1e-4, atol=2e-6, msg=name)
