@@ -218,6 +218,18 @@ int tm_ce_loss(const float* d_row_loss, const int64_t* d_labels, int64_t rows, i
 int tm_ce_scale_grads(uint16_t* d_grad_h, int64_t nh, float* d_grad_w, int64_t nw,
                       const float* d_grad_out, const float* d_n_valid, void* stream);
 
+/*
+ * grad_W hand-over of one chunk (fused_linear_ce.py:80-81 `grad_weight += gw`, and for the
+ * last chunk also :126 `grad_weight.mul_(scale)`):
+ *   d_grad_w[i] = ((accumulate ? d_grad_w[i] : +0.0f) + float(d_chunk[i])) [* scale]
+ * with scale = *d_grad_out / *d_n_valid when d_grad_out is given (both or neither).
+ * accumulate = 0 replaces the zero fill + first `+=` (no read of d_grad_w); the
+ * scaled form lets the last chunk's bf16 grad_W wait for backward and be folded in
+ * together with the scaling, one pass instead of two.
+ */
+int tm_ce_grad_w(float* d_grad_w, const uint16_t* d_chunk, int64_t nw, int accumulate,
+                 const float* d_grad_out, const float* d_n_valid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -116,3 +116,86 @@ def test_fused_linear_ce_all_ignored_and_double_backward():
     assert torch.count_nonzero(hidden.grad).item() == 0 and torch.count_nonzero(weight.grad).item() == 0
     with pytest.raises(RuntimeError, match="backward called twice"):
         loss.backward()
+
+
+@pytest.mark.parametrize("accumulate,scaled,n,offset", [
+    (0, 0, 4096, 0), (1, 0, 4096, 0), (0, 1, 4096, 0), (1, 1, 4096, 0),
+    (1, 1, 1003, 0), (1, 1, 2050, 1), (0, 1, 777, 3)])
+def test_ce_grad_w_handover_bit_exact(accumulate, scaled, n, offset):
+    """tm_ce_grad_w vs the reference's torch ops on the same data
+    (fused_linear_ce.py:80-81 `grad_weight += gw` on a zero-filled fp32 buffer, :126
+    `grad_weight.mul_(grad_out / n_valid)`), bit for bit, including -0, +-inf, NaN and
+    subnormal bf16 inputs, odd sizes and buffers that are not 16-byte aligned."""
+    from torchure_amd import _native
+
+    r = H.rng(n + 7 * offset + accumulate)
+    chunk_bits = oracle.bf16_rne((r.standard_normal(n + offset) * 0.3).astype(np.float32))
+    chunk_bits[offset:offset + 6] = [0x8000, 0x0000, 0x7F80, 0xFF80, 0x7FC0, 0x0001]
+    chunk = torch.from_numpy(chunk_bits.view(np.int16).copy()).to(DEV)[offset:]
+    acc0 = torch.from_numpy((r.standard_normal(n + offset) * 0.1).astype(np.float32)).to(DEV)[offset:]
+    acc0[0] = acc0[6] = -0.0  # -0 + -0 keeps the sign only when accumulating
+    grad_out = torch.tensor([0.37], dtype=torch.float32, device=DEV)
+    n_valid = torch.tensor([977.0], dtype=torch.float32, device=DEV)
+
+    if accumulate:
+        want = acc0.clone()
+    else:
+        want = torch.zeros(n, dtype=torch.float32, device=DEV)
+    want += chunk.view(torch.bfloat16).float()
+    if scaled:
+        want.mul_(grad_out[0] / n_valid[0])
+
+    got = acc0.clone() if accumulate else torch.full((n,), 123.0, device=DEV)
+    got_base = torch.empty(n + offset, dtype=torch.float32, device=DEV)
+    got_view = got_base[offset:]
+    got_view.copy_(got)
+    rc = _native.lib().tm_ce_grad_w(got_view.data_ptr(), chunk.data_ptr(), n, accumulate,
+                                    grad_out.data_ptr() if scaled else None,
+                                    n_valid.data_ptr() if scaled else None, _native.stream_handle(DEV))
+    _native.check(rc, "tm_ce_grad_w")
+    torch.cuda.synchronize()
+    a = got_view.cpu().numpy().view(np.uint32)
+    b = want.cpu().numpy().view(np.uint32)
+    assert np.array_equal(a, b), np.argwhere(a != b)[:5]
+
+
+def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops():
+    """The deferred last chunk changes nothing: grad_W of the op with three chunks
+    equals, bit for bit, the reference's chunk loop run on the same kernels -- zero
+    buffer, `+=` of each chunk's bf16 grad_W, then `mul_(grad_out / n_valid)`
+    (fused_linear_ce.py:67-91,117-126) -- and grad_h likewise
+    (`grad_hidden[s:e] = gh`, then `mul_(scale.to(bf16))`)."""
+    from torchure_amd import _native
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(11)
+    n, d, v, chunk = 700, 128, 2048, 256
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::13] = -100
+    h1 = hidden.clone().requires_grad_(True)
+    w1 = weight.clone().requires_grad_(True)
+    loss = fused_linear_cross_entropy(h1, w1, labels, -100, chunk)
+    (loss * 3.0).backward()
+
+    lib = _native.lib()
+    stream = _native.stream_handle(DEV)
+    w = weight.to(torch.bfloat16)
+    gw_ref = torch.zeros(v, d, dtype=torch.float32, device=DEV)
+    gh_ref = torch.empty_like(hidden)
+    row_loss = torch.empty(n, dtype=torch.float32, device=DEV)
+    for s in range(0, n, chunk):
+        e = min(s + chunk, n)
+        logits = torch.matmul(hidden[s:e], w.t())
+        _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, -100,
+                                          row_loss[s:].data_ptr(), stream), "tm_ce_rows_bf16")
+        gh_ref[s:e] = torch.matmul(logits, w)
+        gw_ref += torch.matmul(logits.t(), hidden[s:e])
+    n_valid = (labels != -100).sum().clamp_min(1)
+    scale = torch.tensor(3.0, device=DEV) / n_valid
+    gw_ref.mul_(scale)
+    gh_ref.mul_(scale.to(torch.bfloat16))
+    torch.cuda.synchronize()
+    assert torch.equal(w1.grad.view(torch.int32), gw_ref.view(torch.int32))
+    assert torch.equal(h1.grad.view(torch.int16), gh_ref.view(torch.int16))

@@ -349,6 +349,45 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(uint16_t* __restrict__ gh
       gw[i] = gw[i] * scale;
 }
 
+// grad_W hand-over, fused_linear_ce.py:80-81,126: the fp32 accumulator gets one more
+// chunk, acc = acc + float(chunk) (kAccumulate) or acc = 0 + float(chunk) (first chunk:
+// the reference adds into a zero-filled buffer, and +0 + x also maps -0 to +0), then,
+// with kScale (the backward of the last chunk), acc *= g / n_valid. Each element sees
+// the same fp32 operations in the same order as the reference's `+=` then `mul_`.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <bool kAccumulate, bool kScale>
+__global__ __launch_bounds__(256) void ce_grad_w_kernel(float* __restrict__ acc,
+                                                        const uint16_t* __restrict__ chunk, int64_t n,
+                                                        const float* __restrict__ grad_out,
+                                                        const float* __restrict__ n_valid) {
+  const float scale = kScale ? *grad_out / *n_valid : 1.0f;
+  const bool vec = ((reinterpret_cast<uint64_t>(acc) | reinterpret_cast<uint64_t>(chunk)) & 15u) == 0;
+  const int64_t vend = vec ? (n & ~int64_t(7)) : 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * 8;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8; i < vend; i += stride) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(chunk + i);
+    f32x4 a = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 b = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i + 4) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    a.x = a.x + lo16(w.x); a.y = a.y + hi16(w.x);
+    a.z = a.z + lo16(w.y); a.w = a.w + hi16(w.y);
+    b.x = b.x + lo16(w.z); b.y = b.y + hi16(w.z);
+    b.z = b.z + lo16(w.w); b.w = b.w + hi16(w.w);
+    if (kScale) {
+      a.x = a.x * scale; a.y = a.y * scale; a.z = a.z * scale; a.w = a.w * scale;
+      b.x = b.x * scale; b.y = b.y * scale; b.z = b.z * scale; b.w = b.w * scale;
+    }
+    *reinterpret_cast<f32x4*>(acc + i) = a;
+    *reinterpret_cast<f32x4*>(acc + i + 4) = b;
+  }
+  for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    float x = (kAccumulate ? acc[i] : 0.0f) + __uint_as_float(static_cast<uint32_t>(chunk[i]) << 16);
+    if (kScale) x = x * scale;
+    acc[i] = x;
+  }
+}
+
 int ce_check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ce_fail(TM_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -403,6 +442,32 @@ int tm_ce_scale_grads(uint16_t* d_grad_h, int64_t nh, float* d_grad_w, int64_t n
                      static_cast<hipStream_t>(stream), d_grad_h, nh, nw > 0 ? d_grad_w : nullptr, nw,
                      d_grad_out, d_n_valid);
   return ce_check_launch("ce_scale_kernel");
+}
+
+int tm_ce_grad_w(float* d_grad_w, const uint16_t* d_chunk, int64_t nw, int accumulate,
+                 const float* d_grad_out, const float* d_n_valid, void* stream) {
+  if (nw < 0) return ce_fail(TM_EINVAL, "tm_ce_grad_w: negative size");
+  if (nw == 0) return TM_OK;
+  if (!d_grad_w || !d_chunk || (d_grad_out != nullptr) != (d_n_valid != nullptr))
+    return ce_fail(TM_EINVAL, "tm_ce_grad_w: null pointer");
+  int64_t blocks = (nw + 256 * 8 - 1) / (256 * 8);
+  if (blocks > 65536) blocks = 65536;
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool scale = d_grad_out != nullptr;
+  if (accumulate && scale)
+    hipLaunchKernelGGL((ce_grad_w_kernel<true, true>), grid, block, 0, s, d_grad_w, d_chunk, nw,
+                       d_grad_out, d_n_valid);
+  else if (accumulate)
+    hipLaunchKernelGGL((ce_grad_w_kernel<true, false>), grid, block, 0, s, d_grad_w, d_chunk, nw,
+                       d_grad_out, d_n_valid);
+  else if (scale)
+    hipLaunchKernelGGL((ce_grad_w_kernel<false, true>), grid, block, 0, s, d_grad_w, d_chunk, nw,
+                       d_grad_out, d_n_valid);
+  else
+    hipLaunchKernelGGL((ce_grad_w_kernel<false, false>), grid, block, 0, s, d_grad_w, d_chunk, nw,
+                       d_grad_out, d_n_valid);
+  return ce_check_launch("ce_grad_w_kernel");
 }
 
 }  // extern "C"

@@ -11,8 +11,15 @@ Per chunk of rows:
   tm_ce_rows_bf16                   one fused kernel: logsumexp, per-row loss and
                                     grad_logits = bf16(softmax - onehot), in place
   grad_h = grad_logits @ W          bf16 GEMM
-  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_grad_accumulate_bf16 into fp32
+  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_ce_grad_w into fp32
 then tm_ce_loss sums the per-row losses in a fixed order (deterministic).
+
+The last chunk's bf16 grad_W is not added in forward: it waits for backward, where
+tm_ce_grad_w adds it and applies grad_out / n_valid in the same pass. With a single
+chunk (the usual case at 4 GiB of logits) the fp32 grad_W is then written once,
+straight from the bf16 GEMM output (6 B per element), instead of a zero fill, an
+accumulate and a scaling pass (22 B per element); the fp32 additions and the scaling
+are the reference's, in the reference's order, so the bits are unchanged.
 
 MI355X sizing: the chunk is chosen so that the bf16 logits of a chunk take up to
 ``logits_bytes`` (4 GiB by default) instead of 1024 rows: with 288 GB of HBM the
@@ -56,7 +63,12 @@ class _FusedLinearCE(torch.autograd.Function):
         w = weight.to(hidden.dtype).contiguous()  # cast once, not per chunk
         chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
         grad_hidden = torch.empty_like(hidden)
-        grad_weight = torch.zeros_like(weight, dtype=torch.float32) if weight.requires_grad else None
+        want_w = weight.requires_grad
+        # fp32 grad_W holds chunks 0..k-2; chunk k-1 stays bf16 until backward
+        grad_weight = None
+        if want_w and n > chunk:
+            grad_weight = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
+        last_gw, accumulated = None, False
         row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
         for s in range(0, n, chunk):
             e = min(s + chunk, n)
@@ -66,18 +78,26 @@ class _FusedLinearCE(torch.autograd.Function):
                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
                           "tm_ce_rows_bf16")
             torch.matmul(logits, w, out=grad_hidden[s:e])
-            if grad_weight is not None:
+            if want_w:
                 gw = torch.matmul(logits.t(), h)  # (V, D) bf16
-                _native.check(lib.tm_grad_accumulate_bf16(grad_weight.data_ptr(), gw.data_ptr(),
-                                                          gw.numel(), stream), "tm_grad_accumulate_bf16")
-                del gw
+                if e < n:
+                    _native.check(lib.tm_ce_grad_w(grad_weight.data_ptr(), gw.data_ptr(), gw.numel(),
+                                                   int(accumulated), None, None, stream), "tm_ce_grad_w")
+                    accumulated = True
+                    del gw
+                else:
+                    last_gw = gw
             del logits
         out3 = torch.empty(3, dtype=torch.float32, device=hidden.device)
         _native.check(lib.tm_ce_loss(row_loss.data_ptr(), labels.data_ptr(), n, int(ignore_index),
                                      out3.data_ptr(), stream), "tm_ce_loss")
         ctx.n_valid = out3[1:2]
         ctx.grad_hidden = grad_hidden
+        ctx.want_w = want_w
         ctx.grad_weight = grad_weight
+        ctx.last_gw = last_gw
+        ctx.accumulated = accumulated
+        ctx.weight_meta = (weight.shape, weight.device)
         return out3[2].clone()
 
     @staticmethod
@@ -87,13 +107,28 @@ class _FusedLinearCE(torch.autograd.Function):
                 "fused_linear_cross_entropy: backward called twice. the stashed grads are "
                 "consumed in place on the first call, so retain_graph does not work through this op")
         grad_hidden, grad_weight, n_valid = ctx.grad_hidden, ctx.grad_weight, ctx.n_valid
-        ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = None
+        last_gw = ctx.last_gw
+        ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = ctx.last_gw = None
+        lib = _native.lib()
+        stream = _native.stream_handle(grad_hidden.device)
         g = grad_out.detach().to(torch.float32).contiguous()
-        rc = _native.lib().tm_ce_scale_grads(
+        scale_w = None  # an fp32 grad_W that still needs the plain scaling pass
+        if ctx.want_w:
+            shape, device = ctx.weight_meta
+            if last_gw is not None:
+                if grad_weight is None:
+                    grad_weight = torch.empty(shape, dtype=torch.float32, device=device)
+                _native.check(lib.tm_ce_grad_w(grad_weight.data_ptr(), last_gw.data_ptr(), last_gw.numel(),
+                                               int(ctx.accumulated), g.data_ptr(), n_valid.data_ptr(),
+                                               stream), "tm_ce_grad_w")
+                del last_gw
+            else:  # no rows at all: the reference scales its zero-filled buffer
+                grad_weight = scale_w = torch.zeros(shape, dtype=torch.float32, device=device)
+        rc = lib.tm_ce_scale_grads(
             grad_hidden.data_ptr(), grad_hidden.numel(),
-            grad_weight.data_ptr() if grad_weight is not None else None,
-            grad_weight.numel() if grad_weight is not None else 0,
-            g.data_ptr(), n_valid.data_ptr(), _native.stream_handle(grad_hidden.device))
+            scale_w.data_ptr() if scale_w is not None else None,
+            scale_w.numel() if scale_w is not None else 0,
+            g.data_ptr(), n_valid.data_ptr(), stream)
         _native.check(rc, "tm_ce_scale_grads")
         return grad_hidden, grad_weight, None, None, None
 
