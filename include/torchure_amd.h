@@ -87,14 +87,19 @@ typedef struct tm_chunk {
   uint32_t chunk;
 } tm_chunk_t;
 
+/* tm_accum_t.flags */
+#define TM_ACCUM_ASSIGN 1  /* acc = (float)micro, acc is not read (first micro-step) */
+
 /* One tensor of a micro-step accumulation list (32 bytes, device memory):
- * acc (fp32, updated in place) += micro (bf16), numel elements. micro may be 0:
- * the accumulator is then left as is and only enters the norm. */
+ * acc (fp32, updated in place) += micro (bf16), numel elements; with TM_ACCUM_ASSIGN
+ * acc = micro instead, as autograd assigns the first grad (torch's AccumulateGrad
+ * stores the first incoming grad and adds later ones). micro may be 0: the
+ * accumulator is then left as is and only enters the norm. */
 typedef struct tm_accum {
   uint64_t acc;
   uint64_t micro;
   int64_t numel;
-  int64_t reserved;
+  int64_t flags;
 } tm_accum_t;
 
 /* Hyper-parameters of one param group, as torch.optim.AdamW holds them

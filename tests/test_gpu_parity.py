@@ -741,6 +741,116 @@ def test_step_bumps_autograd_versions():
         y.backward()
 
 
+def test_state_storage_swapped_between_steps():
+    """`.data =` on a state tensor or a working copy replaces its storage (the old one is
+    freed) without changing the object; the next step must write the new storage.
+    Checked against an identical optimizer whose tensors were left alone."""
+    host = H.make_host_set([(64, 48), (33,), (8, 8)], seed=41)
+    a_params, a_work, a_opt = H.device_setup(host, DEV)
+    b_params, b_work, b_opt = H.device_setup(host, DEV)
+    a_opt.step()
+    b_opt.step()
+    # the master keeps its storage, so only the new checks can notice each swap
+    st0, st2 = a_opt.state[a_params[0]], a_opt.state[a_params[2]]
+    for k in ("exp_avg", "exp_avg_sq", "step"):
+        st0[k].data = st0[k].data.clone()
+    a_work[1].data = a_work[1].data.clone()
+    st2["exp_avg_sq"].data = st2["exp_avg_sq"].data.clone()
+    torch.cuda.synchronize()
+    a_opt.step()
+    b_opt.step()
+    torch.cuda.synchronize()
+    for (p, w), (q, u) in zip(zip(a_params, a_work), zip(b_params, b_work)):
+        assert torch.equal(p, q) and torch.equal(w, u)
+        for k in ("exp_avg", "exp_avg_sq", "step"):
+            assert torch.equal(a_opt.state[p][k], b_opt.state[q][k]), k
+
+
+def _clip_setup(defer):
+    import torchure_amd as ta
+
+    host = H.make_host_set([(64, 48), (33,), (8, 8)], seed=43)
+    params, work, opt = H.device_setup(host, DEV, grad_on_master=True)
+    opt.defer_clip = defer
+    norm = ta.clip_grad_norm(params, None, 0.01)  # clips
+    return params, opt, norm
+
+
+def test_deferred_clip_rejects_grads_modified_in_place():
+    """The reference scales at clip time; a grad changed in place before the step cannot
+    be reproduced by scaling later, so the deferred path raises instead of diverging."""
+    params, opt, _ = _clip_setup(True)
+    params[1].grad.add_(1.0)
+    with pytest.raises(RuntimeError, match="modified in place"):
+        opt.step()
+    params, opt, _ = _clip_setup(True)
+    params[0].grad.mul_(2.0)
+    with pytest.raises(RuntimeError, match="modified in place"):
+        opt.materialize_clip()
+
+
+def test_deferred_clip_with_replaced_grad_matches_eager():
+    """A grad replaced by a new tensor after the clip steps unscaled (the reference
+    scaled the old tensor); the others step clipped. Bit-exact against the eager path."""
+    runs = []
+    for defer in (True, False):
+        params, opt, norm = _clip_setup(defer)
+        g = torch.Generator(device=DEV).manual_seed(5)
+        params[2].grad = torch.randn(params[2].shape, device=DEV, generator=g)
+        opt.step()
+        torch.cuda.synchronize()
+        runs.append(([p.detach().clone() for p in params],
+                     [opt.state[p]["exp_avg"].clone() for p in params], norm.clone()))
+    (pa, ma, na), (pb, mb, nb) = runs
+    assert torch.equal(na, nb)
+    for x, y in zip(pa + ma, pb + mb):
+        assert torch.equal(x, y)
+
+
+def test_accumulated_grads_equal_autograd_under_autocast():
+    """Micro-step accumulation against torch's own autograd, bit for bit. Reference:
+    fp32 params under bf16 autocast (torchure/train/trainer.py:372-390): autocast casts
+    each weight to bf16 (RNE), the cast's backward widens the bf16 grad, the first
+    backward assigns p.grad and later ones add to it. This build: bf16 working copies
+    (RNE of the masters), bf16 grads on them, accumulate_grads_ after each backward.
+    Then the assignment itself on special values: a first micro-grad of -0 stays -0
+    (0 + -0 would give +0), NaN and infinities widen unchanged."""
+    import torchure_amd as ta
+    from torchure_amd.optimizer.working import accumulate_grads_
+
+    torch.manual_seed(3)
+    shapes = [(96, 64), (64, 96), (40, 64)]
+    ref = [torch.nn.Parameter(torch.randn(s, device=DEV) * 0.05) for s in shapes]
+    mine = [torch.nn.Parameter(p.detach().clone()) for p in ref]
+    work = ta.attach_bf16_working_params(mine)
+    micro = 3
+    g = torch.Generator(device=DEV).manual_seed(8)
+    xs = [torch.randn(32, 64, device=DEV, generator=g) for _ in range(micro)]
+
+    def forward(ws, x):
+        h = torch.nn.functional.silu(torch.nn.functional.linear(x, ws[0]))
+        h = torch.nn.functional.linear(h, ws[1])
+        return torch.nn.functional.linear(h, ws[2]).float().square().mean() / micro
+
+    for x in xs:
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            forward(ref, x).backward()
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            forward(work, x.to(torch.bfloat16)).backward()
+        accumulate_grads_(mine)
+    torch.cuda.synchronize()
+    for a, b in zip(mine, ref):
+        assert torch.equal(a.grad.view(torch.int32), b.grad.view(torch.int32))
+
+    bits = np.array([0x8000, 0x0000, 0x7FC0, 0x7F80, 0xFF80, 0x3FC0, 0x0001] * 5, dtype=np.uint16)
+    q = torch.nn.Parameter(torch.zeros(bits.size, device=DEV))
+    (w,) = ta.attach_bf16_working_params([q])
+    w.grad = torch.from_numpy(bits.view(np.int16).copy()).to(DEV).view(torch.bfloat16)
+    accumulate_grads_([q])
+    got = q.grad.view(torch.int32).cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, bits.astype(np.uint32) << 16)
+
+
 def test_full_size_config3_fp32_accumulation():
     """Config 3 at full size (Qwen3-0.6B shapes, 596M params): four bf16 micro-steps
     accumulated into fp32 .grad (the last one also measuring the norm), grads scaled

@@ -48,7 +48,8 @@ TENSOR_DTYPE = np.dtype(
 assert TENSOR_DTYPE.itemsize == 64
 
 # tm_accum_t, 32 bytes.
-ACCUM_DTYPE = np.dtype([("acc", "<u8"), ("micro", "<u8"), ("numel", "<i8"), ("reserved", "<i8")])
+ACCUM_DTYPE = np.dtype([("acc", "<u8"), ("micro", "<u8"), ("numel", "<i8"), ("flags", "<i8")])
+TM_ACCUM_ASSIGN = 1
 assert ACCUM_DTYPE.itemsize == 32
 
 # tm_chunk_t, 8 bytes.

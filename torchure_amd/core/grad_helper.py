@@ -18,7 +18,10 @@ that optimizer, whose next ``step()`` multiplies each grad by it inside the
 fused update kernel (the same single fp32 multiply, so the update is bitwise
 the same). Until that step, ``p.grad`` holds the unscaled values;
 ``AdamW.materialize_clip()`` applies the pending scale in place if a caller
-needs the clipped grads before stepping. In every other case (plain tensors,
+needs the clipped grads before stepping. A grad modified in place between the
+clip and the step makes the step raise (scaling it afterwards would not give
+the reference's scale-then-modify result); a grad replaced by a new tensor
+steps unscaled, as it does in the reference. In every other case (plain tensors,
 params of several optimizers, or ``defer_clip=False``) the grads are scaled in
 place immediately by the scale kernel, as the reference does.
 """
@@ -172,7 +175,7 @@ def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
 
     opt = next(iter(owners)) if len(owners) == 1 else None
     if opt is not None and opt.defer_clip:
-        opt._set_pending_clip(coef, holders)
+        opt._set_pending_clip(coef, holders, grads)
     else:
         scale_grads_(grads, coef)
     return norm

@@ -89,10 +89,16 @@ class ChunkTableCache:
         self._d: OrderedDict = OrderedDict()
 
     def get(self, numels: tuple[int, ...], chunk_elems: int, device: torch.device):
+        """The table for these sizes, for a launch on the device's current stream.
+
+        A cached table may be read on a stream other than the one it was allocated
+        on; record_stream keeps the caching allocator from reusing its block before
+        that stream's work has run, should the table be evicted and freed."""
         key = (numels, chunk_elems, str(device))
         hit = self._d.get(key)
         if hit is not None:
             self._d.move_to_end(key)
+            hit[0].record_stream(torch.cuda.current_stream(device))
             return hit
         table = _native.fill_chunks(np.asarray(numels, dtype=np.int64), chunk_elems)
         dev = upload(table, device) if len(table) else torch.empty(8, dtype=torch.uint8, device=device)

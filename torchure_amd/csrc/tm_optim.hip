@@ -238,6 +238,24 @@ struct AccumBf16 {
   }
 };
 
+// acc (fp32) = micro (bf16) widened, stored without reading acc: the first micro-step,
+// where autograd assigns the grad rather than adding it (so -0 stays -0).
+struct AssignBf16 {
+  float* acc;
+  const uint16_t* micro;
+  __device__ __forceinline__ f32x4 group(int64_t e) const {
+    const u32x2 w = ld<true>(reinterpret_cast<const u32x2*>(micro + e));
+    const f32x4 a = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+    st<true>(reinterpret_cast<f32x4*>(acc + e), a);
+    return a;
+  }
+  __device__ __forceinline__ float one(int64_t i) const {
+    const float a = bf16_at(micro, i);
+    acc[i] = a;
+    return a;
+  }
+};
+
 // ------------------------------------------------------------------- norm pass 1
 
 __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
@@ -564,9 +582,10 @@ __global__ __launch_bounds__(kThreads) void accumulate_list_kernel(
     const int64_t end = min(start + chunk_elems, d.numel);
     if (d.micro) {
       const bool vec = aligned16(d.acc) && aligned8(d.micro);
-      acc += sumsq_range_f32(AccumBf16{reinterpret_cast<float*>(d.acc),
-                                       reinterpret_cast<const uint16_t*>(d.micro)},
-                             start, end, vec);
+      float* a = reinterpret_cast<float*>(d.acc);
+      const uint16_t* m = reinterpret_cast<const uint16_t*>(d.micro);
+      acc += (d.flags & TM_ACCUM_ASSIGN) ? sumsq_range_f32(AssignBf16{a, m}, start, end, vec)
+                                         : sumsq_range_f32(AccumBf16{a, m}, start, end, vec);
     } else if (kNorm) {  // no micro-grad this step: the accumulator only enters the norm
       acc += sumsq_range_f32(ReadF32{reinterpret_cast<const float*>(d.acc)}, start, end,
                              aligned16(d.acc));

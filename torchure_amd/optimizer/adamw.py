@@ -118,7 +118,7 @@ class AdamW(torch.optim.Optimizer):
         }
         self.chunk_elems = tables.check_chunk_elems(chunk_elems)
         self.defer_clip = bool(defer_clip)
-        self._pending = None  # (coef device tensor, set of ids of params it applies to)
+        self._pending = None  # (coef device tensor, {id(param): (grad, grad._version)})
         self._uploader = tables.TableUploader()
         self._verified: dict = {}  # id(param) -> _ParamEntry
         super().__init__(params, defaults)
@@ -145,19 +145,33 @@ class AdamW(torch.optim.Optimizer):
 
     # ------------------------------------------------------------ deferred clip
 
-    def _set_pending_clip(self, coef: torch.Tensor, params) -> None:
-        self._pending = (coef, {id(p) for p in params})
+    def _set_pending_clip(self, coef: torch.Tensor, params, grads) -> None:
+        """Defer ``grads *= coef`` into the next step. Each grad is recorded with its
+        autograd version: the reference scales at clip time, so a grad modified in
+        place before the step cannot be reproduced by scaling later (the step raises),
+        while a grad replaced by a new tensor simply steps unscaled, as it would there."""
+        self._pending = (coef, {id(p): (g, g._version) for p, g in zip(params, grads)})
+
+    @staticmethod
+    def _modified_error() -> RuntimeError:
+        return RuntimeError(
+            "torchure_amd.AdamW: a grad was modified in place after clip_grad_norm deferred its "
+            "scaling into this optimizer; call optimizer.materialize_clip() before changing grads "
+            "between clip_grad_norm and step(), or build the optimizer with defer_clip=False")
 
     def materialize_clip(self) -> None:
-        """Apply a pending clip coefficient to the grads in place and drop it."""
+        """Apply a pending clip coefficient to the grads it measured, in place, and drop it."""
         if self._pending is None:
             return
-        coef, ids = self._pending
+        coef, recs = self._pending
         self._pending = None
-        from torchure_amd.core.grad_helper import grads_of, scale_grads_
+        from torchure_amd.core.grad_helper import scale_grads_
 
-        held = [p for g in self.param_groups for p in g["params"] if id(p) in ids]
-        grads, _ = grads_of(held)
+        grads = []
+        for g, ver in recs.values():
+            if g._version != ver:
+                raise self._modified_error()
+            grads.append(g)
         scale_grads_(grads, coef)
 
     # ------------------------------------------------------------ step
@@ -181,7 +195,11 @@ class AdamW(torch.optim.Optimizer):
         """Collect the params with grads (creating their state lazily) and return
         the native launches of one step without running them. ``step()`` runs
         them once; calling a launch again applies one more step to the same
-        tensors and grads (bench.py uses this to time the kernels back to back)."""
+        tensors and grads (bench.py uses this to time the kernels back to back).
+
+        ``clip_ids`` names the params whose grads are multiplied by ``coef``: a set of
+        ids, or the {id: (grad, version)} record of a deferred clip, which is checked."""
+        checked = isinstance(clip_ids, dict)
         per_dev: dict = {}
         hyper = []
         state_map = self.state
@@ -208,9 +226,14 @@ class AdamW(torch.optim.Optimizer):
                         continue
                 state = state_map[p]
                 ent = verified.get(id(p))
+                # same objects and same storage: a `.data =` swap on any of them (which
+                # frees the old storage) must not leave a stale pointer in the table
                 if (ent is None or ent.param is not p or ent.work is not work
                         or state.get("step") is not ent.step or state.get("exp_avg") is not ent.m
-                        or state.get("exp_avg_sq") is not ent.v or p.data_ptr() != ent.p_ptr):
+                        or state.get("exp_avg_sq") is not ent.v or p.data_ptr() != ent.p_ptr
+                        or ent.m.data_ptr() != ent.m_ptr or ent.v.data_ptr() != ent.v_ptr
+                        or ent.step.data_ptr() != ent.s_ptr
+                        or (work is not None and work.data_ptr() != ent.w_ptr)):
                     ent = self._verify_param(p, state, work)
                     verified[id(p)] = ent
                 gdt = g.dtype
@@ -224,7 +247,15 @@ class AdamW(torch.optim.Optimizer):
                         or not g.is_contiguous() or g.is_sparse):
                     self._check_param(p, g, work)  # raises with a precise message
                 if id(p) in clip_ids:
-                    flags |= clip_flag
+                    if not checked:
+                        flags |= clip_flag
+                    else:
+                        rec_g, rec_v = clip_ids[id(p)]
+                        if rec_g is g:
+                            if g._version != rec_v:
+                                raise self._modified_error()
+                            flags |= clip_flag
+                        # else: grad replaced since the clip; it steps unscaled
                 bucket = per_dev.get(ent.device)
                 if bucket is None:
                     bucket = per_dev[ent.device] = ([], [])

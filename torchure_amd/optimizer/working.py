@@ -109,10 +109,12 @@ def accumulate_grads_(params, *, last: bool = False,
                       chunk_elems: int = tables.DEFAULT_CHUNK_ELEMS) -> torch.Tensor | None:
     """One micro-step of gradient accumulation for fp32 masters with bf16 working copies.
 
-    For every param whose working copy carries a bf16 grad: ``p.grad`` (fp32, created
-    as zeros on first use) += that grad, in one launch over the whole list; the bf16
-    grad is then released. This is the fp32 ``.grad`` accumulation autograd performs
-    across micro-batches in torchure/train/trainer.py:383-390.
+    For every param whose working copy carries a bf16 grad: ``p.grad`` (fp32) += that
+    grad, in one launch over the whole list; the bf16 grad is then released. A param
+    without ``p.grad`` gets one holding the widened grad itself (assigned, not added to
+    zeros, as autograd's first backward assigns the grad). This is the fp32 ``.grad``
+    accumulation autograd performs across micro-batches in
+    torchure/train/trainer.py:383-390.
 
     With ``last=True`` the same pass also computes the global L2 norm of the
     accumulated fp32 grads of all ``params`` (returned as a 0-d fp32 device tensor).
@@ -121,15 +123,16 @@ def accumulate_grads_(params, *, last: bool = False,
     """
     who = "accumulate_grads_"
     params = list(params)
-    accs, micros = [], []
+    accs, micros, assign = [], [], []
     for p in params:
         w = getattr(p, "_tm_working", None)
         mg = w.grad if w is not None else None
         if mg is None and (not last or p.grad is None):
             continue
         tables.require_device_tensor(p, who, "param")
-        if p.grad is None:
-            p.grad = torch.zeros_like(p, memory_format=torch.contiguous_format)
+        fresh = p.grad is None
+        if fresh:  # the kernel assigns the first micro-grad: no zero fill, no read
+            p.grad = torch.empty_like(p, memory_format=torch.contiguous_format)
         g = p.grad
         tables.require_device_tensor(g, who, "fp32 accumulator")
         if g.dtype != torch.float32:
@@ -140,6 +143,7 @@ def accumulate_grads_(params, *, last: bool = False,
                 raise RuntimeError(f"{who}: micro-step grad must be bf16 of the param's size and device")
         accs.append(g)
         micros.append(mg)
+        assign.append(fresh)
     if not accs:
         if last:
             raise AssertionError(f"{who}: no grads to accumulate or measure")
@@ -152,6 +156,7 @@ def accumulate_grads_(params, *, last: bool = False,
     rows["acc"] = np.asarray([a.data_ptr() for a in accs], dtype=np.uint64)
     rows["micro"] = np.asarray([m.data_ptr() if m is not None else 0 for m in micros], dtype=np.uint64)
     rows["numel"] = np.asarray([a.numel() for a in accs], dtype=np.int64)
+    rows["flags"] = np.asarray(assign, dtype=np.int64) * _native.TM_ACCUM_ASSIGN
     chunk_elems = tables.check_chunk_elems(chunk_elems)
     chunks, n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]), chunk_elems, device)
     d_rows = _ACC_UPLOAD(rows, device)
