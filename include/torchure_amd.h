@@ -67,6 +67,10 @@ extern "C" {
  *   group       index into the tm_hyper_t array of the call
  *   flags       TM_GRAD_* | TM_FLAG_CLIP
  * The norm / scale / accumulate entry points read only grad, numel and flags.
+ * Preconditions (the records live in device memory, so the library cannot check them
+ * without a synchronisation): step is non-null; master, exp_avg, exp_avg_sq and grad are
+ * non-null when numel > 0 and hold numel elements; tensors do not overlap. A group index
+ * outside [0, n_groups) is read as group 0.
  */
 typedef struct tm_tensor {
   uint64_t master;
