@@ -9,6 +9,8 @@ exactness separately where it is the stronger claim.
 
 from __future__ import annotations
 
+import copy
+
 import numpy as np
 import pytest
 import torch
@@ -849,6 +851,40 @@ def test_accumulated_grads_equal_autograd_under_autocast():
     accumulate_grads_([q])
     got = q.grad.view(torch.int32).cpu().numpy().view(np.uint32)
     assert np.array_equal(got, bits.astype(np.uint32) << 16)
+
+
+def test_stale_working_copy_detected_and_refreshed():
+    """Masters changed outside the step (a resume via model.load_state_dict) leave the
+    bf16 working copies stale: the step raises instead of training on a forward that used
+    old weights; refresh_bf16_working_params rewrites them as RNE(master) and the step
+    then matches an optimizer built fresh on the new masters."""
+    import torchure_amd as ta
+
+    host = H.make_host_set([(64, 48), (33,)], seed=44)
+    params, work, opt = H.device_setup(host, DEV)
+    opt.step()
+    new = [torch.randn(p.shape, device=DEV) * 0.02 for p in params]
+    model = torch.nn.ParameterList(params)
+    model.load_state_dict({str(i): t for i, t in enumerate(new)})
+    grads = [w.grad.clone() for w in work]
+    with pytest.raises(RuntimeError, match="stale"):
+        opt.step()
+    ta.refresh_bf16_working_params(params)
+    for p, w in zip(params, work):
+        assert torch.equal(w, p.detach().to(torch.bfloat16))
+    ref_params, ref_work, ref_opt = H.device_setup(host, DEV)
+    # deep copy: load_state_dict keeps device tensors as they are, which would alias the state
+    ref_opt.load_state_dict(copy.deepcopy(opt.state_dict()))
+    for p, q, w, g in zip(ref_params, new, ref_work, grads):
+        with torch.no_grad():
+            p.copy_(q)
+        w.grad = g
+    ta.refresh_bf16_working_params(ref_params)
+    opt.step()
+    ref_opt.step()
+    torch.cuda.synchronize()
+    for p, q, w, u in zip(params, ref_params, work, ref_work):
+        assert torch.equal(p, q) and torch.equal(w, u)
 
 
 def test_full_size_config3_fp32_accumulation():

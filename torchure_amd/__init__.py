@@ -13,6 +13,7 @@ from torchure_amd.optimizer import (
     attach_bf16_working_params,
     build_optimizer,
     build_scheduler,
+    refresh_bf16_working_params,
 )
 
 __all__ = [
@@ -23,4 +24,5 @@ __all__ = [
     "attach_bf16_working_params",
     "build_optimizer",
     "build_scheduler",
+    "refresh_bf16_working_params",
 ]

@@ -11,7 +11,12 @@ from torchure_amd.optimizer.scheduler import (
     WarmupStableDecaySchedulder,
     wsd_scale,
 )
-from torchure_amd.optimizer.working import accumulate_grad_, accumulate_grads_, attach_bf16_working_params
+from torchure_amd.optimizer.working import (
+    accumulate_grad_,
+    accumulate_grads_,
+    attach_bf16_working_params,
+    refresh_bf16_working_params,
+)
 
 __all__ = [
     "AdamW",
@@ -26,4 +31,5 @@ __all__ = [
     "accumulate_grad_",
     "accumulate_grads_",
     "attach_bf16_working_params",
+    "refresh_bf16_working_params",
 ]

@@ -256,12 +256,20 @@ class AdamW(torch.optim.Optimizer):
                                 raise self._modified_error()
                             flags |= clip_flag
                         # else: grad replaced since the clip; it steps unscaled
+                if work is not None and getattr(work, "_tm_master_version", None) != p._version:
+                    raise RuntimeError(
+                        "torchure_amd.AdamW: a fp32 master was modified in place since its bf16 "
+                        "working copy was last written, so the forward ran on stale weights; call "
+                        "torchure_amd.refresh_bf16_working_params(params) after changing masters "
+                        "(e.g. after model.load_state_dict)")
                 bucket = per_dev.get(ent.device)
                 if bucket is None:
-                    bucket = per_dev[ent.device] = ([], [])
+                    bucket = per_dev[ent.device] = ([], [], [])
                 bucket[0].append((ent.p_ptr, ent.m_ptr, ent.v_ptr, g.data_ptr(), ent.w_ptr, ent.s_ptr,
                                   ent.numel, gi, flags))
                 bucket[1].extend(ent.written)
+                if work is not None:
+                    bucket[2].append((p, work))
 
         if not per_dev:
             return []
@@ -302,14 +310,14 @@ class AdamW(torch.optim.Optimizer):
     def _plan_launches(self, per_dev, hyper, coef) -> list["StepLaunch"]:
         groups_c = _native.hyper_array(hyper)
         out = []
-        for device, (recs, written) in per_dev.items():
+        for device, (recs, written, pairs) in per_dev.items():
             n = len(recs)
             rows = np.array(recs, dtype=_native.TENSOR_DTYPE)
             if coef is not None and coef.device != device:
                 raise RuntimeError("torchure_amd.AdamW: clip coefficient on another device")
             chunks, n_chunks = tables.CHUNKS.get(tuple(r[6] for r in recs), self.chunk_elems, device)
             out.append(StepLaunch(device, self._uploader(rows, device), n, chunks, n_chunks,
-                                  self.chunk_elems, groups_c, len(hyper), coef, written))
+                                  self.chunk_elems, groups_c, len(hyper), coef, written, pairs))
         return out
 
     @staticmethod
@@ -372,8 +380,9 @@ class StepLaunch:
     """
 
     def __init__(self, device, d_rows, n, chunks, n_chunks, chunk_elems, groups_c, n_groups, coef,
-                 written=()):
+                 written=(), pairs=()):
         self.written = list(written)
+        self.pairs = list(pairs)  # (master, bf16 working copy) written by the launch
         self.device = device
         self.d_rows = d_rows
         self.n = n
@@ -401,6 +410,8 @@ class StepLaunch:
         _native.check(rc, "tm_adamw_step")
         if self.written:
             torch.autograd.graph.increment_version(self.written)
+        for p, w in self.pairs:
+            w._tm_master_version = p._version
 
 
 def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out: bool = True) -> int:

@@ -49,8 +49,38 @@ def attach_bf16_working_params(params) -> list[torch.Tensor]:
         _native.check(lib.tm_cast_bf16(w.data_ptr(), p.data_ptr(), p.numel(), stream), "tm_cast_bf16")
         w = w.detach().requires_grad_(p.requires_grad)
         p._tm_working = w
+        mark_current(p, w)
         out.append(w)
     return out
+
+
+def mark_current(p: torch.Tensor, w: torch.Tensor) -> None:
+    """Record that ``w`` holds RNE(``p``) as of ``p``'s current autograd version."""
+    w._tm_master_version = p._version
+
+
+def is_current(p: torch.Tensor, w: torch.Tensor) -> bool:
+    """True if ``p`` has not been modified in place since ``w`` was last written from it."""
+    return getattr(w, "_tm_master_version", None) == p._version
+
+
+def refresh_bf16_working_params(params) -> None:
+    """Rewrite the attached bf16 working copies as RNE(master), in place.
+
+    Needed after the fp32 masters change outside ``AdamW.step()``, e.g. after
+    ``model.load_state_dict(...)`` on a resume (torchure/train/trainer.py:340-350), so
+    that the next bf16 forward does not run on stale weights. ``AdamW.step()`` raises
+    if it finds a master modified since its copy was last written."""
+    lib = _native.lib()
+    for p in params:
+        w = getattr(p, "_tm_working", None)
+        if w is None:
+            continue
+        tables.require_device_tensor(p, "refresh_bf16_working_params", "param")
+        _native.check(lib.tm_cast_bf16(w.data_ptr(), p.data_ptr(), p.numel(),
+                                       _native.stream_handle(p.device)), "tm_cast_bf16")
+        torch.autograd.graph.increment_version(w)
+        mark_current(p, w)
 
 
 def accumulate_grad_(acc: torch.Tensor, micro: torch.Tensor) -> None:
