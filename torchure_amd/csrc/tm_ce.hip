@@ -67,6 +67,11 @@ __device__ __forceinline__ uint32_t rne16(float f) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// (x - c) * log2(e) with c * log2(e) = cl precomputed: one fma per element. Its rounding
+// differs from the two-step form by at most an ulp of the exponent, well below a bf16 ulp
+// of the result.
+__device__ __forceinline__ float tlog2(float x, float cl) { return fmaf(x, kLog2e, -cl); }
+
 // exp(x - c) through the base-2 exponential: exp2((x - c) * log2(e)), full range
 // (denormal results included).
 __device__ __forceinline__ float exp_shift(float x, float c) { return exp2f((x - c) * kLog2e); }
@@ -143,6 +148,30 @@ __device__ __forceinline__ float block_max(float m) {
   return m;
 }
 
+// Block-wide max of a and max of b in one reduction (b carries a negated minimum).
+template <int kCeThreads>
+__device__ __forceinline__ void block_max2(float& a, float& b) {
+  constexpr int kCeWaves = kCeThreads / 64;
+  __shared__ float la[kMaxWaves], lb[kMaxWaves];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    a = fmaxf(a, __shfl_xor(a, off, 64));
+    b = fmaxf(b, __shfl_xor(b, off, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    la[threadIdx.x >> 6] = a;
+    lb[threadIdx.x >> 6] = b;
+  }
+  __syncthreads();
+  a = la[0];
+  b = lb[0];
+  for (int w = 1; w < kCeWaves; ++w) {
+    a = fmaxf(a, la[w]);
+    b = fmaxf(b, lb[w]);
+  }
+  __syncthreads();
+}
+
 template <int kCeThreads>
 __device__ __forceinline__ float block_sum_f(float s) {
   constexpr int kCeWaves = kCeThreads / 64;
@@ -175,9 +204,11 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
 
   u32x4 keep[kInRegs ? kRegCols : 1];
   float lse;
+  float row_min = -INFINITY;  // known only on the register path
   if constexpr (kInRegs) {
     // The row stays in registers: max pass, then sum-of-exp pass, no second read.
     float m = -INFINITY;
+    float nmin = -INFINITY;  // -(row minimum), reduced with the maximum
     if (vec) {
       // fully unrolled with compile-time indices so that `keep` stays in VGPRs
 #pragma unroll
@@ -188,12 +219,20 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
           keep[k] = w;
           m = fmaxf(m, fmaxf(fmaxf(fmaxf(lo16(w.x), hi16(w.x)), fmaxf(lo16(w.y), hi16(w.y))),
                              fmaxf(fmaxf(lo16(w.z), hi16(w.z)), fmaxf(lo16(w.w), hi16(w.w)))));
+          nmin = fmaxf(nmin, -fminf(fminf(fminf(lo16(w.x), hi16(w.x)), fminf(lo16(w.y), hi16(w.y))),
+                                    fminf(fminf(lo16(w.z), hi16(w.z)), fminf(lo16(w.w), hi16(w.w)))));
         }
       }
     }
-    for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
-      m = fmaxf(m, __uint_as_float(static_cast<uint32_t>(row[i]) << 16));
-    m = block_max<kCeThreads>(m);
+    for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads) {
+      const float x = __uint_as_float(static_cast<uint32_t>(row[i]) << 16);
+      m = fmaxf(m, x);
+      nmin = fmaxf(nmin, -x);
+    }
+    block_max2<kCeThreads>(m, nmin);
+    row_min = -nmin;
+    // exp(x - m) as exp2(x*log2(e) - m*log2(e)): one fma per element
+    const float cm = m * kLog2e;
     float s = 0.0f;
     if (vec) {
 #pragma unroll
@@ -202,10 +241,10 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
         if (v < nvec) {
           const u32x4 w = keep[k];
           // terms below 2^-126 (flushed by the bare exp) cannot move a sum that is >= 1
-          s += exp2_hw((lo16(w.x) - m) * kLog2e) + exp2_hw((hi16(w.x) - m) * kLog2e) +
-               exp2_hw((lo16(w.y) - m) * kLog2e) + exp2_hw((hi16(w.y) - m) * kLog2e) +
-               exp2_hw((lo16(w.z) - m) * kLog2e) + exp2_hw((hi16(w.z) - m) * kLog2e) +
-               exp2_hw((lo16(w.w) - m) * kLog2e) + exp2_hw((hi16(w.w) - m) * kLog2e);
+          s += exp2_hw(tlog2(lo16(w.x), cm)) + exp2_hw(tlog2(hi16(w.x), cm)) +
+               exp2_hw(tlog2(lo16(w.y), cm)) + exp2_hw(tlog2(hi16(w.y), cm)) +
+               exp2_hw(tlog2(lo16(w.z), cm)) + exp2_hw(tlog2(hi16(w.z), cm)) +
+               exp2_hw(tlog2(lo16(w.w), cm)) + exp2_hw(tlog2(hi16(w.w), cm));
         }
       }
     }
@@ -255,20 +294,29 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
     return p;
   };
   const int64_t label_vec = (valid && label >= 0) ? (label >> 3) : -1;
+  const float cl = lse * kLog2e;
+  // the fma is monotonic in x, so the smallest exponent of the row is the row minimum's:
+  // if it is >= -126 no result of the row is denormal and every vector takes the bare exp
+  // (row_min is -inf on the streaming path, which then checks per vector)
+  const bool row_fast = tlog2(row_min, cl) >= -126.0f;
   auto put8 = [&](const u32x4 w, int64_t v) {
     const int64_t b = v * 8;
     u32x4 o;
     if (!valid) {
       o = u32x4{0u, 0u, 0u, 0u};
     } else {
-      float t[8] = {(lo16(w.x) - lse) * kLog2e, (hi16(w.x) - lse) * kLog2e,
-                    (lo16(w.y) - lse) * kLog2e, (hi16(w.y) - lse) * kLog2e,
-                    (lo16(w.z) - lse) * kLog2e, (hi16(w.z) - lse) * kLog2e,
-                    (lo16(w.w) - lse) * kLog2e, (hi16(w.w) - lse) * kLog2e};
+      float t[8] = {tlog2(lo16(w.x), cl), tlog2(hi16(w.x), cl),
+                    tlog2(lo16(w.y), cl), tlog2(hi16(w.y), cl),
+                    tlog2(lo16(w.z), cl), tlog2(hi16(w.z), cl),
+                    tlog2(lo16(w.w), cl), tlog2(hi16(w.w), cl)};
       float p[8];
-      const float tmin = fminf(fminf(fminf(t[0], t[1]), fminf(t[2], t[3])),
-                               fminf(fminf(t[4], t[5]), fminf(t[6], t[7])));
-      if (tmin >= -126.0f) {
+      bool fast = row_fast;
+      if (!fast) {
+        const float tmin = fminf(fminf(fminf(t[0], t[1]), fminf(t[2], t[3])),
+                                 fminf(fminf(t[4], t[5]), fminf(t[6], t[7])));
+        fast = tmin >= -126.0f;
+      }
+      if (fast) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) p[j] = exp2_hw(t[j]);
       } else {  // some result is a denormal: the full-range exp2
