@@ -207,7 +207,8 @@ int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* strea
  * replacing the per-chunk softmax math of torchure/loss/fused_linear_ce.py:40-52:
  *   lse = logsumexp(float(logits)), row_loss = lse - logits[label] (0 on ignored rows),
  *   logits <- bf16(exp(logits - lse) - onehot(label)) on valid rows, 0 on ignored rows.
- * Labels are int64; a row is ignored when label == ignore_index.
+ * Labels are int64; a row is ignored when label == ignore_index. A label outside [0, vocab)
+ * that is not ignore_index gives that row a NaN loss (the reference fails on it in gather).
  */
 int tm_ce_rows_bf16(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows,
                     int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream);

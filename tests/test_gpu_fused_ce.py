@@ -199,3 +199,14 @@ def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops():
     torch.cuda.synchronize()
     assert torch.equal(w1.grad.view(torch.int32), gw_ref.view(torch.int32))
     assert torch.equal(h1.grad.view(torch.int16), gh_ref.view(torch.int16))
+
+
+def test_out_of_range_label_gives_nan_loss():
+    """A label outside [0, vocab) other than ignore_index is an error in the reference (its
+    gather asserts on the device); here the row loss, and so the mean loss, is NaN."""
+    labels = np.array([3, -1, 100000, -100, 7], dtype=np.int64)
+    r = H.rng(11)
+    bits = oracle.bf16_rne((r.standard_normal((5, 4096)) * 2.0).astype(np.float32)).reshape(5, 4096)
+    _, loss = _ce_rows(bits, labels, -100)
+    assert np.isfinite(loss[[0, 4]]).all() and loss[3] == 0.0
+    assert np.isnan(loss[1]) and np.isnan(loss[2])

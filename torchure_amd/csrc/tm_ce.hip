@@ -284,7 +284,11 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
                            ? __uint_as_float(static_cast<uint32_t>(row[label]) << 16)
                            : 0.0f;
   __syncthreads();
-  if (threadIdx.x == 0) row_loss[r] = valid ? (lse - target) : 0.0f;
+  // A label outside [0, vocab) that is not ignore_index makes the reference's gather fail
+  // (a device-side assert); here the row's loss is NaN, so the mean loss shows it without a
+  // host synchronisation. Its gradient row is the plain softmax.
+  const bool in_range = label >= 0 && label < vocab;
+  if (threadIdx.x == 0) row_loss[r] = !valid ? 0.0f : (in_range ? lse - target : __builtin_nanf(""));
 
   // grad = exp(x - lse) on valid rows (0 on ignored rows), minus 1 at the label.
   auto g_of = [&](float x, int64_t idx) -> float {
