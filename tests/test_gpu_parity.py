@@ -887,6 +887,25 @@ def test_stale_working_copy_detected_and_refreshed():
         assert torch.equal(p, q) and torch.equal(w, u)
 
 
+def test_cached_plan_follows_group_list_edits():
+    """Steady-state steps reuse the previous step's table; a param replaced inside a group's
+    list (same length) must be the one updated next, and the old one left alone."""
+    host = H.make_host_set([(32, 16), (16,)], seed=45)
+    params, work, opt = H.device_setup(host, DEV, grad_on_master=True)
+    opt.step()
+    opt.step()  # second step: served from the cached plan
+    old = params[0]
+    new = torch.nn.Parameter(torch.randn_like(old))
+    new.grad = torch.randn_like(old) * 1e-3
+    opt.param_groups[0]["params"][0] = new
+    before_old, before_new = old.detach().clone(), new.detach().clone()
+    opt.step()
+    torch.cuda.synchronize()
+    assert torch.equal(old, before_old)
+    assert not torch.equal(new, before_new)
+    assert float(opt.state[new]["step"]) == 1.0
+
+
 def test_full_size_config3_fp32_accumulation():
     """Config 3 at full size (Qwen3-0.6B shapes, 596M params): four bf16 micro-steps
     accumulated into fp32 .grad (the last one also measuring the norm), grads scaled

@@ -145,3 +145,36 @@ def test_fused_linear_ce_chunk_sizing():
     assert auto_chunk_rows(8192, 151936) == 8192  # 8K tokens fit in one chunk
     assert auto_chunk_rows(10, 151936) == 10
     assert auto_chunk_rows(100000, 10 ** 9) == 256  # never below 256 rows
+
+
+def test_host_list_primitives():
+    """The C++ list walks of the step's host path, on CPU tensors (no GPU work)."""
+    import numpy as np
+
+    from torchure_amd import _native
+
+    h = _native.host()
+    ps = [torch.nn.Parameter(torch.zeros(3)) for _ in range(4)]
+    ws = [None, torch.zeros(3, dtype=torch.bfloat16).requires_grad_(), None,
+          torch.zeros(3, dtype=torch.bfloat16).requires_grad_()]
+    ps[0].grad = torch.ones(3)
+    ws[1].grad = torch.ones(3, dtype=torch.bfloat16)
+    ps[3].grad = torch.ones(3)  # the master's own grad wins over the working copy's
+    ws[3].grad = torch.ones(3, dtype=torch.bfloat16)
+    gs, src = h.grads(ps, ws)
+    assert src == bytes([1, 2, 0, 1])
+    assert gs[0] is ps[0].grad and gs[1] is ws[1].grad and gs[2] is None and gs[3] is ps[3].grad
+    assert list(h.ptrs([ps[0], None])) == [ps[0].data_ptr(), 0]
+    v0 = [p._version for p in ps]
+    h.bump(ps[:2])
+    assert [p._version for p in ps] == [v0[0] + 1, v0[1] + 1, v0[2], v0[3]]
+    assert list(h.versions([ps[0], None])) == [ps[0]._version, -1]
+    assert h.version_sum(ps) == sum(p._version for p in ps)
+    assert h.dense_contiguous(ps) and not h.dense_contiguous([torch.zeros(3, 4).t()])
+    assert not h.dense_contiguous([None]) and not h.dense_contiguous([torch.zeros(2, 2).to_sparse()])
+    assert h.same(ps, list(ps)) and not h.same(ps, ps[::-1]) and not h.same(ps, ps[:3])
+    ptr, numel, code = h.grad_fields([torch.zeros(5)])
+    assert numel[0] == 5 and code[0] == 255  # CPU tensors are not grad-table material
+    with pytest.raises(TypeError):
+        h.ptrs([1])
+    assert isinstance(ptr, np.ndarray)

@@ -125,6 +125,23 @@ def lib() -> ctypes.CDLL:
     return handle
 
 
+_HOST = None
+
+
+def host():
+    """The host-side list primitives (``_tm_host``, CPU-only C++); raises if not built."""
+    global _HOST
+    if _HOST is None:
+        try:
+            from torchure_amd import _tm_host
+        except ImportError as e:
+            raise RuntimeError(
+                "torchure_amd: host extension _tm_host is not built; run "
+                "`python -c 'import __graft_entry__ as g; g.build()'` from the repo root") from e
+        _HOST = _tm_host
+    return _HOST
+
+
 def check(rc: int, what: str) -> None:
     if rc != TM_OK:
         msg = lib().tm_last_error().decode(errors="replace")

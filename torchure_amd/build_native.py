@@ -1,8 +1,13 @@
-"""Compiles libtorchure_amd.so for gfx950 with hipcc (no torch build machinery).
+"""Compiles the package's two native libraries (no torch build machinery):
 
-Flags: -O3, C++17, position-independent shared object, and the packed-fp32
-target feature switched off (``-Xclang -target-feature -Xclang -packed-fp32-ops``)
-so that no v_pk_{add,mul,fma}_f32 instructions are emitted.
+- libtorchure_amd.so: the gfx950 kernels and the C ABI, with hipcc. Flags: -O3, C++17,
+  position-independent shared object, and the packed-fp32 target feature switched off
+  (``-Xclang -target-feature -Xclang -packed-fp32-ops``) so that no v_pk_{add,mul,fma}_f32
+  instructions are emitted.
+- _tm_host.<ext>.so: host-side list primitives (CPU only) as a Python extension, with g++
+  against torch's headers and libraries.
+
+Both are compiled in parallel.
 """
 
 from __future__ import annotations
@@ -42,15 +47,55 @@ def command(output: str = OUTPUT, extra: list[str] | None = None) -> list[str]:
     ]
 
 
+HOST_SOURCE = os.path.join(_HERE, "csrc", "tm_host.cpp")
+
+
+def host_output() -> str:
+    import sysconfig
+
+    return os.path.join(_HERE, "_tm_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def host_command(output: str) -> list[str]:
+    import sysconfig
+
+    import torch
+
+    tdir = os.path.dirname(torch.__file__)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return [
+        shutil.which("g++") or "g++", "-O2", "-std=c++17", "-shared", "-fPIC",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_EXTENSION_NAME=_tm_host", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-I{tdir}/include", f"-I{tdir}/include/torch/csrc/api/include",
+        f"-I{sysconfig.get_paths()['include']}",
+        HOST_SOURCE,
+        f"-L{tdir}/lib", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python", f"-Wl,-rpath,{tdir}/lib",
+        "-o", output,
+    ]
+
+
+def _start(cmd: list[str]) -> subprocess.Popen:
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
 def build(verbose: bool = False) -> str:
-    """Always recompiles; writes to a temporary name and renames into place."""
-    tmp = OUTPUT + ".tmp"
-    res = subprocess.run(command(tmp), capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed:\n{res.stdout}\n{res.stderr}")
-    if verbose and res.stderr:
-        print(res.stderr)
-    os.replace(tmp, OUTPUT)
+    """Always recompiles both libraries; each is written to a temporary name and renamed
+    into place. Returns the kernel library's path."""
+    jobs = []
+    for out, cmd_of, what in ((OUTPUT, command, "hipcc"), (host_output(), host_command, "g++")):
+        tmp = out + ".tmp"
+        jobs.append((out, tmp, what, _start(cmd_of(tmp))))
+    errors = []
+    for out, tmp, what, proc in jobs:
+        stdout, stderr = proc.communicate()
+        if proc.returncode != 0:
+            errors.append(f"{what} failed:\n{stdout}\n{stderr}")
+            continue
+        if verbose and stderr:
+            print(stderr)
+        os.replace(tmp, out)
+    if errors:
+        raise RuntimeError("\n".join(errors))
     return OUTPUT
 
 

@@ -40,15 +40,10 @@ def grads_of(params) -> tuple[list[torch.Tensor], list[torch.nn.Parameter]]:
     A master parameter without its own ``.grad`` contributes the bf16 grad of
     its attached working copy (torchure_amd.optimizer.working), if any.
     """
-    grads, holders = [], []
-    for p in params:
-        g = p.grad
-        if g is None:
-            w = getattr(p, "_tm_working", None)
-            g = w.grad if w is not None else None
-        if g is not None:
-            grads.append(g)
-            holders.append(p)
+    ps = params if isinstance(params, list) else list(params)
+    gs, _ = _native.host().grads(ps, [getattr(p, "_tm_working", None) for p in ps])
+    holders = [p for p, g in zip(ps, gs) if g is not None]
+    grads = [g for g in gs if g is not None]
     return grads, holders
 
 
@@ -72,8 +67,7 @@ class NormLaunch:
         self.device = device
         self.n = len(grads)
         self.chunk_elems = chunk_elems
-        self.chunks, self.n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]),
-                                                       chunk_elems, device)
+        self.chunks, self.n_chunks = tables.CHUNKS.get(rows["numel"], chunk_elems, device)
         self.d_rows = _NORM_UPLOAD(rows, device)
         self.ws = torch.empty(_native.workspace_bytes(len(grads)), dtype=torch.uint8, device=device)
         self.norm = torch.empty((), dtype=torch.float32, device=device)
@@ -118,7 +112,7 @@ def scale_grads_(
     who = "clip_grad_norm"
     device = grads[0].device
     rows = tables.grad_table(grads, who)
-    chunks, n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]), chunk_elems, device)
+    chunks, n_chunks = tables.CHUNKS.get(rows["numel"], chunk_elems, device)
     d_rows = _SCALE_UPLOAD(rows, device)
     rc = _native.lib().tm_grad_scale(
         d_rows.data_ptr(),
@@ -130,8 +124,7 @@ def scale_grads_(
         _native.stream_handle(device),
     )
     _native.check(rc, "tm_grad_scale")
-    for g in grads:
-        torch.autograd.graph.increment_version(g)
+    _native.host().bump(grads)
 
 
 def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:

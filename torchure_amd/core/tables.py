@@ -88,19 +88,21 @@ class ChunkTableCache:
         self._cap = capacity
         self._d: OrderedDict = OrderedDict()
 
-    def get(self, numels: tuple[int, ...], chunk_elems: int, device: torch.device):
-        """The table for these sizes, for a launch on the device's current stream.
+    def get(self, numels, chunk_elems: int, device: torch.device):
+        """The table for these sizes (any int sequence), for a launch on the device's
+        current stream.
 
         A cached table may be read on a stream other than the one it was allocated
         on; record_stream keeps the caching allocator from reusing its block before
         that stream's work has run, should the table be evicted and freed."""
-        key = (numels, chunk_elems, str(device))
+        numels = np.ascontiguousarray(numels, dtype=np.int64)
+        key = (numels.tobytes(), chunk_elems, str(device))
         hit = self._d.get(key)
         if hit is not None:
             self._d.move_to_end(key)
             hit[0].record_stream(torch.cuda.current_stream(device))
             return hit
-        table = _native.fill_chunks(np.asarray(numels, dtype=np.int64), chunk_elems)
+        table = _native.fill_chunks(numels, chunk_elems)
         dev = upload(table, device) if len(table) else torch.empty(8, dtype=torch.uint8, device=device)
         val = (dev, len(table))
         self._d[key] = val
@@ -141,6 +143,19 @@ def require_device_tensor(t: torch.Tensor, who: str, what: str) -> None:
 
 def grad_table(grads: list[torch.Tensor], who: str) -> np.ndarray:
     """tm_tensor_t rows for a grad-only call (norm / scale)."""
+    if not grads:
+        return np.zeros(0, _native.TENSOR_DTYPE)
+    ptr, numel, code = _native.host().grad_fields(grads)
+    if not (code != 255).all():
+        return _grad_table_checked(grads, who)  # raises with the reason
+    rows = np.zeros(len(grads), dtype=_native.TENSOR_DTYPE)
+    rows["grad"] = ptr
+    rows["numel"] = numel
+    rows["flags"] = code  # 0 = TM_GRAD_BF16, 1 = TM_GRAD_F32
+    return rows
+
+
+def _grad_table_checked(grads: list[torch.Tensor], who: str) -> np.ndarray:
     bf16, f32 = torch.bfloat16, torch.float32
     recs = []
     for g in grads:

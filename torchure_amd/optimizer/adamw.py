@@ -118,9 +118,10 @@ class AdamW(torch.optim.Optimizer):
         }
         self.chunk_elems = tables.check_chunk_elems(chunk_elems)
         self.defer_clip = bool(defer_clip)
-        self._pending = None  # (coef device tensor, {id(param): (grad, grad._version)})
+        self._pending = None  # (coef device tensor, _ClipRecord)
         self._uploader = tables.TableUploader()
         self._verified: dict = {}  # id(param) -> _ParamEntry
+        self._plan = None  # _Plan of the last full step, reused while nothing changes
         super().__init__(params, defaults)
         if len(self.param_groups) > _native.TM_MAX_GROUPS:
             raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
@@ -132,6 +133,7 @@ class AdamW(torch.optim.Optimizer):
         ref = weakref.ref(self)
         for p in self.param_groups[-1]["params"]:
             p._tm_owner = ref
+        self._plan = None
 
     def __setstate__(self, state):
         super().__setstate__(state)
@@ -142,6 +144,7 @@ class AdamW(torch.optim.Optimizer):
         self.__dict__.setdefault("_pending", None)
         self.__dict__.setdefault("_uploader", tables.TableUploader())
         self.__dict__.setdefault("_verified", {})
+        self.__dict__.setdefault("_plan", None)
 
     # ------------------------------------------------------------ deferred clip
 
@@ -150,7 +153,8 @@ class AdamW(torch.optim.Optimizer):
         autograd version: the reference scales at clip time, so a grad modified in
         place before the step cannot be reproduced by scaling later (the step raises),
         while a grad replaced by a new tensor simply steps unscaled, as it would there."""
-        self._pending = (coef, {id(p): (g, g._version) for p, g in zip(params, grads)})
+        grads = list(grads)
+        self._pending = (coef, _ClipRecord(list(params), grads, _native.host().versions(grads)))
 
     @staticmethod
     def _modified_error() -> RuntimeError:
@@ -163,16 +167,13 @@ class AdamW(torch.optim.Optimizer):
         """Apply a pending clip coefficient to the grads it measured, in place, and drop it."""
         if self._pending is None:
             return
-        coef, recs = self._pending
+        coef, rec = self._pending
         self._pending = None
         from torchure_amd.core.grad_helper import scale_grads_
 
-        grads = []
-        for g, ver in recs.values():
-            if g._version != ver:
-                raise self._modified_error()
-            grads.append(g)
-        scale_grads_(grads, coef)
+        if not np.array_equal(_native.host().versions(rec.grads), rec.versions):
+            raise self._modified_error()
+        scale_grads_(rec.grads, coef)
 
     # ------------------------------------------------------------ step
 
@@ -198,8 +199,19 @@ class AdamW(torch.optim.Optimizer):
         tensors and grads (bench.py uses this to time the kernels back to back).
 
         ``clip_ids`` names the params whose grads are multiplied by ``coef``: a set of
-        ids, or the {id: (grad, version)} record of a deferred clip, which is checked."""
-        checked = isinstance(clip_ids, dict)
+        ids, or the record of a deferred clip, which is checked (same grad objects, same
+        autograd versions)."""
+        fast = self._plan_fast(coef, clip_ids)
+        if fast is not None:
+            return fast
+        self._plan = None
+        order = []  # (param, entry) of every param with a grad, in table order
+        rec = clip_ids if isinstance(clip_ids, _ClipRecord) else None
+        if rec is not None:
+            clip_ids = rec.index
+            rec_grads = rec.grads
+            vsum = 0  # versions now, of the recorded grads that are still the params' grads
+            matched = []
         per_dev: dict = {}
         hyper = []
         state_map = self.state
@@ -246,22 +258,26 @@ class AdamW(torch.optim.Optimizer):
                 if (not g.is_cuda or g.get_device() != ent.dev_index or g.numel() != ent.numel
                         or not g.is_contiguous() or g.is_sparse):
                     self._check_param(p, g, work)  # raises with a precise message
-                if id(p) in clip_ids:
-                    if not checked:
+                if rec is None:
+                    if id(p) in clip_ids:
                         flags |= clip_flag
-                    else:
-                        rec_g, rec_v = clip_ids[id(p)]
-                        if rec_g is g:
-                            if g._version != rec_v:
-                                raise self._modified_error()
-                            flags |= clip_flag
-                        # else: grad replaced since the clip; it steps unscaled
-                if work is not None and getattr(work, "_tm_master_version", None) != p._version:
-                    raise RuntimeError(
-                        "torchure_amd.AdamW: a fp32 master was modified in place since its bf16 "
-                        "working copy was last written, so the forward ran on stale weights; call "
-                        "torchure_amd.refresh_bf16_working_params(params) after changing masters "
-                        "(e.g. after model.load_state_dict)")
+                else:
+                    k = clip_ids.get(id(p))
+                    # a grad replaced since the clip steps unscaled, as in the reference
+                    if k is not None and rec_grads[k] is g:
+                        flags |= clip_flag
+                        vsum += g._version
+                        matched.append(k)
+                if work is not None:
+                    v = p._version
+                    if v != ent.expect:
+                        if getattr(work, "_tm_master_version", None) != v:
+                            raise RuntimeError(
+                                "torchure_amd.AdamW: a fp32 master was modified in place since its "
+                                "bf16 working copy was last written, so the forward ran on stale "
+                                "weights; call torchure_amd.refresh_bf16_working_params(params) "
+                                "after changing masters (e.g. after model.load_state_dict)")
+                        ent.expect = v
                 bucket = per_dev.get(ent.device)
                 if bucket is None:
                     bucket = per_dev[ent.device] = ([], [], [])
@@ -269,11 +285,90 @@ class AdamW(torch.optim.Optimizer):
                                   ent.numel, gi, flags))
                 bucket[1].extend(ent.written)
                 if work is not None:
-                    bucket[2].append((p, work))
+                    bucket[2].append(ent)
+                order.append((p, ent))
 
+        if rec is not None:
+            vers = rec.versions
+            want = rec.total if len(matched) == len(vers) else sum(vers[k] for k in matched)
+            if vsum != want:  # versions only grow: any in-place change since the clip shows here
+                raise self._modified_error()
         if not per_dev:
             return []
-        return self._plan_launches(per_dev, hyper, coef)
+        launches = self._plan_launches(per_dev, hyper, coef)
+        if len(launches) == 1:
+            self._plan = _Plan(self, order, launches[0])
+        return launches
+
+    def _plan_fast(self, coef, clip_ids):
+        """The steady-state step: the same params have grads from the same sources, and
+        every cached pointer, state object and working-copy version still holds. Then only
+        the grad pointers (and the clip flags) of the cached table change. Returns None
+        whenever anything differs; the full per-param path then rebuilds the plan and
+        reports any error precisely."""
+        plan = self._plan
+        if plan is None or plan.chunk_elems != self.chunk_elems:
+            return None
+        groups = self.param_groups
+        if len(groups) != len(plan.groups):
+            return None
+        host = _native.host()
+        for group, (g0, plist, snap) in zip(groups, plan.groups):
+            if group is not g0 or group["params"] is not plist or not host.same(plist, snap):
+                return None
+        hyper = []
+        for group in groups:
+            lr = group["lr"]
+            if isinstance(lr, torch.Tensor) or any(group.get(k) for k in _UNSUPPORTED):
+                return None
+            b1, b2 = group["betas"]
+            hyper.append((float(lr), float(b1), float(b2), float(group["weight_decay"]), float(group["eps"])))
+        if not host.same([getattr(p, "_tm_working", None) for p in plan.all_params], plan.all_works):
+            return None
+        gs, src = host.grads(plan.all_params, plan.all_works)
+        if src != plan.src:
+            return None
+        gl = [g for g in gs if g is not None]
+        if not host.dense_contiguous(gl) or not np.array_equal(host.ptrs(plan.statics), plan.static_ptrs):
+            return None
+        state_map = self.state
+        states = [state_map.get(p) for p in plan.params]
+        if not host.same(states, plan.states):
+            return None
+        if not (host.same([st.get("exp_avg") for st in states], plan.ms)
+                and host.same([st.get("exp_avg_sq") for st in states], plan.vs)
+                and host.same([st.get("step") for st in states], plan.ss)):
+            return None
+        if plan.wents:
+            want = np.fromiter((e.expect for e in plan.wents), dtype=np.int64, count=len(plan.wents))
+            if not np.array_equal(host.versions(plan.wparams), want):
+                return None
+        flags = plan.flags
+        if coef is not None and clip_ids:
+            if not isinstance(clip_ids, _ClipRecord) or len(clip_ids.grads) != len(gl):
+                return None
+            rec = clip_ids
+            if plan.clip_holders is None or not host.same(rec.holders, plan.clip_holders):
+                perm = [rec.index.get(id(p)) for p in plan.params]
+                if None in perm:
+                    return None
+                plan.clip_holders, plan.clip_perm = rec.holders, perm
+            rg = rec.grads
+            if not host.same([rg[k] for k in plan.clip_perm], gl):
+                return None
+            if host.version_sum(gl) != rec.total:
+                raise self._modified_error()
+            flags = flags | _native.TM_FLAG_CLIP
+        device = plan.device
+        if coef is not None and coef.device != device:
+            return None
+        rows = plan.rows.copy()
+        rows["grad"] = host.ptrs(gl)
+        rows["flags"] = flags
+        plan.chunks.record_stream(torch.cuda.current_stream(device))
+        return [StepLaunch(device, self._uploader(rows, device), plan.n, plan.chunks, plan.n_chunks,
+                           self.chunk_elems, _native.hyper_array(hyper), len(hyper), coef,
+                           plan.written, plan.wents)]
 
     def _verify_param(self, p: torch.Tensor, state: dict, work) -> "_ParamEntry":
         """Full checks of a param, its working copy and its state (created lazily,
@@ -305,6 +400,7 @@ class AdamW(torch.optim.Optimizer):
 
     def load_state_dict(self, state_dict) -> None:
         self._verified.clear()
+        self._plan = None
         super().load_state_dict(state_dict)
 
     def _plan_launches(self, per_dev, hyper, coef) -> list["StepLaunch"]:
@@ -315,9 +411,11 @@ class AdamW(torch.optim.Optimizer):
             rows = np.array(recs, dtype=_native.TENSOR_DTYPE)
             if coef is not None and coef.device != device:
                 raise RuntimeError("torchure_amd.AdamW: clip coefficient on another device")
-            chunks, n_chunks = tables.CHUNKS.get(tuple(r[6] for r in recs), self.chunk_elems, device)
-            out.append(StepLaunch(device, self._uploader(rows, device), n, chunks, n_chunks,
-                                  self.chunk_elems, groups_c, len(hyper), coef, written, pairs))
+            chunks, n_chunks = tables.CHUNKS.get(rows["numel"], self.chunk_elems, device)
+            launch = StepLaunch(device, self._uploader(rows, device), n, chunks, n_chunks,
+                                self.chunk_elems, groups_c, len(hyper), coef, written, pairs)
+            launch.host_rows = rows.tobytes()
+            out.append(launch)
         return out
 
     @staticmethod
@@ -354,7 +452,7 @@ class _ParamEntry:
     """Verified per-param record: the objects it was built from and their pointers."""
 
     __slots__ = ("param", "work", "step", "m", "v", "p_ptr", "m_ptr", "v_ptr", "s_ptr", "w_ptr",
-                 "numel", "device", "dev_index", "written")
+                 "numel", "device", "dev_index", "written", "expect")
 
     def __init__(self, p, work, step, m, v):
         self.param, self.work, self.step, self.m, self.v = p, work, step, m, v
@@ -369,6 +467,63 @@ class _ParamEntry:
         self.numel = p.numel()
         self.device = p.device
         self.dev_index = p.get_device()
+        # autograd version of the master when the working copy last held RNE(master)
+        self.expect = getattr(work, "_tm_master_version", None) if work is not None else None
+
+
+class _ClipRecord:
+    """A deferred clip: the params whose grads it measured, those grad objects and their
+    autograd versions at clip time (``index`` maps id(param) to its position)."""
+
+    __slots__ = ("holders", "grads", "versions", "total", "_index")
+
+    def __init__(self, holders: list, grads: list, versions):
+        self.holders, self.grads, self.versions = holders, grads, versions
+        self.total = int(np.asarray(versions, dtype=np.int64).sum())
+        self._index = None
+
+    @property
+    def index(self) -> dict:
+        if self._index is None:
+            self._index = dict(zip(map(id, self.holders), range(len(self.holders))))
+        return self._index
+
+
+_UNSUPPORTED = ("amsgrad", "maximize", "capturable", "differentiable")
+
+
+class _Plan:
+    """The table of the last full step and what it was built from, for the fast path."""
+
+    __slots__ = ("groups", "all_params", "all_works", "src", "params", "statics", "static_ptrs",
+                 "states", "ms", "vs", "ss", "wents", "wparams", "rows", "flags", "n", "device",
+                 "chunks", "n_chunks", "chunk_elems", "written", "clip_holders", "clip_perm")
+
+    def __init__(self, opt: "AdamW", order: list, launch: "StepLaunch"):
+        host = _native.host()
+        # each group, its params list and a snapshot of that list's contents
+        self.groups = [(g, g["params"], list(g["params"])) for g in opt.param_groups]
+        self.all_params = [p for g in opt.param_groups for p in g["params"]]
+        self.all_works = [getattr(p, "_tm_working", None) for p in self.all_params]
+        self.src = host.grads(self.all_params, self.all_works)[1]
+        self.params = [p for p, _ in order]
+        ents = [e for _, e in order]
+        self.statics = [t for e in ents for t in (e.param, e.m, e.v, e.step, e.work)]
+        self.static_ptrs = host.ptrs(self.statics)
+        self.states = [opt.state[p] for p in self.params]
+        self.ms = [e.m for e in ents]
+        self.vs = [e.v for e in ents]
+        self.ss = [e.step for e in ents]
+        self.wents = launch.pairs
+        self.wparams = [e.param for e in self.wents]
+        self.n = launch.n
+        self.device = launch.device
+        self.chunks, self.n_chunks, self.chunk_elems = launch.chunks, launch.n_chunks, launch.chunk_elems
+        self.written = launch.written
+        self.rows = np.frombuffer(launch.host_rows, dtype=_native.TENSOR_DTYPE).copy()
+        self.flags = self.rows["flags"] & ~np.uint32(_native.TM_FLAG_CLIP)
+        self.clip_holders = None
+        self.clip_perm = None
 
 
 class StepLaunch:
@@ -381,8 +536,9 @@ class StepLaunch:
 
     def __init__(self, device, d_rows, n, chunks, n_chunks, chunk_elems, groups_c, n_groups, coef,
                  written=(), pairs=()):
-        self.written = list(written)
-        self.pairs = list(pairs)  # (master, bf16 working copy) written by the launch
+        self.written = written if isinstance(written, list) else list(written)
+        self.pairs = pairs if isinstance(pairs, list) else list(pairs)  # entries with a working copy
+        self.host_rows = None  # the uploaded table's bytes, when the caller keeps them
         self.device = device
         self.d_rows = d_rows
         self.n = n
@@ -409,9 +565,10 @@ class StepLaunch:
         )
         _native.check(rc, "tm_adamw_step")
         if self.written:
-            torch.autograd.graph.increment_version(self.written)
-        for p, w in self.pairs:
-            w._tm_master_version = p._version
+            _native.host().bump(self.written)
+        for e in self.pairs:  # the bump above made each master's version one higher
+            e.expect += 1
+            e.work._tm_master_version = e.expect
 
 
 def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out: bool = True) -> int:

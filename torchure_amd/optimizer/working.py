@@ -188,7 +188,7 @@ def accumulate_grads_(params, *, last: bool = False,
     rows["numel"] = np.asarray([a.numel() for a in accs], dtype=np.int64)
     rows["flags"] = np.asarray(assign, dtype=np.int64) * _native.TM_ACCUM_ASSIGN
     chunk_elems = tables.check_chunk_elems(chunk_elems)
-    chunks, n_chunks = tables.CHUNKS.get(tuple(int(x) for x in rows["numel"]), chunk_elems, device)
+    chunks, n_chunks = tables.CHUNKS.get(rows["numel"], chunk_elems, device)
     d_rows = _ACC_UPLOAD(rows, device)
     norm = torch.empty((), dtype=torch.float32, device=device) if last else None
     ws = torch.empty(_native.workspace_bytes(0), dtype=torch.uint8, device=device) if last else None
