@@ -5,7 +5,7 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--config qwen3-4b|qwen3-0.6
 One "step" = clip_grad_norm (two-pass norm) + AdamW.step() (step counters,
 fused update, bf16 working copies) over the whole parameter set, through the
 package's public API, with every tensor already resident in HBM. Inputs are
-synthetic (steady state of BASELINE config 4: master ~ N(0, .02),
+synthetic (the 4B steady-state configuration: master ~ N(0, .02),
 m ~ N(0, 1e-4), v = |N(0,1)| * 1e-8, bf16 grads ~ N(0, 1e-3), step 1000,
 lr 3e-4, betas (0.9, 0.95), wd 0.1 on >=2-D, clip 1.0).
 

@@ -1,4 +1,4 @@
-"""GPU parity of the chunked fused linear + cross-entropy.
+"""GPU parity of the chunked fused linear + cross-entropy (torchure/loss/fused_linear_ce.py).
 
 Checks:
 - the fused CE-row kernel vs an fp64 restatement on the same bf16 logits: per-row

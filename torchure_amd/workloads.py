@@ -36,7 +36,7 @@ def qwen3_param_shapes(num_layers, num_heads, num_kv_heads, emb_dim, head_dim, v
     return shapes
 
 
-# BASELINE configurations (name -> Qwen3 kwargs).
+# Benchmark and parity configurations (name -> Qwen3 kwargs).
 CONFIGS = {
     "tiny": dict(num_layers=2, num_heads=4, num_kv_heads=2, emb_dim=256, head_dim=64,
                  vocab_size=4096, ffn_dim=768),
