@@ -906,6 +906,44 @@ def test_cached_plan_follows_group_list_edits():
     assert float(opt.state[new]["step"]) == 1.0
 
 
+def test_steady_state_transitions_match_torch():
+    """Steps served from the cached plan and steps that must leave it, against torch's
+    fused AdamW, bit for bit: grads reused in place (zero_grad(set_to_none=False)), a param
+    whose grad disappears for a step (a frozen layer), fresh grad tensors, and the clip."""
+    import torchure_amd as ta
+
+    torch.manual_seed(12)
+    shapes = [(48, 32), (32,), (16, 8), (8,)]
+    init = [torch.randn(sh, device=DEV) * 0.05 for sh in shapes]
+    mine = [torch.nn.Parameter(t.clone()) for t in init]
+    ref = [torch.nn.Parameter(t.clone()) for t in init]
+    groups = lambda ps: [{"params": [p for p in ps if p.dim() >= 2], "weight_decay": 0.1},
+                         {"params": [p for p in ps if p.dim() < 2], "weight_decay": 0.0}]
+    opt = ta.AdamW(groups(mine), lr=1e-3, betas=(0.9, 0.95), fused=True)
+    opt_r = torch.optim.AdamW(groups(ref), lr=1e-3, betas=(0.9, 0.95), fused=True)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    for k in range(7):
+        grads = [torch.randn(sh, device=DEV, generator=g) * 1e-3 for sh in shapes]
+        for i, (a, b) in enumerate(zip(mine, ref)):
+            frozen = k == 3 and i == 2
+            if frozen:
+                a.grad = b.grad = None
+            elif k < 4 and a.grad is not None:  # in place, as after zero_grad(set_to_none=False)
+                a.grad.copy_(grads[i])
+                b.grad.copy_(grads[i])
+            else:
+                a.grad, b.grad = grads[i].clone(), grads[i].clone()
+        ta.clip_grad_norm(mine, None, 1e9)  # coefficient 1.0, deferred into the step
+        torch.nn.utils.clip_grad_norm_(ref, 1e9)
+        opt.step()
+        opt_r.step()
+    torch.cuda.synchronize()
+    for a, b in zip(mine, ref):
+        assert torch.equal(a, b)
+        for key in ("exp_avg", "exp_avg_sq", "step"):
+            assert torch.equal(opt.state[a][key], opt_r.state[b][key]), key
+
+
 def test_full_size_config3_fp32_accumulation():
     """Config 3 at full size (Qwen3-0.6B shapes, 596M params): four bf16 micro-steps
     accumulated into fp32 .grad (the last one also measuring the norm), grads scaled
