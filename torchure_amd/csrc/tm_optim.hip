@@ -413,7 +413,7 @@ __global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
 // loaded before any is computed, to keep that many 16-byte loads per array in
 // flight per thread.
 #ifndef TM_UPDATE_GROUPS
-#define TM_UPDATE_GROUPS 2
+#define TM_UPDATE_GROUPS 4
 #endif
 #ifndef TM_UPDATE_NT
 #define TM_UPDATE_NT 1
