@@ -231,6 +231,61 @@ def test_matches_torch_rocm_fused_adamw():
         assert torch.equal(w, p.detach().to(torch.bfloat16))
 
 
+_CORNERS = {
+    # name: (lr, beta1, beta2, weight_decay, eps, step, p scale, m scale, v scale, g scale)
+    "lr_zero": (0.0, 0.9, 0.95, 0.1, 1e-8, 10.0, 0.02, 1e-4, 1e-8, 1e-3),
+    "betas_zero": (1e-3, 0.0, 0.0, 0.1, 1e-8, 10.0, 0.02, 1e-4, 1e-8, 1e-3),
+    "strong_decay": (1e-2, 0.9, 0.95, 1.0, 1e-8, 10.0, 0.02, 1e-4, 1e-8, 1e-3),
+    "large_eps": (1e-3, 0.9, 0.95, 0.1, 1.0, 10.0, 0.02, 1e-4, 1e-8, 1e-3),
+    "step_1e6": (3e-4, 0.9, 0.95, 0.1, 1e-8, 1e6, 0.02, 1e-4, 1e-8, 1e-3),
+    "fresh": (3e-4, 0.9, 0.999, 0.1, 1e-8, 0.0, 0.02, 0.0, 0.0, 1e-3),
+    "tiny_values": (3e-4, 0.9, 0.95, 0.1, 1e-8, 100.0, 1e-30, 1e-39, 1e-44, 1e-30),
+    "huge_grads": (3e-4, 0.9, 0.95, 0.1, 1e-8, 100.0, 1.0, 1e15, 1e30, 1e20),
+    "zero_grads": (3e-4, 0.9, 0.95, 0.1, 1e-8, 100.0, 0.02, 1e-4, 1e-8, 0.0),
+    "half_betas": (1e-3, 0.5, 0.5, 0.0, 1e-12, 3.0, 0.02, 1e-4, 1e-8, 1e-3),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_CORNERS))
+def test_hyperparameter_corners_match_torch_rocm(case):
+    """Corner regimes of the update (zero lr or betas, strong decay, large eps, very late and
+    fresh steps, values near the fp32 range limits, zero grads) against torch-ROCm's
+    AdamW(fused=True) on the same device, fp32 grads: within the 2-ulp contract, bit-exact
+    in practice."""
+    import torchure_amd as ta
+
+    lr, b1, b2, wd, eps, step, ps_, ms_, vs_, gs_ = _CORNERS[case]
+    g = torch.Generator(device=DEV).manual_seed(sum(map(ord, case)))  # stable across runs
+    shapes = [(64, 64), (1000,), (7,)]
+    init = [(torch.randn(sh, device=DEV, generator=g) * ps_,
+             torch.randn(sh, device=DEV, generator=g) * ms_,
+             torch.randn(sh, device=DEV, generator=g).abs() * vs_,
+             torch.randn(sh, device=DEV, generator=g) * gs_) for sh in shapes]
+    mine = [torch.nn.Parameter(t[0].clone()) for t in init]
+    ref = [torch.nn.Parameter(t[0].clone()) for t in init]
+    opt = ta.AdamW(mine, lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd, fused=True)
+    topt = torch.optim.AdamW(ref, lr=lr, betas=(b1, b2), eps=eps, weight_decay=wd, fused=True)
+    for o, ps in ((opt, mine), (topt, ref)):
+        for q, t in zip(ps, init):
+            q.grad = t[3].clone()
+            o.state[q]["step"] = torch.tensor(step, dtype=torch.float32, device=DEV)
+            o.state[q]["exp_avg"] = t[1].clone()
+            o.state[q]["exp_avg_sq"] = t[2].clone()
+    opt.step()
+    topt.step()
+    torch.cuda.synchronize()
+    worst, exact, n = 0, 0, 0
+    for a, b in zip(mine, ref):
+        pairs = [(a, b)] + [(opt.state[a][k], topt.state[b][k]) for k in ("exp_avg", "exp_avg_sq", "step")]
+        for x, y in pairs:
+            d = H.ulp_diff(x.detach().cpu().numpy().reshape(-1), y.detach().cpu().numpy().reshape(-1))
+            worst = max(worst, int(d.max()))
+            exact += int((d == 0).sum())
+            n += d.size
+    print(f"{case}: max ulp {worst}, bit-exact {exact}/{n}")
+    assert worst <= 2, (case, worst)
+
+
 def test_reference_clip_known_answers():
     """torchure tests/grad_helper.py:105-160,188-204 restated on the GPU path."""
     import torchure_amd as ta
