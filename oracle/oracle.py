@@ -128,14 +128,27 @@ def sumsq(g) -> float:
     return float(lib().orc_sumsq_f32(_ptr(g), g.size))
 
 
+# Smallest value that fp32 rounding sends to infinity (2^128 - 2^103).
+F32_OVERFLOW = float.fromhex("0x1.ffffffp+127")
+
+
+def _f32_norm(sq: float) -> np.float32:
+    """sqrt of a sum of squares as an fp32 reduction returns it: inf once the sum
+    itself would round past FLT_MAX."""
+    if sq >= F32_OVERFLOW:
+        return np.float32(np.inf)
+    return np.float32(np.sqrt(sq))
+
+
 def global_norm(grads) -> np.float32:
     """grad_helper.py:17-18: per-tensor fp32 L2 norms, then the norm of the stack.
 
     Each per-tensor norm is computed in fp64 and rounded to fp32 (what a
-    well-conditioned fp32 reduction converges to); the outer norm likewise.
+    well-conditioned fp32 reduction converges to); the outer norm likewise. torch
+    reduces both in fp32, so a sum of squares beyond the fp32 range gives inf.
     """
-    norms = np.array([np.float32(np.sqrt(sumsq(g))) for g in grads], dtype=np.float32)
-    return np.float32(np.sqrt(np.sum(norms.astype(np.float64) ** 2)))
+    norms = np.array([_f32_norm(sumsq(g)) for g in grads], dtype=np.float32)
+    return _f32_norm(float(np.sum(norms.astype(np.float64) ** 2)))
 
 
 def clip_coef(total, max_norm) -> np.float32:

@@ -10,6 +10,7 @@ exactness separately where it is the stronger claim.
 from __future__ import annotations
 
 import copy
+import math
 
 import numpy as np
 import pytest
@@ -284,6 +285,50 @@ def test_hyperparameter_corners_match_torch_rocm(case):
             n += d.size
     print(f"{case}: max ulp {worst}, bit-exact {exact}/{n}")
     assert worst <= 2, (case, worst)
+
+
+@pytest.mark.parametrize("grad_dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("scale", [1e18, 3e17])
+def test_norm_overflow_matches_torch(grad_dtype, scale):
+    """torch's fp32 norm reductions give inf once the sum of squares leaves the fp32 range
+    (1000 x 1e18 does; 1000 x 3e17 does not), and the clip coefficient becomes 0. The fp64
+    norm is cut at the same point, so the clipped step matches the reference's: norm bit for
+    bit when finite within 1e-6, and the update equal to torch's fused AdamW on the grads
+    torch's clip composition leaves."""
+    import torchure_amd as ta
+    from oracle.torch_composition import clip_grad_norm_reference
+
+    shapes = [(1000,), (10,)]
+    vals = [scale, 1.0]
+    mine = [torch.nn.Parameter(torch.full(sh, 0.01, device=DEV)) for sh in shapes]
+    ref = [torch.nn.Parameter(torch.full(sh, 0.01, device=DEV)) for sh in shapes]
+    if grad_dtype == "bf16":
+        work = ta.attach_bf16_working_params(mine)
+        for w, sh, v in zip(work, shapes, vals):
+            w.grad = torch.full(sh, v, device=DEV, dtype=torch.bfloat16)
+        gvals = [float(torch.tensor(v, dtype=torch.bfloat16)) for v in vals]
+    else:
+        for p, sh, v in zip(mine, shapes, vals):
+            p.grad = torch.full(sh, v, device=DEV)
+        gvals = vals
+    for q, sh, v in zip(ref, shapes, gvals):
+        q.grad = torch.full(sh, v, device=DEV)
+    opt = ta.AdamW(mine, lr=1e-3, fused=True)
+    topt = torch.optim.AdamW(ref, lr=1e-3, fused=True)
+    norm = ta.clip_grad_norm(mine, None, 1.0)
+    want = clip_grad_norm_reference([q.grad for q in ref], 1.0)
+    torch.cuda.synchronize()
+    if math.isinf(want.item()):
+        assert math.isinf(norm.item())
+    else:
+        assert abs(norm.item() - want.item()) <= 1e-6 * want.item()
+    opt.step()
+    topt.step()
+    torch.cuda.synchronize()
+    if math.isinf(want.item()):  # coefficient 0: the reference steps on zeroed grads
+        for a, b in zip(mine, ref):
+            assert torch.equal(a, b)
+            assert torch.equal(opt.state[a]["exp_avg"], topt.state[b]["exp_avg"])
 
 
 def test_reference_clip_known_answers():

@@ -240,3 +240,18 @@ def test_bf16_update_equals_widened_update():
     oracle.adamw_update(p2, m2, v2, gw, 1001.0, 3e-4, 0.9, 0.95, 0.1, 1e-8)
     assert np.array_equal(p, p2) and np.array_equal(m, m2) and np.array_equal(v, v2)
     assert np.array_equal(out, oracle.bf16_rne(p))
+
+
+@pytest.mark.parametrize("scale,n", [(1e18, 1000), (3e17, 1000), (1e19, 4), (1e30, 1), (5e18, 13)])
+def test_global_norm_overflows_like_torch(scale, n):
+    """torch's fp32 norm reductions return inf once the sum of squares leaves the fp32
+    range (1000 x 1e18 already does); the oracle follows them, including just below it."""
+    import torch
+
+    grads = [np.full(n, scale, dtype=np.float32), np.full(10, 1.0, dtype=np.float32)]
+    want = torch.linalg.vector_norm(torch.stack(torch._foreach_norm([torch.from_numpy(g) for g in grads], 2.0)), 2.0)
+    got = oracle.global_norm(grads)
+    if np.isinf(want.item()):
+        assert np.isinf(got)
+    else:
+        assert abs(float(got) - want.item()) <= 1e-6 * want.item()

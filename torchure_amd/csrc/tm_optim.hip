@@ -328,7 +328,11 @@ __global__ __launch_bounds__(kThreads) void norm_finalize_kernel(
   for (int i = threadIdx.x; i < TM_NORM_PARTIALS; i += kThreads) acc += partials[i];
   const double total = block_sum(acc);
   if (threadIdx.x == 0) {
-    const float norm = static_cast<float>(sqrt(total));
+    // The reference's norms reduce in fp32 (torch._foreach_norm, then vector_norm of the
+    // stack): once the sum of squares rounds past FLT_MAX they return inf, and the clip
+    // coefficient becomes 0. The fp64 sum here would stay finite, so it is cut at the same
+    // point: 2^128 - 2^103, the smallest value fp32 rounding sends to infinity.
+    const float norm = total >= 0x1.ffffffp+127 ? INFINITY : static_cast<float>(sqrt(total));
     *norm_out = norm;
     if (clip) *coef_out = clip_coef(norm, max_norm);
   }
