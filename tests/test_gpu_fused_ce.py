@@ -210,3 +210,33 @@ def test_out_of_range_label_gives_nan_loss():
     _, loss = _ce_rows(bits, labels, -100)
     assert np.isfinite(loss[[0, 4]]).all() and loss[3] == 0.0
     assert np.isnan(loss[1]) and np.isnan(loss[2])
+
+
+def test_ce_rows_edge_rows_vs_fp64():
+    """Rows the random tests do not reach: masked vocabulary entries (-inf), a range wide
+    enough that most results are denormal or zero (the full-range exp fallback), constant
+    rows, large magnitudes, and a label on a -inf logit (infinite loss)."""
+    v = 4096
+    r = H.rng(21)
+    rows = []
+    x = (r.standard_normal(v) * 2.0).astype(np.float32); x[::3] = -np.inf; rows.append(x)      # masked
+    x = np.linspace(-200.0, 20.0, v).astype(np.float32); rows.append(x)                       # denormal tail
+    rows.append(np.full(v, 1.5, dtype=np.float32))                                            # constant
+    x = (r.standard_normal(v) * 1e4).astype(np.float32); rows.append(x)                       # large spread
+    x = (r.standard_normal(v) + 1e30).astype(np.float32); rows.append(x)                      # huge offset
+    x = (r.standard_normal(v)).astype(np.float32); x[5] = -np.inf; rows.append(x)             # label on -inf
+    bits = oracle.bf16_rne(np.stack(rows)).reshape(len(rows), v)
+    labels = np.array([1, 4000, 7, 123, 99, 5], dtype=np.int64)
+    grad_bits, loss = _ce_rows(bits, labels, -100)
+    xd = oracle.bf16_to_f32(bits).reshape(len(rows), v).astype(np.float64)
+    mx = xd.max(axis=1, keepdims=True)
+    lse = (mx + np.log(np.exp(xd - mx).sum(axis=1, keepdims=True)))[:, 0]
+    want_loss = lse - xd[np.arange(len(rows)), labels]
+    assert np.isinf(loss[5]) and loss[5] > 0
+    np.testing.assert_allclose(loss[:5], want_loss[:5], rtol=1e-6, atol=1e-6)
+    probs = np.exp(xd - lse[:, None])
+    probs[np.arange(len(rows)), labels] -= 1.0
+    want_bits = oracle.bf16_rne(probs.astype(np.float32)).reshape(len(rows), v)
+    diff = np.abs(grad_bits.astype(np.int32) - want_bits.astype(np.int32))
+    assert diff.max() <= 1, (diff.max(), np.argwhere(diff > 1)[:4])
+    assert np.all(grad_bits[0, ::3] == 0)  # exp(-inf) = 0 exactly

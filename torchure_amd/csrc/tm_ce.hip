@@ -26,6 +26,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "torchure_amd.h"
 #include "tm_internal.h"
 
@@ -67,10 +69,17 @@ __device__ __forceinline__ uint32_t rne16(float f) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// (x - c) * log2(e) with c * log2(e) = cl precomputed: one fma per element. Its rounding
-// differs from the two-step form by at most an ulp of the exponent, well below a bf16 ulp
-// of the result.
-__device__ __forceinline__ float tlog2(float x, float cl) { return fmaf(x, kLog2e, -cl); }
+// The exponent (x - c) * log2(e) of exp(x - c). With kFold it is one fma against the
+// precomputed cl = c * log2(e); cl carries an absolute rounding error of half an ulp of
+// |c| * log2(e), which for |c| <= kFoldMax is at most 3.8e-6 (a relative error below
+// 2.6e-6 in the result, far under half a bf16 ulp). Rows with larger |c| take the two-step
+// form, exact at x = c and accurate at any magnitude.
+constexpr float kFoldMax = 64.0f;
+
+template <bool kFold>
+__device__ __forceinline__ float tlog2(float x, float c, float cl) {
+  return kFold ? fmaf(x, kLog2e, -cl) : (x - c) * kLog2e;
+}
 
 // exp(x - c) through the base-2 exponential: exp2((x - c) * log2(e)), full range
 // (denormal results included).
@@ -231,23 +240,26 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
     }
     block_max2<kCeThreads>(m, nmin);
     row_min = -nmin;
-    // exp(x - m) as exp2(x*log2(e) - m*log2(e)): one fma per element
     const float cm = m * kLog2e;
-    float s = 0.0f;
-    if (vec) {
+    // terms below 2^-126 (flushed by the bare exp) cannot move a sum that is >= 1
+    auto sum_exp = [&](auto fold) {
+      constexpr bool F = decltype(fold)::value;
+      float acc = 0.0f;
 #pragma unroll
       for (int k = 0; k < kRegCols; ++k) {
         const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
         if (v < nvec) {
           const u32x4 w = keep[k];
-          // terms below 2^-126 (flushed by the bare exp) cannot move a sum that is >= 1
-          s += exp2_hw(tlog2(lo16(w.x), cm)) + exp2_hw(tlog2(hi16(w.x), cm)) +
-               exp2_hw(tlog2(lo16(w.y), cm)) + exp2_hw(tlog2(hi16(w.y), cm)) +
-               exp2_hw(tlog2(lo16(w.z), cm)) + exp2_hw(tlog2(hi16(w.z), cm)) +
-               exp2_hw(tlog2(lo16(w.w), cm)) + exp2_hw(tlog2(hi16(w.w), cm));
+          acc += exp2_hw(tlog2<F>(lo16(w.x), m, cm)) + exp2_hw(tlog2<F>(hi16(w.x), m, cm)) +
+                 exp2_hw(tlog2<F>(lo16(w.y), m, cm)) + exp2_hw(tlog2<F>(hi16(w.y), m, cm)) +
+                 exp2_hw(tlog2<F>(lo16(w.z), m, cm)) + exp2_hw(tlog2<F>(hi16(w.z), m, cm)) +
+                 exp2_hw(tlog2<F>(lo16(w.w), m, cm)) + exp2_hw(tlog2<F>(hi16(w.w), m, cm));
         }
       }
-    }
+      return acc;
+    };
+    float s = 0.0f;
+    if (vec) s = fabsf(m) <= kFoldMax ? sum_exp(std::true_type{}) : sum_exp(std::false_type{});
     for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
       s += exp_shift(__uint_as_float(static_cast<uint32_t>(row[i]) << 16), m);
     s = block_sum_f<kCeThreads>(s);
@@ -299,20 +311,22 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
   };
   const int64_t label_vec = (valid && label >= 0) ? (label >> 3) : -1;
   const float cl = lse * kLog2e;
-  // the fma is monotonic in x, so the smallest exponent of the row is the row minimum's:
-  // if it is >= -126 no result of the row is denormal and every vector takes the bare exp
-  // (row_min is -inf on the streaming path, which then checks per vector)
-  const bool row_fast = tlog2(row_min, cl) >= -126.0f;
-  auto put8 = [&](const u32x4 w, int64_t v) {
+  const bool fold = fabsf(lse) <= kFoldMax;
+  // both exponent forms are monotonic in x, so the smallest exponent of the row is the row
+  // minimum's: if it is >= -126 no result of the row is denormal and every vector takes the
+  // bare exp (row_min is -inf on the streaming path, which then checks per vector)
+  const bool row_fast = (fold ? tlog2<true>(row_min, lse, cl) : tlog2<false>(row_min, lse, cl)) >= -126.0f;
+  auto put8 = [&](const u32x4 w, int64_t v, auto fold_tag) {
+    constexpr bool F = decltype(fold_tag)::value;
     const int64_t b = v * 8;
     u32x4 o;
     if (!valid) {
       o = u32x4{0u, 0u, 0u, 0u};
     } else {
-      float t[8] = {tlog2(lo16(w.x), cl), tlog2(hi16(w.x), cl),
-                    tlog2(lo16(w.y), cl), tlog2(hi16(w.y), cl),
-                    tlog2(lo16(w.z), cl), tlog2(hi16(w.z), cl),
-                    tlog2(lo16(w.w), cl), tlog2(hi16(w.w), cl)};
+      float t[8] = {tlog2<F>(lo16(w.x), lse, cl), tlog2<F>(hi16(w.x), lse, cl),
+                    tlog2<F>(lo16(w.y), lse, cl), tlog2<F>(hi16(w.y), lse, cl),
+                    tlog2<F>(lo16(w.z), lse, cl), tlog2<F>(hi16(w.z), lse, cl),
+                    tlog2<F>(lo16(w.w), lse, cl), tlog2<F>(hi16(w.w), lse, cl)};
       float p[8];
       bool fast = row_fast;
       if (!fast) {
@@ -335,17 +349,21 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
     }
     *reinterpret_cast<u32x4*>(row + b) = o;
   };
-  if (vec) {
+  auto write_row = [&](auto fold_tag) {
     if constexpr (kInRegs) {
 #pragma unroll
       for (int k = 0; k < kRegCols; ++k) {
         const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
-        if (v < nvec) put8(keep[k], v);
+        if (v < nvec) put8(keep[k], v, fold_tag);
       }
     } else {
       for (int64_t v = threadIdx.x; v < nvec; v += kCeThreads)
-        put8(*reinterpret_cast<const u32x4*>(row + v * 8), v);
+        put8(*reinterpret_cast<const u32x4*>(row + v * 8), v, fold_tag);
     }
+  };
+  if (vec) {
+    if (fold) write_row(std::true_type{});
+    else write_row(std::false_type{});
   }
   for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads)
     row[i] = static_cast<uint16_t>(rne16(g_of(__uint_as_float(static_cast<uint32_t>(row[i]) << 16), i)));
