@@ -212,11 +212,13 @@ def test_out_of_range_label_gives_nan_loss():
     assert np.isnan(loss[1]) and np.isnan(loss[2])
 
 
-def test_ce_rows_edge_rows_vs_fp64():
+@pytest.mark.parametrize("v", [4096, 1001, 200000])
+def test_ce_rows_edge_rows_vs_fp64(v):
     """Rows the random tests do not reach: masked vocabulary entries (-inf), a range wide
     enough that most results are denormal or zero (the full-range exp fallback), constant
-    rows, large magnitudes, and a label on a -inf logit (infinite loss)."""
-    v = 4096
+    rows, large magnitudes, and a label on a -inf logit (infinite loss). On the in-register
+    path (4096), the element-wise path (1001: rows not 16-byte aligned) and the two-read
+    path (200000)."""
     r = H.rng(21)
     rows = []
     x = (r.standard_normal(v) * 2.0).astype(np.float32); x[::3] = -np.inf; rows.append(x)      # masked
@@ -226,7 +228,7 @@ def test_ce_rows_edge_rows_vs_fp64():
     x = (r.standard_normal(v) + 1e30).astype(np.float32); rows.append(x)                      # huge offset
     x = (r.standard_normal(v)).astype(np.float32); x[5] = -np.inf; rows.append(x)             # label on -inf
     bits = oracle.bf16_rne(np.stack(rows)).reshape(len(rows), v)
-    labels = np.array([1, 4000, 7, 123, 99, 5], dtype=np.int64)
+    labels = np.array([1, v - 96, 7, 123, 99, 5], dtype=np.int64)
     grad_bits, loss = _ce_rows(bits, labels, -100)
     xd = oracle.bf16_to_f32(bits).reshape(len(rows), v).astype(np.float64)
     mx = xd.max(axis=1, keepdims=True)
