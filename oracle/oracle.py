@@ -111,6 +111,8 @@ def adamw_update_bf16(p, m, v, g_bits, out_bits, coef, clip, step_after, lr, bet
     for a in (p, m, v):
         assert a.dtype == np.float32 and a.flags.c_contiguous
     assert g_bits.dtype == np.uint16
+    assert p.size == m.size == v.size == g_bits.size
+    assert out_bits is None or (out_bits.dtype == np.uint16 and out_bits.size == p.size)
     lib(threaded).orc_adamw_update_bf16(
         _ptr(p), _ptr(m), _ptr(v), _ptr(g_bits), _ptr(out_bits) if out_bits is not None else None,
         p.size, float(coef), int(clip), float(step_after), lr, beta1, beta2, weight_decay, eps)

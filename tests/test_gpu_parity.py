@@ -1044,6 +1044,50 @@ def test_steady_state_transitions_match_torch():
             assert torch.equal(opt.state[a][key], opt_r.state[b][key]), key
 
 
+def test_tensor_beyond_2_31_elements():
+    """One tensor of 2^31 + 12,345 elements (odd: the element-wise tail runs too), the
+    64-bit addressing of every kernel on the path: attach (cast), clip (norm + deferred
+    coefficient) and the step. Windows at the start, across element 2^31 and at the end are
+    checked bit for bit against the oracle; the norm against fp64 over every element."""
+    import torchure_amd as ta
+
+    n = 2**31 + 12345
+    g = torch.Generator(device=DEV).manual_seed(31)
+    p = torch.nn.Parameter(torch.randn((1, n), device=DEV, generator=g) * 0.02)
+    (w,) = ta.attach_bf16_working_params([p])
+    w.grad = (torch.randn((1, n), device=DEV, generator=g) * 1e-3).to(torch.bfloat16)
+    opt = ta.AdamW([p], lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, fused=True)
+    st = opt.state[p]
+    st["step"] = torch.tensor(1000.0, device=DEV)
+    st["exp_avg"] = torch.randn((1, n), device=DEV, generator=g) * 1e-4
+    st["exp_avg_sq"] = torch.randn((1, n), device=DEV, generator=g).abs_() * 1e-8
+    wins = [(0, 40000), (2**31 - 20000, 2**31 + 10000), (n - 40001, n)]
+    assert all(0 <= a < b <= n for a, b in wins)
+    flat = lambda t: t.detach().reshape(-1)
+    before = [(flat(p)[a:b].cpu().numpy().copy(), flat(st["exp_avg"])[a:b].cpu().numpy().copy(),
+               flat(st["exp_avg_sq"])[a:b].cpu().numpy().copy(),
+               flat(w.grad)[a:b].view(torch.int16).cpu().numpy().view(np.uint16).copy()) for a, b in wins]
+    norm = ta.clip_grad_norm([p], None, 1.0)
+    coef = float(opt._pending[0].item())
+    opt.step()
+    torch.cuda.synchronize()
+    gr = flat(w.grad)
+    exact = sum(float((gr[s:s + 2**28].double() ** 2).sum()) for s in range(0, n, 2**28))
+    assert abs(norm.item() - np.sqrt(exact)) <= 1e-6 * np.sqrt(exact)
+    assert coef < 1.0
+    for (a, b), (p0, m0, v0, g0) in zip(wins, before):
+        assert p0.size == b - a
+        out = np.zeros(b - a, np.uint16)
+        oracle.adamw_update_bf16(p0, m0, v0, g0, out, coef, True, 1001.0, 3e-4, 0.9, 0.95, 0.1, 1e-8)
+        assert np.array_equal(flat(p)[a:b].cpu().numpy(), p0), (a, b)
+        assert np.array_equal(flat(st["exp_avg"])[a:b].cpu().numpy(), m0), (a, b)
+        assert np.array_equal(flat(st["exp_avg_sq"])[a:b].cpu().numpy(), v0), (a, b)
+        assert np.array_equal(flat(w)[a:b].view(torch.int16).cpu().numpy().view(np.uint16), out), (a, b)
+    assert float(st["step"]) == 1001.0
+    del p, w, opt, st, gr
+    torch.cuda.empty_cache()
+
+
 def test_full_size_config3_fp32_accumulation():
     """Config 3 at full size (Qwen3-0.6B shapes, 596M params): four bf16 micro-steps
     accumulated into fp32 .grad (the last one also measuring the norm), grads scaled
