@@ -75,6 +75,40 @@ def test_ce_rows_kernel_vs_fp64(vocab):
     assert np.all(grad_bits[~valid] == 0)
 
 
+def test_ce_rows_beyond_one_launch():
+    """More rows than one launch of 1024-thread blocks holds (2^32 work-items): the
+    entry point splits them, and every row still matches an fp64 restatement (here in
+    torch float64 on the device, over all 4.2M rows)."""
+    from torchure_amd import _native
+
+    rows, v = 0xFFFFFFFF // 1024 + 2001, 16
+    g = torch.Generator(device=DEV).manual_seed(11)
+    # unit-scale logits: no row has a softmax entry within 1e-4 of 1, where fp32's
+    # p - 1 cancels (the reference's fp32 softmax loses the same bits there)
+    logits = torch.randn(rows, v, device=DEV, generator=g).to(torch.bfloat16)
+    labels = torch.randint(0, v, (rows,), device=DEV, generator=g)
+    labels[::1009] = -100
+    xd = logits.double()
+    work = logits.clone()
+    loss = torch.empty(rows, dtype=torch.float32, device=DEV)
+    rc = _native.lib().tm_ce_rows_bf16(work.data_ptr(), v, labels.data_ptr(), rows, v, -100,
+                                       loss.data_ptr(), _native.stream_handle(DEV))
+    _native.check(rc, "tm_ce_rows_bf16")
+    valid = labels != -100
+    lse = torch.logsumexp(xd, dim=1)
+    picked = xd.gather(1, labels.clamp(min=0)[:, None])[:, 0]
+    want = torch.where(valid, lse - picked, torch.zeros_like(lse))
+    torch.testing.assert_close(loss.double(), want, rtol=1e-6, atol=1e-6)
+    probs = torch.exp(xd - lse[:, None])
+    probs[valid.nonzero()[:, 0], labels[valid]] -= 1.0
+    probs[~valid] = 0.0
+    want_bits = probs.float().to(torch.bfloat16).view(torch.int16).int()
+    diff = (work.view(torch.int16).int() - want_bits).abs()
+    assert int(diff.max()) <= 1
+    assert float((diff == 0).double().mean()) > 0.99
+    del xd, probs
+
+
 @pytest.mark.parametrize("chunk", [None, 300])
 def test_fused_linear_ce_matches_reference_composition(chunk):
     from torchure_amd.loss import fused_linear_cross_entropy

@@ -569,6 +569,30 @@ def test_cached_norm_invalidated_by_inplace_change():
     assert abs(n2 - want) <= 1e-6 * want and abs(n2 - n1) > 1e-3 * n1
 
 
+def test_accumulate_rejects_before_touching_any_grad():
+    """A bad entry anywhere in the list raises before any p.grad is created or written,
+    so the params ahead of it keep their grads (here: none, and one existing)."""
+    from torchure_amd.optimizer.working import accumulate_grads_
+
+    a = torch.nn.Parameter(torch.randn(64, device=DEV))
+    b = torch.nn.Parameter(torch.randn(64, device=DEV))
+    bad = torch.nn.Parameter(torch.randn(64, device=DEV, dtype=torch.float16))
+    for p in (a, b, bad):
+        w = torch.zeros(64, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+        w.grad = torch.ones(64, device=DEV, dtype=torch.bfloat16)
+        p._tm_working = w
+    b.grad = torch.full((64,), 3.0, device=DEV)
+    with pytest.raises(RuntimeError, match="float32"):
+        accumulate_grads_([a, b, bad])
+    assert a.grad is None
+    assert torch.equal(b.grad, torch.full((64,), 3.0, device=DEV))
+    assert a._tm_working.grad is not None and b._tm_working.grad is not None
+    accumulate_grads_([a, b])
+    assert torch.equal(a.grad, torch.ones(64, device=DEV))
+    assert torch.equal(b.grad, torch.full((64,), 4.0, device=DEV))
+    assert a._tm_working.grad is None and bad._tm_working.grad is not None
+
+
 def test_ragged_full_size_three_chained_steps():
     """Config 5 at full size: 10,000 tensors, ~1.02e10 elements (~163 GB resident),
     ~30% odd lengths, 40% 1-D (no decay), 1% all-zero grads; three chained steps.

@@ -475,18 +475,23 @@ int tm_ce_rows_bf16(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int
                    (long long)rows, (long long)vocab, (long long)ld);
   if (rows == 0) return TM_OK;
   if (!d_logits || !d_labels || !d_row_loss) return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: null pointer");
-  if (rows > 0x7FFFFFFFll) return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: too many rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool regs = TM_CE_REG_ROWS && (vocab >> 3) <= static_cast<int64_t>(kRowThreadsRegs) * kRegCols;
-  if (regs)
-    hipLaunchKernelGGL((ce_rows_kernel<true, kRowThreadsRegs>), dim3(static_cast<uint32_t>(rows)),
-                       dim3(kRowThreadsRegs), 0, s, d_logits, ld, d_labels, vocab, ignore_index,
-                       d_row_loss);
-  else
-    hipLaunchKernelGGL((ce_rows_kernel<false, kRowThreadsStream>), dim3(static_cast<uint32_t>(rows)),
-                       dim3(kRowThreadsStream), kStreamLds, s, d_logits, ld, d_labels, vocab,
-                       ignore_index, d_row_loss);
-  return ce_check_launch("ce_rows_kernel");
+  // One block per row, and a launch holds fewer than 2^32 work-items: longer row lists
+  // (small vocabularies in one chunk) go in several launches.
+  const int64_t max_rows = 0xFFFFFFFFll / (regs ? kRowThreadsRegs : kRowThreadsStream);
+  for (int64_t r0 = 0; r0 < rows; r0 += max_rows) {
+    const uint32_t nr = static_cast<uint32_t>(rows - r0 < max_rows ? rows - r0 : max_rows);
+    uint16_t* lg = d_logits + r0 * ld;
+    if (regs)
+      hipLaunchKernelGGL((ce_rows_kernel<true, kRowThreadsRegs>), dim3(nr), dim3(kRowThreadsRegs), 0, s,
+                         lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
+    else
+      hipLaunchKernelGGL((ce_rows_kernel<false, kRowThreadsStream>), dim3(nr), dim3(kRowThreadsStream),
+                         kStreamLds, s, lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
+    if (int rc = ce_check_launch("ce_rows_kernel")) return rc;
+  }
+  return TM_OK;
 }
 
 int tm_ce_loss(const float* d_row_loss, const int64_t* d_labels, int64_t rows, int64_t ignore_index,

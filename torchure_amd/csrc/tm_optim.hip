@@ -648,7 +648,11 @@ int check_table(const void* d_tensors, int64_t n_tensors, const void* d_chunks, 
   if (n_tensors > 0 && !d_tensors) return fail(TM_EINVAL, "%s: null tensor table", who);
   if (n_chunks > 0 && !d_chunks) return fail(TM_EINVAL, "%s: null chunk table", who);
   if (n_tensors > 0xFFFFFFFFll) return fail(TM_EINVAL, "%s: too many tensors", who);
-  if (n_chunks > 0x7FFFFFFFll) return fail(TM_EINVAL, "%s: too many chunks", who);
+  // One block per chunk, and a launch holds fewer than 2^32 work-items: at most 16,777,215
+  // chunks (2.7e11 elements at the default 16,384-element chunk, beyond what HBM holds).
+  if (n_chunks > 0xFFFFFFFFll / kThreads)
+    return fail(TM_EINVAL, "%s: %lld chunks, at most %lld per launch (use larger chunks)", who,
+                (long long)n_chunks, (long long)(0xFFFFFFFFll / kThreads));
   if (chunk_elems <= 0 || chunk_elems % TM_CHUNK_ALIGN != 0 || chunk_elems > (int64_t(1) << 30))
     return fail(TM_EINVAL, "%s: chunk_elems %lld must be a positive multiple of %d, <= 2^30", who,
                 (long long)chunk_elems, TM_CHUNK_ALIGN);

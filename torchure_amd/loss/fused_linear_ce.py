@@ -58,10 +58,14 @@ class _FusedLinearCE(torch.autograd.Function):
         if weight.shape[1] != d or labels.shape[0] != n:
             raise RuntimeError(f"{who}: shapes hidden {tuple(hidden.shape)}, weight {tuple(weight.shape)}, "
                                f"labels {tuple(labels.shape)} do not match")
+        if weight.device != hidden.device or labels.device != hidden.device:
+            raise RuntimeError(f"{who}: hidden, weight and labels must be on one device")
+        chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
+        if chunk < 1:
+            raise ValueError(f"{who}: chunk_size must be positive, got {chunk_size}")
         lib = _native.lib()
         stream = _native.stream_handle(hidden.device)
         w = weight.to(hidden.dtype).contiguous()  # cast once, not per chunk
-        chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
         grad_hidden = torch.empty_like(hidden)
         want_w = weight.requires_grad
         # fp32 grad_W holds chunks 0..k-2; chunk k-1 stays bf16 until backward

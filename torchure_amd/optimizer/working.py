@@ -153,34 +153,41 @@ def accumulate_grads_(params, *, last: bool = False,
     """
     who = "accumulate_grads_"
     params = list(params)
-    accs, micros, assign = [], [], []
+    todo = []  # (param, its fp32 accumulator or None on a first micro-step, bf16 micro grad or None)
     for p in params:
         w = getattr(p, "_tm_working", None)
         mg = w.grad if w is not None else None
-        if mg is None and (not last or p.grad is None):
+        g = p.grad
+        if mg is None and (not last or g is None):
             continue
         tables.require_device_tensor(p, who, "param")
-        fresh = p.grad is None
-        if fresh:  # the kernel assigns the first micro-grad: no zero fill, no read
-            p.grad = torch.empty_like(p, memory_format=torch.contiguous_format)
-        g = p.grad
-        tables.require_device_tensor(g, who, "fp32 accumulator")
-        if g.dtype != torch.float32:
-            raise RuntimeError(f"{who}: the accumulator (p.grad) must be float32, got {g.dtype}")
+        dt = p.dtype if g is None else g.dtype
+        if g is not None:
+            tables.require_device_tensor(g, who, "fp32 accumulator")
+        if dt != torch.float32:
+            raise RuntimeError(f"{who}: the accumulator (p.grad) must be float32, got {dt}")
         if mg is not None:
             tables.require_device_tensor(mg, who, "bf16 micro-step grad")
-            if mg.dtype != torch.bfloat16 or mg.numel() != g.numel() or mg.device != g.device:
+            if mg.dtype != torch.bfloat16 or mg.numel() != p.numel() or mg.device != p.device:
                 raise RuntimeError(f"{who}: micro-step grad must be bf16 of the param's size and device")
-        accs.append(g)
-        micros.append(mg)
-        assign.append(fresh)
-    if not accs:
+        todo.append((p, g, mg))
+    if not todo:
         if last:
             raise AssertionError(f"{who}: no grads to accumulate or measure")
         return None
-    device = accs[0].device
-    if any(a.device != device for a in accs):
+    device = todo[0][0].device
+    if any(p.device != device for p, _, _ in todo):
         raise RuntimeError(f"{who}: all params must be on one device")
+    # Every check has passed: only now give first micro-steps their accumulator, which the
+    # kernel assigns (no zero fill, no read), so an error above leaves no p.grad behind.
+    accs, micros, assign = [], [], []
+    for p, g, mg in todo:
+        fresh = g is None
+        if fresh:
+            g = p.grad = torch.empty_like(p, memory_format=torch.contiguous_format)
+        accs.append(g)
+        micros.append(mg)
+        assign.append(fresh)
     drop_cached_norm(device)
     rows = np.zeros(len(accs), dtype=_native.ACCUM_DTYPE)
     rows["acc"] = np.asarray([a.data_ptr() for a in accs], dtype=np.uint64)
