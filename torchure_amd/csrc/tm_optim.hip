@@ -104,15 +104,26 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
   return (f != f) ? 0x7FC0u : r;
 }
 
+// Vector accesses go through global-address-space pointers. The arrays' addresses come
+// from the tensor table as plain integers, so the compiler would otherwise emit FLAT
+// instructions, which count in both vmcnt and lgkmcnt and can only be waited for all at
+// once: every first use of a loaded value then drained every load and store in flight.
+// Global instructions count in vmcnt only, in order, so a wave keeps its other loads and
+// its stores outstanding while it computes (the update measured 0.3-0.5% faster in every
+// HBM region; the mixed read/write stream, not the waits, bounds it). Every buffer here is
+// device-visible global memory (never LDS or scratch), which global instructions address.
+#define TM_GLOBAL __attribute__((address_space(1)))
 template <bool kNT, typename T>
 __device__ __forceinline__ T ld(const T* p) {
-  if constexpr (kNT) return __builtin_nontemporal_load(p);
-  else return *p;
+  const TM_GLOBAL T* g = (const TM_GLOBAL T*)p;
+  if constexpr (kNT) return __builtin_nontemporal_load(g);
+  else return *g;
 }
 template <bool kNT, typename T>
 __device__ __forceinline__ void st(T* p, T v) {
-  if constexpr (kNT) __builtin_nontemporal_store(v, p);
-  else *p = v;
+  TM_GLOBAL T* g = (TM_GLOBAL T*)p;
+  if constexpr (kNT) __builtin_nontemporal_store(v, g);
+  else *g = v;
 }
 
 // One AdamW element. p, m, v are the fp32 values in memory; g is the (clipped) fp32
