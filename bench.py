@@ -45,7 +45,8 @@ def parse():
     ap.add_argument("--cpu-sample-blocks", type=int, default=2,
                     help="transformer blocks of the config timed for the CPU baseline (0 = skip)")
     ap.add_argument("--cpu-steps", type=int, default=3)
-    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,qwen3-4b-dropin,ragged",
+    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,qwen3-4b-dropin,"
+                                      "qwen3-4b-ddpbuckets,ragged",
                     help="comma list of extra configs reported under 'extra' (empty = none)")
     ap.add_argument("--mode", choices=("bench", "kernels", "ce"), default="bench",
                     help="kernels: only the norm and update launches, --reps times each, plus a "
@@ -193,12 +194,45 @@ def run_gpu(config: str, steps: int, warmup: int, chunk_elems, dev):
     return out
 
 
-def run_gpu_dropin(config: str, steps: int, warmup: int, chunk_elems, dev):
+def ddp_bucket_grads(params, bucket_mb: int = 25) -> int:
+    """Gives ``params`` fp32 grads laid out as torchure's DDP leaves them after a sync
+    (torchure/parallelism/data_parallel.py:53-66,86-105,120-130): buckets in reverse
+    parameter order, closed before a param that would push them past ``bucket_mb`` MiB; a
+    bucket of several params is one flat buffer and each ``.grad`` is a view of it, a
+    bucket of one param keeps that param's own grad tensor. Returns the bucket count."""
+    import torch
+
+    cap = bucket_mb * 1024 * 1024
+    runs, run, run_bytes = [], [], 0
+    for p in reversed(params):
+        nb = p.numel() * p.element_size()
+        if run and run_bytes + nb > cap:
+            runs.append(run)
+            run, run_bytes = [], 0
+        run.append(p)
+        run_bytes += nb
+    if run:
+        runs.append(run)
+    for run in runs:
+        if len(run) == 1:
+            continue
+        flat = torch.empty(sum(p.numel() for p in run), dtype=torch.float32, device=run[0].device)
+        off = 0
+        for p in run:
+            view = flat[off: off + p.numel()].view_as(p)
+            view.copy_(p.grad)
+            p.grad = view
+            off += p.numel()
+    return len(runs)
+
+
+def run_gpu_dropin(config: str, steps: int, warmup: int, chunk_elems, dev, buckets: bool = False):
     """The plain drop-in configuration: fp32 masters with fp32 .grad (what autograd
     leaves when the model trains on fp32 params under autocast, as the reference's
     trainer does), no bf16 working copies. One step = clip_grad_norm (norm pass,
     4 B/param) + AdamW.step() with the clip fused (28 B/param: read g/p/m/v, write
-    p/m/v) = 32 B/param."""
+    p/m/v) = 32 B/param. With ``buckets`` the grads are views into DDP's flat bucket
+    buffers (``ddp_bucket_grads``), the layout the step reads after a multi-GPU sync."""
     import torch
 
     import torchure_amd as ta
@@ -210,6 +244,7 @@ def run_gpu_dropin(config: str, steps: int, warmup: int, chunk_elems, dev):
     params = [torch.nn.Parameter(torch.randn(s, device=dev, generator=g) * 0.02) for s in shapes]
     for p in params:
         p.grad = torch.randn(p.shape, device=dev, generator=g) * 1e-3
+    n_buckets = ddp_bucket_grads(params) if buckets else None
     opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
                              {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True,
                               "chunk_elems": chunk_elems or tables.DEFAULT_CHUNK_ELEMS})
@@ -234,9 +269,12 @@ def run_gpu_dropin(config: str, steps: int, warmup: int, chunk_elems, dev):
     n = sum(p.numel() for p in params)
     del params, opt
     torch.cuda.empty_cache()
-    return dict(config=config + "-dropin-fp32grads", n_params=n, ms_per_step=round(ms, 4),
-                bytes_per_param=32, GBps=round(32 * n / (ms * 1e-3) / 1e9, 1),
-                frac_of_peak=round(32 * n / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+    out = dict(config=config + ("-ddp-buckets-fp32grads" if buckets else "-dropin-fp32grads"), n_params=n,
+               ms_per_step=round(ms, 4), bytes_per_param=32, GBps=round(32 * n / (ms * 1e-3) / 1e9, 1),
+               frac_of_peak=round(32 * n / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4))
+    if buckets:
+        out["ddp_buckets_25MiB"] = n_buckets
+    return out
 
 
 def run_gpu_fp32acc(config: str, steps: int, warmup: int, chunk_elems, dev):
@@ -509,8 +547,10 @@ def main():
     print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
     extra = {}
     for cfg in [c for c in args.also.split(",") if c and c != args.config]:
-        if cfg.endswith("-dropin"):
-            r = run_gpu_dropin(cfg[: -len("-dropin")], args.steps, args.warmup, args.chunk_elems, dev)
+        if cfg.endswith("-dropin") or cfg.endswith("-ddpbuckets"):
+            bucketed = cfg.endswith("-ddpbuckets")
+            base_cfg = cfg.rsplit("-", 1)[0]
+            r = run_gpu_dropin(base_cfg, args.steps, args.warmup, args.chunk_elems, dev, buckets=bucketed)
             extra[cfg] = r
             print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
             continue

@@ -178,3 +178,25 @@ def test_host_list_primitives():
     with pytest.raises(TypeError):
         h.ptrs([1])
     assert isinstance(ptr, np.ndarray)
+
+
+def test_bench_ddp_bucket_layout():
+    """bench.py's DDP bucket leg lays grads out as torchure's DDP does
+    (torchure/parallelism/data_parallel.py:86-105): reverse parameter order, a bucket closes
+    before the param that would push it past the cap, and only multi-param buckets get a
+    flat buffer whose views become the grads (values kept)."""
+    import bench
+
+    sizes = [100_000, 200_000, 50_000, 300_000, 10_000]  # fp32: 0.4, 0.8, 0.2, 1.2, 0.04 MB
+    ps = [torch.nn.Parameter(torch.zeros(n)) for n in sizes]
+    for i, p in enumerate(ps):
+        p.grad = torch.full((p.numel(),), float(i))
+    own = [p.grad for p in ps]
+    # reversed: [10k] | [300k] | [50k, 200k] (1,000,000 B <= 1 MiB) | [100k]
+    assert bench.ddp_bucket_grads(ps, bucket_mb=1) == 4
+    for i in (0, 3, 4):
+        assert ps[i].grad is own[i]
+    g50, g200 = ps[2].grad, ps[1].grad
+    assert g50.untyped_storage().data_ptr() == g200.untyped_storage().data_ptr()
+    assert g200.data_ptr() == g50.data_ptr() + 4 * 50_000
+    assert torch.equal(g50, torch.full((50_000,), 2.0)) and torch.equal(g200, torch.full((200_000,), 1.0))
