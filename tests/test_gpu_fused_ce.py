@@ -8,7 +8,9 @@ Checks:
 - the whole op (forward + backward through autograd) vs the reference's own
   composition (torchure/loss/fused_linear_ce.py, same torch calls) on the same
   device: same GEMMs, so the loss agrees within 1e-5 relative and the grads
-  within bf16 resolution.
+  within bf16 resolution;
+- the reference's own test cases (tests/fused_linear_ce.py), against an unfused
+  lm_head + F.cross_entropy at that test's bars.
 """
 
 from __future__ import annotations
@@ -276,3 +278,47 @@ def test_ce_rows_edge_rows_vs_fp64(v):
     diff = np.abs(grad_bits.astype(np.int32) - want_bits.astype(np.int32))
     assert diff.max() <= 1, (diff.max(), np.argwhere(diff > 1)[:4])
     assert np.all(grad_bits[0, ::3] == 0)  # exp(-inf) = 0 exactly
+
+
+@pytest.mark.parametrize("b,s,d,v,chunk,ignore_frac", [
+    (2, 128, 64, 1000, 64, 0.1),          # uneven chunks
+    (2, 256, 128, 5000, 512, 0.0),        # one chunk
+    (2, 4096, 1024, 151936, 1024, 0.05),  # the Qwen3 head at the reference's chunk size
+    (2, 4096, 1024, 151936, None, 0.05),  # the same with this build's default (one chunk)
+])
+def test_reference_cases_vs_plain_cross_entropy(b, s, d, v, chunk, ignore_frac):
+    """The cases and bars of the reference's own test (tests/fused_linear_ce.py:23-56): the
+    op against an unfused lm_head + F.cross_entropy on fp32 logits, through autograd, with
+    bf16 hidden states and an fp32 head weight: |loss difference| < 2e-3 * max(1, loss) and
+    relative L2 error of both grads < 3e-2. The unfused side uses 2-D products only."""
+    import torch.nn.functional as F
+
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    torch.manual_seed(0)
+    hidden = torch.randn(b, s, d, device=DEV, dtype=torch.bfloat16) * 0.5
+    weight = torch.randn(v, d, device=DEV, dtype=torch.float32) * 0.02
+    labels = torch.randint(0, v, (b, s), device=DEV)
+    labels[torch.rand(b, s, device=DEV) < ignore_frac] = -100
+
+    h1 = hidden.clone().requires_grad_(True)
+    w1 = weight.clone().requires_grad_(True)
+    logits = h1.reshape(-1, d) @ w1.to(torch.bfloat16).t()
+    loss_ref = F.cross_entropy(logits.float(), labels.reshape(-1), ignore_index=-100)
+    loss_ref.backward()
+    del logits
+
+    h2 = hidden.clone().requires_grad_(True)
+    w2 = weight.clone().requires_grad_(True)
+    loss = fused_linear_cross_entropy(h2, w2, labels, -100, chunk)
+    loss.backward()
+
+    def rel(a, b_):
+        return float((a.float() - b_.float()).norm() / b_.float().norm().clamp_min(1e-12))
+
+    dh, dw = rel(h2.grad, h1.grad), rel(w2.grad, w1.grad)
+    print(f"V={v} chunk={chunk}: loss {loss.item():.6f} vs {loss_ref.item():.6f}, rel dh {dh:.2e}, dw {dw:.2e}")
+    assert abs(loss_ref.item() - loss.item()) < 2e-3 * max(1.0, loss_ref.item())
+    assert dh < 3e-2
+    assert dw < 3e-2
+    assert h2.grad.dtype == torch.bfloat16 and w2.grad.dtype == torch.float32
