@@ -380,6 +380,63 @@ def test_reference_clip_known_answers():
     assert torch.equal(ps[0].grad, ref)
 
 
+def test_shard_dims_of_size_one():
+    """clip_grad_norm with shard_dims naming mesh dimensions of size 1. The reference's sharded
+    path (torchure/core/grad_helper.py:20-24) squares the norm, sums it over each dimension
+    (the identity for one rank) and takes the root. Checked: the sharded case of
+    tests/grad_helper.py:163-185 at one rank; bitwise equality with the local path for an
+    ordinary norm (eager and deferred clip); inf, and a zero coefficient, once the fp32 square
+    overflows, as torch's ops give."""
+    import torchure_amd as ta
+
+    class Mesh:
+        def size(self, dim):
+            return 1
+
+    def params_with(grads):
+        out = []
+        for g in grads:
+            p = torch.nn.Parameter(torch.zeros_like(g, device=DEV))
+            p.grad = g.to(DEV).clone()
+            out.append(p)
+        return out
+
+    full = torch.arange(1, 5, dtype=torch.float32)
+    true = full.norm()
+    mx = (true / 2).item()
+    ps = params_with([full])
+    total = ta.clip_grad_norm(ps, Mesh(), mx, shard_dims=("dp",))
+    torch.testing.assert_close(total.cpu(), true, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(ps[0].grad.cpu(), full * (mx / true), rtol=1e-5, atol=1e-6)
+
+    gen = torch.Generator().manual_seed(5)
+    grads = [torch.randn(1000, generator=gen) * 3e-3, torch.randn(37, 11, generator=gen)]
+    a, b = params_with(grads), params_with(grads)
+    na = ta.clip_grad_norm(a, None, 1.0)
+    nb = ta.clip_grad_norm(b, Mesh(), 1.0, shard_dims=("dp", "tp"))
+    assert na.view(torch.int32).item() == nb.view(torch.int32).item()
+    for pa, pb in zip(a, b):
+        assert torch.equal(pa.grad, pb.grad)
+    # the same through an optimizer that defers the clip into its step
+    a, b = params_with(grads), params_with(grads)
+    opt_a = ta.build_optimizer(torch.nn.ParameterList(a), "adamw", {"lr": 1e-3, "fused": True})
+    opt_b = ta.build_optimizer(torch.nn.ParameterList(b), "adamw", {"lr": 1e-3, "fused": True})
+    ta.clip_grad_norm(a, None, 1.0)
+    ta.clip_grad_norm(b, Mesh(), 1.0, shard_dims=("dp",))
+    opt_a.step()
+    opt_b.step()
+    for pa, pb in zip(a, b):
+        assert torch.equal(pa, pb)
+
+    big = torch.tensor([1e20, 0.0, -3.0])
+    ps = params_with([big])
+    total = ta.clip_grad_norm(ps, Mesh(), 1.0, shard_dims=("dp",))
+    ref_total = (torch.linalg.vector_norm(big.to(DEV)) ** 2.0) ** 0.5
+    ref_coef = torch.clamp(1.0 / (ref_total + 1e-6), max=1.0)
+    assert math.isinf(total.item()) and math.isinf(ref_total.item())
+    assert torch.equal(ps[0].grad, big.to(DEV) * ref_coef)
+
+
 def test_skip_params_without_grad_and_zero_numel():
     import torchure_amd as ta
 

@@ -89,6 +89,20 @@ def test_clip_errors():
     with pytest.raises(NotImplementedError):
         ta.clip_grad_norm([p], None, 1.0, shard_dims=("dp",))
 
+    class Mesh:  # the MeshLike surface clip_grad_norm reads (torchure/core/collective.py:66-85)
+        def __init__(self, sizes):
+            self.sizes = sizes
+
+        def size(self, dim):
+            return self.sizes[dim]
+
+    # a shard dimension with more than one rank needs a collective: rejected before any work
+    with pytest.raises(NotImplementedError, match="'fsdp' has 2 ranks"):
+        ta.clip_grad_norm([p], Mesh({"dp": 1, "fsdp": 2}), 1.0, shard_dims=("dp", "fsdp"))
+    # size-1 dimensions pass the check and reach the device path (no GPU here)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        ta.clip_grad_norm([p], Mesh({"dp": 1}), 1.0, shard_dims=("dp",))
+
 
 def test_wsd_scheduler_matches_closed_form():
     m = _model()

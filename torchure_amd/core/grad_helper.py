@@ -127,19 +127,32 @@ def scale_grads_(
     _native.host().bump(grads)
 
 
+def _check_shard_dims(mesh, shard_dims) -> None:
+    """The sharded path (grad_helper.py:20-24) sums the squared norm over each listed mesh
+    dimension. A dimension of size 1 makes that sum the identity; larger ones need a
+    cross-GPU all_reduce, which this single-GPU build does not provide."""
+    for dim in shard_dims:
+        size = mesh.size(dim) if mesh is not None else None
+        if size != 1:
+            raise NotImplementedError(
+                f"clip_grad_norm: shard dim {dim!r} has {size} ranks; summing the squared norm "
+                "across GPUs needs a collective, and this single-GPU build has none (a mesh "
+                "dimension of size 1 is supported)")
+
+
 def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
     """Returns the pre-clip global grad norm; clips grads (in place or deferred).
 
     Signature and semantics of torchure/core/grad_helper.py:8-34. ``mesh`` is
-    unused on the local path, as in the reference. ``shard_dims`` (the sharded
-    sum-of-squares all-reduce, grad_helper.py:20-24) needs collectives, which
-    this single-GPU build does not provide.
+    unused on the local path, as in the reference. ``shard_dims`` may name mesh
+    dimensions of size 1, over which the reference's all-reduce of the squared norm
+    is the identity; the norm still takes its ``(total ** 2) ** 0.5`` round trip
+    (grad_helper.py:20-24), which keeps its bits while the fp32 square neither
+    overflows nor underflows, and gives inf above sqrt(FLT_MAX) as the reference does.
+    Larger shard dimensions raise NotImplementedError.
     """
     if shard_dims:
-        raise NotImplementedError(
-            "clip_grad_norm: shard_dims needs a cross-GPU all_reduce of the squared norm; "
-            "this single-GPU build supports only the local path (shard_dims=())"
-        )
+        _check_shard_dims(mesh, shard_dims)
     grads, holders = grads_of(params)
     if not grads:
         assert grads, "clip_grad_norm got no grads; backward didn't run, or all params are frozen"
@@ -152,19 +165,21 @@ def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
 
     from torchure_amd.optimizer.working import cached_norm
 
+    # the last micro-step's fused accumulate+norm may already have measured exactly these grads
     norm = cached_norm(grads)
-    if norm is not None:
-        # the last micro-step's fused accumulate+norm already measured exactly these grads
-        coef = None
-        if max_norm is not None:
-            coef = torch.empty((), dtype=torch.float32, device=norm.device)
-            rc = _native.lib().tm_clip_coef(norm.data_ptr(), float(max_norm), coef.data_ptr(),
-                                            _native.stream_handle(norm.device))
-            _native.check(rc, "tm_clip_coef")
-    else:
-        norm, coef = grad_norm_launch(grads, max_norm)
+    coef = None
+    if norm is None:
+        norm, coef = grad_norm_launch(grads, None if shard_dims else max_norm)
+    if shard_dims:
+        # grad_helper.py:21-24 with the sum over size-1 dimensions being the identity
+        norm = (norm ** 2.0) ** (1.0 / 2.0)
     if max_norm is None:
         return norm
+    if coef is None:  # the coefficient of a norm that is already on the device
+        coef = torch.empty((), dtype=torch.float32, device=norm.device)
+        rc = _native.lib().tm_clip_coef(norm.data_ptr(), float(max_norm), coef.data_ptr(),
+                                        _native.stream_handle(norm.device))
+        _native.check(rc, "tm_clip_coef")
 
     opt = next(iter(owners)) if len(owners) == 1 else None
     if opt is not None and opt.defer_clip:
