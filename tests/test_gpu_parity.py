@@ -851,6 +851,72 @@ def test_checkpoint_file_roundtrip_continues_bit_exact(tmp_path):
             assert ob.state[b][k].device == b.device
 
 
+def test_checkpoint_from_non_fused_torch_adamw(tmp_path):
+    """A checkpoint written by torch's default (foreach, non-fused) AdamW keeps `step` as a
+    CPU tensor and `fused=None` in its groups, so torch's load policy leaves `step` where it
+    is (torch/optim/optimizer.py:770-799) and copies `fused=None` over the loading
+    optimizer's groups (torch's own fused AdamW then continues with the foreach recipe).
+    Loaded into this AdamW, the groups say fused again, the first step moves `step` to the
+    param's device as fp32, and the result equals torch's fused AdamW given the same state
+    (its groups set back to fused and its steps moved to the device, which its fused path
+    needs)."""
+    import torchure_amd as ta
+
+    gen = torch.Generator(device=DEV).manual_seed(41)
+    shapes = [(64, 32), (32,), (17, 5)]
+    init = [torch.randn(s, device=DEV, generator=gen) * 0.02 for s in shapes]
+    grads = [[torch.randn(s, device=DEV, generator=gen) * 1e-3 for s in shapes] for _ in range(3)]
+
+    def groups_of(ps):
+        return [{"params": [p for p in ps if p.dim() >= 2], "weight_decay": 0.1},
+                {"params": [p for p in ps if p.dim() < 2], "weight_decay": 0.0}]
+
+    src = [torch.nn.Parameter(t.clone()) for t in init]
+    topt = torch.optim.AdamW(groups_of(src), lr=3e-4, betas=(0.9, 0.95))  # foreach on the GPU
+    for k in range(2):
+        for p, g in zip(src, grads[k]):
+            p.grad = g.clone()
+        topt.step()
+    sd = topt.state_dict()
+    assert all(st["step"].device.type == "cpu" for st in sd["state"].values())
+    torch.save(sd, tmp_path / "optimizer.pt")
+
+    def resumed(make):
+        ps = [torch.nn.Parameter(p.detach().clone()) for p in src]
+        opt = make(ps)
+        opt.load_state_dict(torch.load(tmp_path / "optimizer.pt", map_location="cpu", weights_only=True))
+        for p, g in zip(ps, grads[2]):
+            p.grad = g.clone()
+        opt.step()
+        return ps, opt
+
+    mine, mopt = resumed(lambda ps: ta.build_optimizer(torch.nn.ParameterList(ps), "adamw",
+                                                       {"lr": 3e-4, "weight_decay": 0.1,
+                                                        "betas": (0.9, 0.95), "fused": True}))
+    def fused_torch(ps):
+        opt = torch.optim.AdamW(groups_of(ps), lr=3e-4, betas=(0.9, 0.95), fused=True)
+        load = opt.load_state_dict
+
+        def load_as_fused(sd):
+            load(sd)
+            for g in opt.param_groups:
+                g["fused"], g["foreach"] = True, None
+            for st in opt.state.values():
+                st["step"] = st["step"].to(device=DEV, dtype=torch.float32)
+        opt.load_state_dict = load_as_fused
+        return opt
+
+    ref, ropt = resumed(fused_torch)
+    assert all(g["fused"] is True and g["foreach"] is None for g in mopt.state_dict()["param_groups"])
+    torch.cuda.synchronize()
+    for a, b in zip(mine, ref):
+        assert torch.equal(a, b)
+        sa, sb = mopt.state[a], ropt.state[b]
+        assert sa["step"].device == a.device and sa["step"].dtype == torch.float32
+        assert sa["step"].item() == 3.0 and sb["step"].item() == 3.0
+        assert torch.equal(sa["exp_avg"], sb["exp_avg"]) and torch.equal(sa["exp_avg_sq"], sb["exp_avg_sq"])
+
+
 def test_grads_as_views_into_flat_buckets():
     """DDP-style flat grad buckets (torchure/parallelism/data_parallel.py:53-66): grads
     are views into one flat fp32 buffer at arbitrary offsets, including ones that

@@ -54,7 +54,8 @@ def test_param_groups_have_torch_adamw_keys():
 
 def test_load_torch_cpu_state_dict():
     """A checkpoint of torch.optim.AdamW (what torchure's Checkpointer saves)
-    loads into the drop-in with identical state tensors and groups."""
+    loads into the drop-in with identical state tensors and groups, except that the
+    groups say fused (and foreach None), which is what this optimizer runs."""
     m = _model()
     ref = torch.optim.AdamW(m.parameters(), lr=1e-3)
     for _ in range(3):
@@ -65,7 +66,7 @@ def test_load_torch_cpu_state_dict():
     mine = AdamW(m.parameters(), lr=1e-3)
     mine.load_state_dict(sd)
     got = mine.state_dict()
-    assert got["param_groups"] == sd["param_groups"]
+    assert got["param_groups"] == [dict(g, fused=True, foreach=None) for g in sd["param_groups"]]
     for k in sd["state"]:
         for key in ("step", "exp_avg", "exp_avg_sq"):
             assert torch.equal(got["state"][k][key], sd["state"][k][key])

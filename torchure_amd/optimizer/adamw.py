@@ -399,9 +399,18 @@ class AdamW(torch.optim.Optimizer):
         return _ParamEntry(p, work, state["step"], state["exp_avg"], state["exp_avg_sq"])
 
     def load_state_dict(self, state_dict) -> None:
+        """torch's loader (torch/optim/optimizer.py:877-1014), then the groups say what runs.
+        torch copies the saved groups' flags over the live ones, so a checkpoint of a
+        non-fused AdamW would leave ``fused=None`` here; this optimizer always runs the fused
+        recipe, and its groups say so again (``state_dict()`` then reports what ran). Step
+        counters that torch's policy leaves on the CPU for such checkpoints are moved to the
+        param's device, as fp32, by the first step."""
         self._verified.clear()
         self._plan = None
         super().load_state_dict(state_dict)
+        for group in self.param_groups:
+            group["fused"] = True
+            group["foreach"] = None
 
     def _plan_launches(self, per_dev, hyper, coef) -> list["StepLaunch"]:
         groups_c = _native.hyper_array(hyper)
