@@ -85,7 +85,8 @@ typedef struct tm_tensor {
 } tm_tensor_t;
 
 /* One work item: elements [chunk*chunk_elems, min((chunk+1)*chunk_elems, numel))
- * of tensor `tensor`. */
+ * of tensor `tensor`. A call takes at most 16,777,215 chunks (one 256-thread workgroup
+ * each; a launch holds fewer than 2^32 work-items); larger tables return TM_EINVAL. */
 typedef struct tm_chunk {
   uint32_t tensor;
   uint32_t chunk;
