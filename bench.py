@@ -443,6 +443,13 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
            "flops": flops, "ms": round(timed(ours), 4)}
     out["TFLOPs"] = round(flops / (out["ms"] * 1e-3) / 1e12, 1)
     out["frac_of_bf16_mfma_peak"] = round(out["TFLOPs"] / 2500.0, 4)
+
+    def evaluate():  # no input needs a gradient: the logits GEMM and the row losses only
+        with torch.no_grad():
+            fused_linear_cross_entropy(hidden, weight, labels)
+
+    out["loss_only_ms"] = round(timed(evaluate), 4)
+    out["loss_only_TFLOPs"] = round(2.0 * n * d * v / (out["loss_only_ms"] * 1e-3) / 1e12, 1)
     if with_reference:
         comp = torch.compile(_ce_chunk_reference, dynamic=False)
 

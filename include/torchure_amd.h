@@ -215,6 +215,15 @@ int tm_ce_rows_bf16(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int
                     int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream);
 
 /*
+ * The row losses of tm_ce_rows_bf16 without the gradient: the logits are only read. Same
+ * arithmetic, so the same bits. For a call whose inputs need no gradient (evaluation under
+ * torch.no_grad), where the reference's forward (fused_linear_ce.py:63-93) still computes
+ * and discards the gradients.
+ */
+int tm_ce_rows_loss_bf16(const uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows,
+                         int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream);
+
+/*
  * Deterministic loss reduction (fused_linear_ce.py:76-90): d_out3[0] = sum of row
  * losses, d_out3[1] = n_valid = max(1, count(label != ignore_index)),
  * d_out3[2] = d_out3[0] / d_out3[1] (the mean loss).

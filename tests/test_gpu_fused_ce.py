@@ -322,3 +322,65 @@ def test_reference_cases_vs_plain_cross_entropy(b, s, d, v, chunk, ignore_frac):
     assert dh < 3e-2
     assert dw < 3e-2
     assert h2.grad.dtype == torch.bfloat16 and w2.grad.dtype == torch.float32
+
+
+@pytest.mark.parametrize("vocab", [4096, 1001, 200000])
+def test_loss_only_rows_equal_gradient_rows(vocab):
+    """tm_ce_rows_loss_bf16 gives the row losses of tm_ce_rows_bf16 bit for bit (register,
+    element-wise and streaming paths) and leaves the logits untouched."""
+    from torchure_amd import _native
+
+    g = torch.Generator(device=DEV).manual_seed(vocab)
+    rows = 29
+    logits = (torch.randn(rows, vocab, device=DEV, generator=g) * 3.0).to(torch.bfloat16)
+    labels = torch.randint(0, vocab, (rows,), device=DEV, generator=g)
+    labels[[2, 11]] = -100
+    keep = logits.clone()
+    a = torch.empty(rows, device=DEV)
+    b = torch.empty(rows, device=DEV)
+    lib, s = _native.lib(), _native.stream_handle(DEV)
+    _native.check(lib.tm_ce_rows_loss_bf16(logits.data_ptr(), vocab, labels.data_ptr(), rows, vocab, -100,
+                                           a.data_ptr(), s), "tm_ce_rows_loss_bf16")
+    assert torch.equal(logits.view(torch.int16), keep.view(torch.int16))
+    _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), vocab, labels.data_ptr(), rows, vocab, -100,
+                                      b.data_ptr(), s), "tm_ce_rows_bf16")
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+@pytest.mark.parametrize("chunk", [None, 300])
+def test_loss_without_grad_and_partial_grads(chunk):
+    """Under torch.no_grad the op takes the loss-only path and returns the training path's
+    loss bit for bit. With only the weight (or only the hidden states) requiring a
+    gradient, that gradient equals the one computed with both, bit for bit, and the other
+    input gets none."""
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(3)
+    n, d, v = 1000, 256, 4096
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::23] = -100
+
+    h = hidden.clone().requires_grad_(True)
+    w = weight.clone().requires_grad_(True)
+    loss = fused_linear_cross_entropy(h, w, labels, -100, chunk)
+    loss.backward()
+    with torch.no_grad():
+        eval_loss = fused_linear_cross_entropy(h, w, labels, -100, chunk)
+    assert not eval_loss.requires_grad
+    assert eval_loss.view(torch.int32).item() == loss.detach().view(torch.int32).item()
+    # inputs that require no gradient: the loss-only path too
+    plain = fused_linear_cross_entropy(hidden, weight, labels, -100, chunk)
+    assert plain.view(torch.int32).item() == loss.detach().view(torch.int32).item()
+
+    w_only = weight.clone().requires_grad_(True)
+    l1 = fused_linear_cross_entropy(hidden, w_only, labels, -100, chunk)
+    l1.backward()
+    assert torch.equal(w_only.grad, w.grad)
+    assert l1.detach().view(torch.int32).item() == loss.detach().view(torch.int32).item()
+
+    h_only = hidden.clone().requires_grad_(True)
+    l2 = fused_linear_cross_entropy(h_only, weight, labels, -100, chunk)
+    l2.backward()
+    assert torch.equal(h_only.grad.view(torch.int16), h.grad.view(torch.int16))

@@ -196,8 +196,9 @@ __device__ __forceinline__ float block_sum_f(float s) {
 }
 
 // logits: rows x vocab bf16 (row-major, row stride ld elements), overwritten with
-// grad_logits. labels: int64 per row. row_loss: fp32 per row (0 for ignored rows).
-template <bool kInRegs, int kCeThreads>
+// grad_logits (kGrad; without it the logits are only read). labels: int64 per row.
+// row_loss: fp32 per row (0 for ignored rows).
+template <bool kInRegs, int kCeThreads, bool kGrad>
 __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restrict__ logits,
                                                              int64_t ld,
                                                              const int64_t* __restrict__ labels,
@@ -301,6 +302,7 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
   // host synchronisation. Its gradient row is the plain softmax.
   const bool in_range = label >= 0 && label < vocab;
   if (threadIdx.x == 0) row_loss[r] = !valid ? 0.0f : (in_range ? lse - target : __builtin_nanf(""));
+  if constexpr (!kGrad) return;  // loss only: no gradient pass (no barrier follows)
 
   // grad = exp(x - lse) on valid rows (0 on ignored rows), minus 1 at the label.
   auto g_of = [&](float x, int64_t idx) -> float {
@@ -464,34 +466,50 @@ int ce_check_launch(const char* what) {
   return TM_OK;
 }
 
+// One block per row. The kernel (register or streaming path) depends only on the vocabulary,
+// so the loss-only pass runs the same arithmetic as the gradient pass and gives the same bits.
+template <bool kGrad>
+int ce_rows_launch(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows, int64_t vocab,
+                   int64_t ignore_index, float* d_row_loss, void* stream, const char* who) {
+  if (rows < 0 || vocab <= 0 || ld < vocab)
+    return ce_fail(TM_EINVAL, "%s: bad sizes rows=%lld vocab=%lld ld=%lld", who, (long long)rows,
+                   (long long)vocab, (long long)ld);
+  if (rows == 0) return TM_OK;
+  if (!d_logits || !d_labels || !d_row_loss) return ce_fail(TM_EINVAL, "%s: null pointer", who);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool regs = TM_CE_REG_ROWS && (vocab >> 3) <= static_cast<int64_t>(kRowThreadsRegs) * kRegCols;
+  // a launch holds fewer than 2^32 work-items: longer row lists (small vocabularies in one
+  // chunk) go in several launches
+  const int64_t max_rows = 0xFFFFFFFFll / (regs ? kRowThreadsRegs : kRowThreadsStream);
+  for (int64_t r0 = 0; r0 < rows; r0 += max_rows) {
+    const uint32_t nr = static_cast<uint32_t>(rows - r0 < max_rows ? rows - r0 : max_rows);
+    uint16_t* lg = d_logits + r0 * ld;
+    if (regs)
+      hipLaunchKernelGGL((ce_rows_kernel<true, kRowThreadsRegs, kGrad>), dim3(nr), dim3(kRowThreadsRegs), 0, s,
+                         lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
+    else
+      hipLaunchKernelGGL((ce_rows_kernel<false, kRowThreadsStream, kGrad>), dim3(nr), dim3(kRowThreadsStream),
+                         kStreamLds, s, lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
+    if (int rc = ce_check_launch(who)) return rc;
+  }
+  return TM_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 int tm_ce_rows_bf16(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows,
                     int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream) {
-  if (rows < 0 || vocab <= 0 || ld < vocab)
-    return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: bad sizes rows=%lld vocab=%lld ld=%lld",
-                   (long long)rows, (long long)vocab, (long long)ld);
-  if (rows == 0) return TM_OK;
-  if (!d_logits || !d_labels || !d_row_loss) return ce_fail(TM_EINVAL, "tm_ce_rows_bf16: null pointer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool regs = TM_CE_REG_ROWS && (vocab >> 3) <= static_cast<int64_t>(kRowThreadsRegs) * kRegCols;
-  // One block per row, and a launch holds fewer than 2^32 work-items: longer row lists
-  // (small vocabularies in one chunk) go in several launches.
-  const int64_t max_rows = 0xFFFFFFFFll / (regs ? kRowThreadsRegs : kRowThreadsStream);
-  for (int64_t r0 = 0; r0 < rows; r0 += max_rows) {
-    const uint32_t nr = static_cast<uint32_t>(rows - r0 < max_rows ? rows - r0 : max_rows);
-    uint16_t* lg = d_logits + r0 * ld;
-    if (regs)
-      hipLaunchKernelGGL((ce_rows_kernel<true, kRowThreadsRegs>), dim3(nr), dim3(kRowThreadsRegs), 0, s,
-                         lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
-    else
-      hipLaunchKernelGGL((ce_rows_kernel<false, kRowThreadsStream>), dim3(nr), dim3(kRowThreadsStream),
-                         kStreamLds, s, lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
-    if (int rc = ce_check_launch("ce_rows_kernel")) return rc;
-  }
-  return TM_OK;
+  return ce_rows_launch<true>(d_logits, ld, d_labels, rows, vocab, ignore_index, d_row_loss, stream,
+                              "tm_ce_rows_bf16");
+}
+
+int tm_ce_rows_loss_bf16(const uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows,
+                         int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream) {
+  // the kGrad=false kernels only read the logits
+  return ce_rows_launch<false>(const_cast<uint16_t*>(d_logits), ld, d_labels, rows, vocab, ignore_index,
+                               d_row_loss, stream, "tm_ce_rows_loss_bf16");
 }
 
 int tm_ce_loss(const float* d_row_loss, const int64_t* d_labels, int64_t rows, int64_t ignore_index,

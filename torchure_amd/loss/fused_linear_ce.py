@@ -21,6 +21,13 @@ straight from the bf16 GEMM output (6 B per element), instead of a zero fill, an
 accumulate and a scaling pass (22 B per element); the fp32 additions and the scaling
 are the reference's, in the reference's order, so the bits are unchanged.
 
+Only the gradients autograd needs are computed. With grad mode off, or no input that
+requires a gradient (evaluation), the call returns the loss from the logits GEMM and
+tm_ce_rows_loss_bf16, which runs the same per-row arithmetic without the gradient
+write, so the loss bits are those of the training path. When only one input requires a
+gradient, the other's GEMM is skipped. The reference computes both gradients whenever
+the weight requires one (fused_linear_ce.py:63-93) and lets autograd drop them.
+
 MI355X sizing: the chunk is chosen so that the bf16 logits of a chunk take up to
 ``logits_bytes`` (4 GiB by default) instead of 1024 rows: with 288 GB of HBM the
 whole Qwen3 vocabulary for 8K-16K tokens fits in one chunk, so the fp32 grad_W
@@ -43,31 +50,65 @@ def auto_chunk_rows(n_rows: int, vocab: int, logits_bytes: int = DEFAULT_LOGITS_
     return max(1, min(n_rows, rows))
 
 
+def _checked(hidden, weight, labels, chunk_size):
+    """Argument checks shared by both paths; returns (n, v, chunk rows)."""
+    who = "fused_linear_cross_entropy"
+    for t, what in ((hidden, "hidden"), (weight, "weight"), (labels, "labels")):
+        tables.require_device_tensor(t, who, what)
+    if hidden.dtype != torch.bfloat16:
+        raise NotImplementedError(f"{who}: hidden must be bfloat16 (the autocast activation dtype)")
+    if labels.dtype != torch.int64:
+        raise RuntimeError(f"{who}: labels must be int64")
+    n, d = hidden.shape
+    v = weight.shape[0]
+    if weight.shape[1] != d or labels.shape[0] != n:
+        raise RuntimeError(f"{who}: shapes hidden {tuple(hidden.shape)}, weight {tuple(weight.shape)}, "
+                           f"labels {tuple(labels.shape)} do not match")
+    if weight.device != hidden.device or labels.device != hidden.device:
+        raise RuntimeError(f"{who}: hidden, weight and labels must be on one device")
+    chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
+    if chunk < 1:
+        raise ValueError(f"{who}: chunk_size must be positive, got {chunk_size}")
+    return n, v, chunk
+
+
+def _mean_loss(row_loss, labels, n, ignore_index, lib, stream):
+    """(mean loss as a 0-d tensor, n_valid as a 1-element view) from the per-row losses."""
+    out3 = torch.empty(3, dtype=torch.float32, device=row_loss.device)
+    _native.check(lib.tm_ce_loss(row_loss.data_ptr(), labels.data_ptr(), n, int(ignore_index),
+                                 out3.data_ptr(), stream), "tm_ce_loss")
+    return out3[2].clone(), out3[1:2]
+
+
+def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
+    """The loss when no input needs a gradient (e.g. evaluation under torch.no_grad): the
+    same logits GEMM and the same per-row arithmetic as the training path, so the same
+    bits, without the two gradient GEMMs or the gradient write. The reference's forward
+    computes and drops the gradients in this case (fused_linear_ce.py:63-93)."""
+    n, v, chunk = _checked(hidden, weight, labels, chunk_size)
+    lib = _native.lib()
+    stream = _native.stream_handle(hidden.device)
+    w = weight.to(hidden.dtype).contiguous()
+    row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
+    for s in range(0, n, chunk):
+        e = min(s + chunk, n)
+        logits = torch.matmul(hidden[s:e], w.t())
+        _native.check(lib.tm_ce_rows_loss_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
+                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
+                      "tm_ce_rows_loss_bf16")
+        del logits
+    return _mean_loss(row_loss, labels, n, ignore_index, lib, stream)[0]
+
+
 class _FusedLinearCE(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, labels, ignore_index, chunk_size):
-        who = "fused_linear_cross_entropy"
-        for t, what in ((hidden, "hidden"), (weight, "weight"), (labels, "labels")):
-            tables.require_device_tensor(t, who, what)
-        if hidden.dtype != torch.bfloat16:
-            raise NotImplementedError(f"{who}: hidden must be bfloat16 (the autocast activation dtype)")
-        if labels.dtype != torch.int64:
-            raise RuntimeError(f"{who}: labels must be int64")
-        n, d = hidden.shape
-        v = weight.shape[0]
-        if weight.shape[1] != d or labels.shape[0] != n:
-            raise RuntimeError(f"{who}: shapes hidden {tuple(hidden.shape)}, weight {tuple(weight.shape)}, "
-                               f"labels {tuple(labels.shape)} do not match")
-        if weight.device != hidden.device or labels.device != hidden.device:
-            raise RuntimeError(f"{who}: hidden, weight and labels must be on one device")
-        chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
-        if chunk < 1:
-            raise ValueError(f"{who}: chunk_size must be positive, got {chunk_size}")
+        n, v, chunk = _checked(hidden, weight, labels, chunk_size)
         lib = _native.lib()
         stream = _native.stream_handle(hidden.device)
         w = weight.to(hidden.dtype).contiguous()  # cast once, not per chunk
-        grad_hidden = torch.empty_like(hidden)
-        want_w = weight.requires_grad
+        want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        grad_hidden = torch.empty_like(hidden) if want_h else None
         # fp32 grad_W holds chunks 0..k-2; chunk k-1 stays bf16 until backward
         grad_weight = None
         if want_w and n > chunk:
@@ -81,7 +122,8 @@ class _FusedLinearCE(torch.autograd.Function):
             _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
                           "tm_ce_rows_bf16")
-            torch.matmul(logits, w, out=grad_hidden[s:e])
+            if want_h:
+                torch.matmul(logits, w, out=grad_hidden[s:e])
             if want_w:
                 gw = torch.matmul(logits.t(), h)  # (V, D) bf16
                 if e < n:
@@ -92,17 +134,14 @@ class _FusedLinearCE(torch.autograd.Function):
                 else:
                     last_gw = gw
             del logits
-        out3 = torch.empty(3, dtype=torch.float32, device=hidden.device)
-        _native.check(lib.tm_ce_loss(row_loss.data_ptr(), labels.data_ptr(), n, int(ignore_index),
-                                     out3.data_ptr(), stream), "tm_ce_loss")
-        ctx.n_valid = out3[1:2]
+        loss, ctx.n_valid = _mean_loss(row_loss, labels, n, ignore_index, lib, stream)
         ctx.grad_hidden = grad_hidden
         ctx.want_w = want_w
         ctx.grad_weight = grad_weight
         ctx.last_gw = last_gw
         ctx.accumulated = accumulated
         ctx.weight_meta = (weight.shape, weight.device)
-        return out3[2].clone()
+        return loss
 
     @staticmethod
     def backward(ctx, grad_out):
@@ -114,7 +153,7 @@ class _FusedLinearCE(torch.autograd.Function):
         last_gw = ctx.last_gw
         ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = ctx.last_gw = None
         lib = _native.lib()
-        stream = _native.stream_handle(grad_hidden.device)
+        stream = _native.stream_handle(n_valid.device)
         g = grad_out.detach().to(torch.float32).contiguous()
         scale_w = None  # an fp32 grad_W that still needs the plain scaling pass
         if ctx.want_w:
@@ -129,7 +168,8 @@ class _FusedLinearCE(torch.autograd.Function):
             else:  # no rows at all: the reference scales its zero-filled buffer
                 grad_weight = scale_w = torch.zeros(shape, dtype=torch.float32, device=device)
         rc = lib.tm_ce_scale_grads(
-            grad_hidden.data_ptr(), grad_hidden.numel(),
+            grad_hidden.data_ptr() if grad_hidden is not None else None,
+            grad_hidden.numel() if grad_hidden is not None else 0,
             scale_w.data_ptr() if scale_w is not None else None,
             scale_w.numel() if scale_w is not None else 0,
             g.data_ptr(), n_valid.data_ptr(), stream)
@@ -147,4 +187,7 @@ def fused_linear_cross_entropy(
     if hidden.dim() == 3:
         hidden = hidden.reshape(-1, hidden.shape[-1])
         labels = labels.reshape(-1)
-    return _FusedLinearCE.apply(hidden.contiguous(), weight, labels.contiguous(), ignore_index, chunk_size)
+    hidden, labels = hidden.contiguous(), labels.contiguous()
+    if not (torch.is_grad_enabled() and (hidden.requires_grad or weight.requires_grad)):
+        return _loss_only(hidden, weight, labels, ignore_index, chunk_size)
+    return _FusedLinearCE.apply(hidden, weight, labels, ignore_index, chunk_size)
