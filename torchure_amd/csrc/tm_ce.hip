@@ -219,19 +219,25 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
     // The row stays in registers: max pass, then sum-of-exp pass, no second read.
     float m = -INFINITY;
     float nmin = -INFINITY;  // -(row minimum), reduced with the maximum
-    if (vec) {
-      // fully unrolled with compile-time indices so that `keep` stays in VGPRs
+    if (vec && nvec > 0) {
+      // Every load is issued before any is used (fully unrolled, compile-time indices, so
+      // `keep` stays in VGPRs): a load under a per-thread branch next to its use made each
+      // of them wait for the one before. A thread past the row's last vector loads that
+      // last vector again, a real element of the row, which leaves the max and min as they
+      // are; the sum and the stores below skip those slots.
 #pragma unroll
       for (int k = 0; k < kRegCols; ++k) {
         const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
-        if (v < nvec) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(row + v * 8);
-          keep[k] = w;
-          m = fmaxf(m, fmaxf(fmaxf(fmaxf(lo16(w.x), hi16(w.x)), fmaxf(lo16(w.y), hi16(w.y))),
-                             fmaxf(fmaxf(lo16(w.z), hi16(w.z)), fmaxf(lo16(w.w), hi16(w.w)))));
-          nmin = fmaxf(nmin, -fminf(fminf(fminf(lo16(w.x), hi16(w.x)), fminf(lo16(w.y), hi16(w.y))),
-                                    fminf(fminf(lo16(w.z), hi16(w.z)), fminf(lo16(w.w), hi16(w.w)))));
-        }
+        keep[k] = *reinterpret_cast<const u32x4*>(row + (v < nvec ? v : nvec - 1) * 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from starting the max before the last load
+#pragma unroll
+      for (int k = 0; k < kRegCols; ++k) {
+        const u32x4 w = keep[k];
+        m = fmaxf(m, fmaxf(fmaxf(fmaxf(lo16(w.x), hi16(w.x)), fmaxf(lo16(w.y), hi16(w.y))),
+                           fmaxf(fmaxf(lo16(w.z), hi16(w.z)), fmaxf(lo16(w.w), hi16(w.w)))));
+        nmin = fmaxf(nmin, -fminf(fminf(fminf(lo16(w.x), hi16(w.x)), fminf(lo16(w.y), hi16(w.y))),
+                                  fminf(fminf(lo16(w.z), hi16(w.z)), fminf(lo16(w.w), hi16(w.w)))));
       }
     }
     for (int64_t i = vend + threadIdx.x; i < vocab; i += kCeThreads) {
