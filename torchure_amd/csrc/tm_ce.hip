@@ -49,6 +49,7 @@ constexpr int kStreamLds = TM_CE_STREAM_LDS;
 #ifndef TM_CE_REG_ROWS
 #define TM_CE_REG_ROWS 1
 #endif
+constexpr int kStreamUnroll = 4;  // vectors per thread loaded together on the streaming path
 constexpr int kRegCols = 20;  // 8-element vectors per thread kept in registers (V <= 163,840)
 constexpr int kMaxWaves = (kRowThreadsRegs > TM_CE_STREAM_THREADS ? kRowThreadsRegs : TM_CE_STREAM_THREADS) / 64;
 
@@ -282,13 +283,23 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
         mm[j] = -INFINITY;
         ss[j] = 0.0f;
       }
-      for (int64_t v = threadIdx.x; v < nvec; v += kCeThreads) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(row + v * 8);
+      auto add8 = [&](const u32x4 w) {
         ms_add(mm[0], ss[0], lo16(w.x)); ms_add(mm[1], ss[1], hi16(w.x));
         ms_add(mm[2], ss[2], lo16(w.y)); ms_add(mm[3], ss[3], hi16(w.y));
         ms_add(mm[4], ss[4], lo16(w.z)); ms_add(mm[5], ss[5], hi16(w.z));
         ms_add(mm[6], ss[6], lo16(w.w)); ms_add(mm[7], ss[7], hi16(w.w));
+      };
+      // kStreamUnroll loads in flight before they are used, same element order per lane
+      int64_t v = threadIdx.x;
+      for (; v + (kStreamUnroll - 1) * kCeThreads < nvec; v += kStreamUnroll * kCeThreads) {
+        u32x4 w[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u)
+          w[u] = *reinterpret_cast<const u32x4*>(row + (v + u * kCeThreads) * 8);
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) add8(w[u]);
       }
+      for (; v < nvec; v += kCeThreads) add8(*reinterpret_cast<const u32x4*>(row + v * 8));
 #pragma unroll
       for (int j = 0; j < 8; ++j) ms_merge(m, s, mm[j], ss[j]);
     }
@@ -365,8 +376,16 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
         if (v < nvec) put8(keep[k], v, fold_tag);
       }
     } else {
-      for (int64_t v = threadIdx.x; v < nvec; v += kCeThreads)
-        put8(*reinterpret_cast<const u32x4*>(row + v * 8), v, fold_tag);
+      int64_t v = threadIdx.x;
+      for (; v + (kStreamUnroll - 1) * kCeThreads < nvec; v += kStreamUnroll * kCeThreads) {
+        u32x4 w[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u)
+          w[u] = *reinterpret_cast<const u32x4*>(row + (v + u * kCeThreads) * 8);
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) put8(w[u], v + u * kCeThreads, fold_tag);
+      }
+      for (; v < nvec; v += kCeThreads) put8(*reinterpret_cast<const u32x4*>(row + v * 8), v, fold_tag);
     }
   };
   if (vec) {
