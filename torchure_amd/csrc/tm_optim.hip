@@ -366,16 +366,41 @@ __global__ __launch_bounds__(kThreads) void grad_scale_kernel(
   if (start >= d.numel) return;
   const int64_t end = min(start + chunk_elems, d.numel);
   const float coef = *coef_p;
+  // 16-byte vectors where the grad is 16-byte aligned (chunk starts are multiples of
+  // TM_CHUNK_ALIGN elements, so then every vector is), element by element otherwise and
+  // for the tail; the same single multiply per element either way
+  const bool vec = aligned16(d.grad);
   if (d.flags & TM_GRAD_F32) {
     float* __restrict__ g = reinterpret_cast<float*>(d.grad);
-    for (int64_t i = start + threadIdx.x; i < end; i += kThreads) g[i] = g[i] * coef;
+    const int64_t vend = vec ? start + ((end - start) & ~int64_t(3)) : start;
+    for (int64_t e = start + threadIdx.x * 4; e < vend; e += kThreads * 4) {
+      f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(g + e));
+      a.x = a.x * coef;
+      a.y = a.y * coef;
+      a.z = a.z * coef;
+      a.w = a.w * coef;
+      st<true>(reinterpret_cast<f32x4*>(g + e), a);
+    }
+    for (int64_t i = vend + threadIdx.x; i < end; i += kThreads) g[i] = g[i] * coef;
   } else {
     // torch._foreach_mul_ on a bf16 list holds the 0-d scalar in the list's dtype
     // (BinaryOpScalarTensorFunctor, torch/include/ATen/native/hip/ForeachFunctors.cuh:
     // 309-342): the coefficient is rounded to bf16 before the fp32 multiply.
     const float coef_b = __uint_as_float(bf16_rne(coef) << 16);
     uint16_t* __restrict__ g = reinterpret_cast<uint16_t*>(d.grad);
-    for (int64_t i = start + threadIdx.x; i < end; i += kThreads)
+    auto scale2 = [&](uint32_t w) -> uint32_t {
+      return bf16_rne(bf16_lo(w) * coef_b) | (bf16_rne(bf16_hi(w) * coef_b) << 16);
+    };
+    const int64_t vend = vec ? start + ((end - start) & ~int64_t(kVec - 1)) : start;
+    for (int64_t e = start + threadIdx.x * kVec; e < vend; e += kThreads * kVec) {
+      u32x4 w = ld<true>(reinterpret_cast<const u32x4*>(g + e));
+      w.x = scale2(w.x);
+      w.y = scale2(w.y);
+      w.z = scale2(w.z);
+      w.w = scale2(w.w);
+      st<true>(reinterpret_cast<u32x4*>(g + e), w);
+    }
+    for (int64_t i = vend + threadIdx.x; i < end; i += kThreads)
       g[i] = static_cast<uint16_t>(bf16_rne(bf16_at(g, i) * coef_b));
   }
 }
