@@ -69,6 +69,34 @@ def test_bf16_copy_is_rne_of_master():
         assert np.array_equal(H.from_dev_bf16(w), oracle.bf16_rne(p.detach().cpu().numpy().reshape(-1)))
 
 
+def test_attach_and_refresh_cast_is_rne():
+    """attach_bf16_working_params and refresh_bf16_working_params write RNE(master)
+    (torch/headeronly/util/BFloat16.h:100-114, NaN -> 0x7FC0) bit for bit: special values,
+    halfway cases, odd lengths, and masters that are views at offsets that are not 16-byte
+    aligned (the element-wise path)."""
+    import torchure_amd as ta
+
+    r = H.rng(91)
+    base = (r.standard_normal(300_000) * 10.0).astype(np.float32)
+    base[:12] = [np.nan, np.inf, -np.inf, -0.0, 1e-40, -1e-42, 3.4e38, 1.0 + 2.0 ** -8,
+                 1.0 + 3 * 2.0 ** -8, -(1.0 + 2.0 ** -8), 65504.0, 2.0 ** -126]
+    dev = torch.from_numpy(base).to(DEV)
+    spans = [(0, 12), (12, 12 + 8 * 1000), (9000, 9000 + 16384 * 3 + 5), (100_001, 100_001 + 777),
+             (200_003, 200_003 + 40_000)]
+    params = [torch.nn.Parameter(dev[a:b]) for a, b in spans]
+    work = ta.attach_bf16_working_params(params)
+    torch.cuda.synchronize()
+    for (a, b), w in zip(spans, work):
+        assert np.array_equal(H.from_dev_bf16(w), oracle.bf16_rne(base[a:b])), (a, b)
+    with torch.no_grad():
+        for p in params:
+            p.mul_(-0.5)
+    ta.refresh_bf16_working_params(params)
+    torch.cuda.synchronize()
+    for p, w in zip(params, work):
+        assert np.array_equal(H.from_dev_bf16(w), oracle.bf16_rne(p.detach().cpu().numpy().reshape(-1)))
+
+
 def test_norm_vs_fp64_and_deterministic():
     import torchure_amd as ta
     from torchure_amd.core.grad_helper import grad_norm_launch
