@@ -516,8 +516,21 @@ def run_cpu_baseline(config: str, blocks: int, steps: int):
         kind="port",
         sample=(f"{config} blocks 0..{blocks - 1} ({len(params)} tensors, {n} params), median of "
                 f"{steps} steps after 1 warm-up, {med * 1e3:.1f} ms/step; torch CPU foreach-norm clip + "
-                f"AdamW(fused=True) + bf16 cast; GB/s on the same 30 B/param basis"),
+                f"AdamW(fused=True) + bf16 cast; GB/s on the same 30 B/param basis; "
+                f"{threads} threads of {os.cpu_count()} logical CPUs, host RAM {_host_ram_gib()} GiB"),
     )
+
+
+def _host_ram_gib() -> str:
+    """Total host memory from /proc/meminfo, or '?' where it cannot be read."""
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemTotal:"):
+                    return f"{int(line.split()[1]) / 2 ** 20:.0f}"
+    except OSError:
+        pass
+    return "?"
 
 
 def load_traffic(config: str):
