@@ -983,6 +983,39 @@ def test_grads_as_views_into_flat_buckets():
     assert w == {"p": 0, "m": 0, "v": 0, "bf16": 0, "step": 0}, w
 
 
+def test_two_optimizers_on_two_streams_concurrently():
+    """Two independent optimizers whose clip + step calls are issued interleaved on two
+    streams (default priority) give the same bits as running them one after the other on
+    the default stream: the tables, workspaces and staging buffers of one call are never
+    reused by the other's while it may still read them."""
+    import torchure_amd as ta
+
+    def setups():
+        a = H.device_setup(H.make_host_set(shapes_for("tiny"), seed=61), DEV)
+        b = H.device_setup(H.make_host_set(shapes_for("tiny")[::-1], seed=62), DEV)
+        return a, b
+
+    def run(pairs, streams):
+        for _ in range(3):
+            for (params, work, opt), s in zip(pairs, streams):
+                with torch.cuda.stream(s):
+                    ta.clip_grad_norm(params, None, 1.0)
+                    opt.step()
+        torch.cuda.synchronize()
+
+    seq = setups()
+    run(seq, [torch.cuda.current_stream(), torch.cuda.current_stream()])
+    con = setups()
+    torch.cuda.synchronize()
+    run(con, [torch.cuda.Stream(), torch.cuda.Stream()])
+    for (pa, wa, oa), (pb, wb, ob) in zip(seq, con):
+        for x, y, u, v in zip(pa, pb, wa, wb):
+            assert torch.equal(x, y)
+            assert torch.equal(u.view(torch.int16), v.view(torch.int16))
+            for k in ("step", "exp_avg", "exp_avg_sq"):
+                assert torch.equal(oa.state[x][k], ob.state[y][k])
+
+
 def test_eager_scale_matches_foreach_mul():
     """The eager clip's in-place scale against torch._foreach_mul_ with the same 0-d device
     coefficient (torchure/core/grad_helper.py:33), bit for bit, for fp32 and bf16 grads:
