@@ -32,6 +32,19 @@ def test_constructor_rejects_unsupported():
         AdamW(p, chunk_elems=1000)
 
 
+def test_at_most_16_param_groups():
+    """One launch carries up to TM_MAX_GROUPS (16) hyper-parameter groups; more are refused
+    at construction and by add_param_group, before any GPU work."""
+    ps = [torch.nn.Parameter(torch.zeros(2)) for _ in range(17)]
+    AdamW([{"params": [p]} for p in ps[:16]])
+    with pytest.raises(ValueError, match="at most 16"):
+        AdamW([{"params": [p]} for p in ps])
+    opt = AdamW([{"params": [p]} for p in ps[:16]])
+    with pytest.raises(ValueError, match="at most 16"):
+        opt.add_param_group({"params": [ps[16]]})
+    assert len(opt.param_groups) == 16  # the refused group was not added
+
+
 def test_param_groups_have_torch_adamw_keys():
     m1, m2 = _model(), _model()
     mine = build_optimizer(m1, "adamw", {"lr": 3e-4, "weight_decay": 0.1, "betas": [0.9, 0.95], "fused": True})

@@ -123,13 +123,12 @@ class AdamW(torch.optim.Optimizer):
         self._verified: dict = {}  # id(param) -> _ParamEntry
         self._plan = None  # _Plan of the last full step, reused while nothing changes
         super().__init__(params, defaults)
-        if len(self.param_groups) > _native.TM_MAX_GROUPS:
-            raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
 
     def add_param_group(self, param_group: dict) -> None:
-        super().add_param_group(param_group)
-        if len(self.param_groups) > _native.TM_MAX_GROUPS:
+        # checked first, so a refused group leaves the optimizer as it was
+        if len(self.param_groups) >= _native.TM_MAX_GROUPS:
             raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
+        super().add_param_group(param_group)
         ref = weakref.ref(self)
         for p in self.param_groups[-1]["params"]:
             p._tm_owner = ref
