@@ -1016,6 +1016,33 @@ def test_two_optimizers_on_two_streams_concurrently():
                 assert torch.equal(oa.state[x][k], ob.state[y][k])
 
 
+def test_shared_params_clip_in_place():
+    """Params held by two optimizers: the clip scales their grads in place (no deferral into
+    one optimizer), so both steps read the clipped grads, as with the reference's in-place
+    clip. Checked bit for bit against the same sequence with defer_clip=False."""
+    import torchure_amd as ta
+
+    def run(defer):
+        gen = torch.Generator(device=DEV).manual_seed(8)
+        shared = torch.nn.Parameter(torch.randn(64, 32, device=DEV, generator=gen) * 0.02)
+        own = torch.nn.Parameter(torch.randn(100, device=DEV, generator=gen) * 0.02)
+        shared.grad = torch.randn(64, 32, device=DEV, generator=gen)
+        own.grad = torch.randn(100, device=DEV, generator=gen)
+        o1 = ta.AdamW([shared, own], lr=1e-3, defer_clip=defer)
+        o2 = ta.AdamW([shared], lr=2e-3, defer_clip=defer)
+        norm = ta.clip_grad_norm([shared, own], None, 1.0)
+        assert o1._pending is None and o2._pending is None
+        o1.step()
+        o2.step()
+        torch.cuda.synchronize()
+        return norm, shared.detach().clone(), own.detach().clone(), shared.grad.clone()
+
+    a, b = run(True), run(False)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+    assert a[0].item() > 1.0  # the clip was active
+
+
 def test_eager_scale_matches_foreach_mul():
     """The eager clip's in-place scale against torch._foreach_mul_ with the same 0-d device
     coefficient (torchure/core/grad_helper.py:33), bit for bit, for fp32 and bf16 grads:

@@ -45,6 +45,26 @@ def test_at_most_16_param_groups():
     assert len(opt.param_groups) == 16  # the refused group was not added
 
 
+def test_param_in_two_optimizers_has_no_single_owner():
+    """A param held by two AdamW instances reads as unowned, so a clip over it scales in
+    place (both optimizers see the scaled grads) instead of deferring into one of them."""
+    from torchure_amd.optimizer.adamw import owner_of
+
+    a, b = torch.nn.Parameter(torch.zeros(2)), torch.nn.Parameter(torch.zeros(2))
+    o1 = AdamW([a, b])
+    assert owner_of(a) is o1 and owner_of(b) is o1
+    o2 = AdamW([b])
+    assert owner_of(a) is o1 and owner_of(b) is None
+    AdamW([b])
+    assert owner_of(b) is None  # stays shared
+    del o1
+    import gc
+    gc.collect()
+    c = torch.nn.Parameter(torch.zeros(2))
+    o3 = AdamW([a, c])  # a's previous owner is gone: o3 owns it
+    assert owner_of(a) is o3 and owner_of(c) is o3 and o2 is not None
+
+
 def test_param_groups_have_torch_adamw_keys():
     m1, m2 = _model(), _model()
     mine = build_optimizer(m1, "adamw", {"lr": 3e-4, "weight_decay": 0.1, "betas": [0.9, 0.95], "fused": True})

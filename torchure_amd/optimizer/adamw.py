@@ -39,8 +39,16 @@ import weakref
 from torchure_amd import _native
 from torchure_amd.core import tables
 
+def _shared_owner():
+    """The owner mark of a param held by more than one AdamW: it reads as no owner, so a clip
+    over it scales the grads in place (every optimizer then sees them scaled, as in the
+    reference) instead of deferring the scale into one of them."""
+    return None
+
+
 def owner_of(p: torch.Tensor):
-    """The torchure_amd AdamW that owns ``p`` (a weak reference set by add_param_group), or None."""
+    """The torchure_amd AdamW that owns ``p`` (a weak reference set by add_param_group), or None
+    (no owner, or several)."""
     ref = getattr(p, "_tm_owner", None)
     return ref() if ref is not None else None
 
@@ -131,7 +139,11 @@ class AdamW(torch.optim.Optimizer):
         super().add_param_group(param_group)
         ref = weakref.ref(self)
         for p in self.param_groups[-1]["params"]:
-            p._tm_owner = ref
+            cur = getattr(p, "_tm_owner", None)
+            if cur is _shared_owner:
+                continue
+            prev = cur() if cur is not None else None
+            p._tm_owner = ref if prev is None or prev is self else _shared_owner
         self._plan = None
 
     def __setstate__(self, state):
