@@ -549,11 +549,12 @@ def test_state_dict_roundtrip_with_torch_adamw():
         assert opt2.state[p]["step"].device == p.device
 
 
-@pytest.mark.parametrize("config", ["qwen3-0.6b", "qwen3-4b"])
+@pytest.mark.parametrize("config", ["qwen3-0.6b", "qwen3-0.6b-ref", "qwen3-4b"])
 def test_full_size_properties(config):
-    """Configs 2 and 4 at full size (596M / 4.02B params): norm vs fp64 over every
-    grad, the bf16 copy is RNE(master) everywhere, and sampled tensors -- including
-    the tied embedding, the largest tensor -- match the oracle bit for bit."""
+    """Configs 2 and 4 at full size (596M / 4.02B params, and the reference's default 0.6B
+    shape with MLP 2816, 574M): norm vs fp64 over every grad, the bf16 copy is RNE(master)
+    everywhere, and sampled tensors -- including the tied embedding, the largest tensor --
+    match the oracle bit for bit."""
     import torchure_amd as ta
 
     shapes = shapes_for(config)
