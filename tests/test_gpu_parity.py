@@ -1044,6 +1044,21 @@ def test_shared_params_clip_in_place():
     assert a[0].item() > 1.0  # the clip was active
 
 
+def test_sparse_grads_are_refused():
+    """A sparse grad (nn.Embedding(sparse=True)) is refused with torch's AdamW message by the
+    step, and with a clear message by the clip, before any kernel runs."""
+    import torchure_amd as ta
+
+    emb = torch.nn.Embedding(50, 8, sparse=True).to(DEV)
+    emb(torch.tensor([1, 2, 3], device=DEV)).sum().backward()
+    assert emb.weight.grad.is_sparse
+    opt = ta.AdamW(emb.parameters())
+    with pytest.raises(RuntimeError, match="does not support sparse gradients"):
+        opt.step()
+    with pytest.raises(RuntimeError, match="dense grads only"):
+        ta.clip_grad_norm(emb.parameters(), None, 1.0)
+
+
 def test_eager_scale_matches_foreach_mul():
     """The eager clip's in-place scale against torch._foreach_mul_ with the same 0-d device
     coefficient (torchure/core/grad_helper.py:33), bit for bit, for fp32 and bf16 grads:

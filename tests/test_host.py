@@ -223,6 +223,8 @@ def test_host_list_primitives():
     assert h.same(ps, list(ps)) and not h.same(ps, ps[::-1]) and not h.same(ps, ps[:3])
     ptr, numel, code = h.grad_fields([torch.zeros(5)])
     assert numel[0] == 5 and code[0] == 255  # CPU tensors are not grad-table material
+    _, _, code = h.grad_fields([torch.zeros(5, 2).to_sparse()])  # no storage: reported, not raised
+    assert code[0] == 255
     with pytest.raises(TypeError):
         h.ptrs([1])
     assert isinstance(ptr, np.ndarray)

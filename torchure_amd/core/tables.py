@@ -166,6 +166,8 @@ def _grad_table_checked(grads: list[torch.Tensor], who: str) -> np.ndarray:
             flags = _native.TM_GRAD_F32
         else:
             flags = grad_flags(g, who)  # raises
+        if g.layout != torch.strided:
+            raise RuntimeError(f"{who}: {g.layout} grads are not supported (dense grads only)")
         if not g.is_cuda or not g.is_contiguous():
             require_device_tensor(g, who, "grad")  # raises with the reason
         recs.append((0, 0, 0, g.data_ptr(), 0, 0, g.numel(), 0, flags))

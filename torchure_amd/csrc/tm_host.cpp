@@ -122,14 +122,15 @@ py::tuple grad_fields(const py::list& ts) {
   uint8_t* pc = code.mutable_data();
   for (Py_ssize_t i = 0; i < n; ++i) {
     const at::Tensor* t = tensor_or_null(list_item(ts, i));
+    const bool strided = t && t->defined() && t->layout() == at::kStrided;  // sparse ones have no data_ptr
     uint8_t c = 255;
-    if (t && t->defined() && t->layout() == at::kStrided && t->is_cuda() && t->is_contiguous()) {
+    if (strided && t->is_cuda() && t->is_contiguous()) {
       const auto st = t->scalar_type();
       c = st == at::kBFloat16 ? 0 : (st == at::kFloat ? 1 : 255);
     }
     pc[i] = c;
-    pp[i] = (t && t->defined()) ? reinterpret_cast<uint64_t>(t->data_ptr()) : 0u;
-    pn[i] = (t && t->defined()) ? t->numel() : 0;
+    pp[i] = strided ? reinterpret_cast<uint64_t>(t->data_ptr()) : 0u;
+    pn[i] = strided ? t->numel() : 0;
   }
   return py::make_tuple(ptr, numel, code);
 }

@@ -266,8 +266,8 @@ class AdamW(torch.optim.Optimizer):
                     flags = _native.TM_GRAD_F32
                 else:
                     flags = tables.grad_flags(g, "torchure_amd.AdamW")  # raises
-                if (not g.is_cuda or g.get_device() != ent.dev_index or g.numel() != ent.numel
-                        or not g.is_contiguous() or g.is_sparse):
+                if (g.is_sparse or not g.is_cuda or g.get_device() != ent.dev_index
+                        or g.numel() != ent.numel or not g.is_contiguous()):
                     self._check_param(p, g, work)  # raises with a precise message
                 if rec is None:
                     if id(p) in clip_ids:
