@@ -225,6 +225,17 @@ def test_host_list_primitives():
     assert numel[0] == 5 and code[0] == 255  # CPU tensors are not grad-table material
     _, _, code = h.grad_fields([torch.zeros(5, 2).to_sparse()])  # no storage: reported, not raised
     assert code[0] == 255
+    from collections import defaultdict
+    st = defaultdict(dict)
+    st[ps[0]] = {"exp_avg": ps[1], "exp_avg_sq": ps[2], "step": ps[3]}
+    sd = [st[ps[0]]]
+    assert h.states_same(st, [ps[0]], sd, [ps[1]], [ps[2]], [ps[3]])
+    assert not h.states_same(st, [ps[0]], sd, [ps[1]], [ps[3]], [ps[3]])  # another tensor
+    assert not h.states_same(st, [ps[1]], sd, [ps[1]], [ps[2]], [ps[3]])  # no entry: no factory run
+    assert ps[1] not in st
+    ps[0]._tm_working = ws[1]
+    assert h.attrs_same(ps[:2], "_tm_working", [ws[1], None])
+    assert not h.attrs_same(ps[:2], "_tm_working", [None, None])
     with pytest.raises(TypeError):
         h.ptrs([1])
     assert isinstance(ptr, np.ndarray)

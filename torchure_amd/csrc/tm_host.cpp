@@ -135,6 +135,51 @@ py::tuple grad_fields(const py::list& ts) {
   return py::make_tuple(ptr, numel, code);
 }
 
+// True if, for every i, state_map[params[i]] is states[i] and that dict's "exp_avg",
+// "exp_avg_sq" and "step" entries are ms[i], vs[i] and ss[i] (object identity). A missing
+// entry is a mismatch: the lookup does not run a defaultdict's factory.
+bool states_same(const py::dict& state_map, const py::list& params, const py::list& states,
+                 const py::list& ms, const py::list& vs, const py::list& ss) {
+  const Py_ssize_t n = PyList_GET_SIZE(params.ptr());
+  for (const py::list* l : {&states, &ms, &vs, &ss})
+    if (PyList_GET_SIZE(l->ptr()) != n) return false;
+  static PyObject* k_m = PyUnicode_InternFromString("exp_avg");
+  static PyObject* k_v = PyUnicode_InternFromString("exp_avg_sq");
+  static PyObject* k_s = PyUnicode_InternFromString("step");
+  auto item = [](PyObject* d, PyObject* k) -> PyObject* {  // borrowed, or nullptr if absent
+    PyObject* r = PyDict_GetItemWithError(d, k);
+    if (!r && PyErr_Occurred()) throw py::error_already_set();
+    return r;
+  };
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* st = item(state_map.ptr(), list_item(params, i));
+    if (!st || st != list_item(states, i) || !PyDict_Check(st)) return false;
+    if (item(st, k_m) != list_item(ms, i) || item(st, k_v) != list_item(vs, i) ||
+        item(st, k_s) != list_item(ss, i))
+      return false;
+  }
+  return true;
+}
+
+// True if getattr(objs[i], name, None) is expected[i] for every i.
+bool attrs_same(const py::list& objs, const py::str& name, const py::list& expected) {
+  const Py_ssize_t n = PyList_GET_SIZE(objs.ptr());
+  if (PyList_GET_SIZE(expected.ptr()) != n) return false;
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* a = PyObject_GetAttr(list_item(objs, i), name.ptr());  // new reference
+    if (!a) {
+      if (!PyErr_ExceptionMatches(PyExc_AttributeError)) throw py::error_already_set();
+      PyErr_Clear();
+      Py_INCREF(Py_None);
+      a = Py_None;
+    }
+    const bool same_obj = a == list_item(expected, i);
+    Py_DECREF(a);
+    if (!same_obj) return false;
+  }
+  return true;
+}
+
 // Bumps the autograd version counter of every tensor, as an in-place op would.
 void bump(const py::list& ts) {
   const Py_ssize_t n = PyList_GET_SIZE(ts.ptr());
@@ -154,4 +199,6 @@ PYBIND11_MODULE(_tm_host, m) {
   m.def("same", &same, "element-wise object identity of two lists");
   m.def("bump", &bump, "bump the autograd version of each tensor");
   m.def("grad_fields", &grad_fields, "(data_ptr, numel, dtype code) of each grad");
+  m.def("states_same", &states_same, "optimizer state dicts and their tensors are the given objects");
+  m.def("attrs_same", &attrs_same, "getattr(obj, name, None) of each object is the given object");
 }

@@ -334,7 +334,7 @@ class AdamW(torch.optim.Optimizer):
                 return None
             b1, b2 = group["betas"]
             hyper.append((float(lr), float(b1), float(b2), float(group["weight_decay"]), float(group["eps"])))
-        if not host.same([getattr(p, "_tm_working", None) for p in plan.all_params], plan.all_works):
+        if not host.attrs_same(plan.all_params, "_tm_working", plan.all_works):
             return None
         gs, src = host.grads(plan.all_params, plan.all_works)
         if src != plan.src:
@@ -342,13 +342,7 @@ class AdamW(torch.optim.Optimizer):
         gl = [g for g in gs if g is not None]
         if not host.dense_contiguous(gl) or not np.array_equal(host.ptrs(plan.statics), plan.static_ptrs):
             return None
-        state_map = self.state
-        states = [state_map.get(p) for p in plan.params]
-        if not host.same(states, plan.states):
-            return None
-        if not (host.same([st.get("exp_avg") for st in states], plan.ms)
-                and host.same([st.get("exp_avg_sq") for st in states], plan.vs)
-                and host.same([st.get("step") for st in states], plan.ss)):
+        if not host.states_same(self.state, plan.params, plan.states, plan.ms, plan.vs, plan.ss):
             return None
         if plan.wents:
             want = np.fromiter((e.expect for e in plan.wents), dtype=np.int64, count=len(plan.wents))
