@@ -65,6 +65,30 @@ def test_param_in_two_optimizers_has_no_single_owner():
     assert owner_of(a) is o3 and owner_of(c) is o3 and o2 is not None
 
 
+def test_owned_params_pickle_and_copy():
+    """Params of this AdamW pickle, save and deep-copy as with torch's optimizers (the owner
+    mark is not carried over: the saved or copied param belongs to no optimizer)."""
+    import copy
+    import io
+    import pickle
+
+    from torchure_amd.optimizer.adamw import owner_of
+
+    m = torch.nn.Linear(4, 3)
+    opt = AdamW(m.parameters())
+    buf = io.BytesIO()
+    torch.save(m, buf)
+    buf.seek(0)
+    m2 = torch.load(buf, weights_only=False)  # a file this test wrote
+    assert torch.equal(m2.weight, m.weight) and owner_of(m2.weight) is None
+    w = pickle.loads(pickle.dumps(m.weight))
+    assert torch.equal(w, m.weight) and owner_of(w) is None
+    t = m.weight.detach().clone()
+    t._tm_owner = m.weight._tm_owner
+    assert owner_of(copy.deepcopy(t)) is None  # (a shallow copy shares the mark, as it shares all attributes)
+    assert owner_of(m.weight) is opt
+
+
 def test_param_groups_have_torch_adamw_keys():
     m1, m2 = _model(), _model()
     mine = build_optimizer(m1, "adamw", {"lr": 3e-4, "weight_decay": 0.1, "betas": [0.9, 0.95], "fused": True})

@@ -39,11 +39,34 @@ import weakref
 from torchure_amd import _native
 from torchure_amd.core import tables
 
-def _shared_owner():
-    """The owner mark of a param held by more than one AdamW: it reads as no owner, so a clip
-    over it scales the grads in place (every optimizer then sees them scaled, as in the
-    reference) instead of deferring the scale into one of them."""
-    return None
+class _Owner:
+    """``p._tm_owner``: a weak reference to the AdamW that holds ``p``; calling it gives that
+    optimizer, or None once it is gone. Pickling and copying give an empty mark (a saved or
+    copied param belongs to no optimizer), so ``torch.save(model)`` and ``copy.deepcopy`` work
+    as with torch's own optimizers, which leave params untouched."""
+
+    __slots__ = ("ref",)
+
+    def __init__(self, opt=None):
+        self.ref = weakref.ref(opt) if opt is not None else None
+
+    def __call__(self):
+        return self.ref() if self.ref is not None else None
+
+    def __reduce__(self):
+        return (_Owner, ())
+
+    def __copy__(self):
+        return _Owner()
+
+    def __deepcopy__(self, memo):
+        return _Owner()
+
+
+# The owner mark of a param held by more than one AdamW: it reads as no owner, so a clip over
+# it scales the grads in place (every optimizer then sees them scaled, as in the reference)
+# instead of deferring the scale into one of them.
+_SHARED = _Owner()
 
 
 def owner_of(p: torch.Tensor):
@@ -137,13 +160,13 @@ class AdamW(torch.optim.Optimizer):
         if len(self.param_groups) >= _native.TM_MAX_GROUPS:
             raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
         super().add_param_group(param_group)
-        ref = weakref.ref(self)
+        own = _Owner(self)
         for p in self.param_groups[-1]["params"]:
             cur = getattr(p, "_tm_owner", None)
-            if cur is _shared_owner:
+            if cur is _SHARED:
                 continue
             prev = cur() if cur is not None else None
-            p._tm_owner = ref if prev is None or prev is self else _shared_owner
+            p._tm_owner = own if prev is None or prev is self else _SHARED
         self._plan = None
 
     def __setstate__(self, state):
