@@ -87,6 +87,12 @@ def test_owned_params_pickle_and_copy():
     t._tm_owner = m.weight._tm_owner
     assert owner_of(copy.deepcopy(t)) is None  # (a shallow copy shares the mark, as it shares all attributes)
     assert owner_of(m.weight) is opt
+    # the optimizer itself: its settings survive, and it owns the params it comes back with
+    o = AdamW(m.parameters(), chunk_elems=4096, defer_clip=False)
+    for o2 in (pickle.loads(pickle.dumps(o)), copy.deepcopy(o)):
+        assert (o2.chunk_elems, o2.defer_clip) == (4096, False)
+        assert all(owner_of(p) is o2 for g in o2.param_groups for p in g["params"])
+        assert o2.param_groups[0]["params"][0] is not m.weight
 
 
 def test_param_groups_have_torch_adamw_keys():

@@ -160,19 +160,30 @@ class AdamW(torch.optim.Optimizer):
         if len(self.param_groups) >= _native.TM_MAX_GROUPS:
             raise ValueError(f"torchure_amd.AdamW: at most {_native.TM_MAX_GROUPS} param groups")
         super().add_param_group(param_group)
+        self._mark_owned(self.param_groups[-1]["params"])
+        self._plan = None
+
+    def _mark_owned(self, params) -> None:
         own = _Owner(self)
-        for p in self.param_groups[-1]["params"]:
+        for p in params:
             cur = getattr(p, "_tm_owner", None)
             if cur is _SHARED:
                 continue
             prev = cur() if cur is not None else None
             p._tm_owner = own if prev is None or prev is self else _SHARED
-        self._plan = None
+
+    def __getstate__(self):
+        """torch's pickled state (defaults, state, param_groups) plus this optimizer's settings."""
+        state = super().__getstate__()
+        state["chunk_elems"] = self.chunk_elems
+        state["defer_clip"] = self.defer_clip
+        return state
 
     def __setstate__(self, state):
         super().__setstate__(state)
         for group in self.param_groups:
             group["decoupled_weight_decay"] = True
+            self._mark_owned(group["params"])
         self.__dict__.setdefault("chunk_elems", tables.DEFAULT_CHUNK_ELEMS)
         self.__dict__.setdefault("defer_clip", True)
         self.__dict__.setdefault("_pending", None)
