@@ -250,6 +250,14 @@ int tm_ce_scale_grads(uint16_t* d_grad_h, int64_t nh, float* d_grad_w, int64_t n
 int tm_ce_grad_w(float* d_grad_w, const uint16_t* d_chunk, int64_t nw, int accumulate,
                  const float* d_grad_out, const float* d_n_valid, void* stream);
 
+/*
+ * grad_hidden of fp32 hidden states (fused_linear_ce.py:68,80,120 under autocast: the
+ * buffer has the hidden states' dtype, holds the widened bf16 GEMM result and is scaled
+ * in place in fp32): d_dst[i] = float(d_src[i]) * (*d_grad_out / *d_n_valid), -0 kept.
+ */
+int tm_ce_widen_scale(float* d_dst, const uint16_t* d_src, int64_t n, const float* d_grad_out,
+                      const float* d_n_valid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

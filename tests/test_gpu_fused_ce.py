@@ -280,37 +280,46 @@ def test_ce_rows_edge_rows_vs_fp64(v):
     assert np.all(grad_bits[0, ::3] == 0)  # exp(-inf) = 0 exactly
 
 
-@pytest.mark.parametrize("b,s,d,v,chunk,ignore_frac", [
-    (2, 128, 64, 1000, 64, 0.1),          # uneven chunks
-    (2, 256, 128, 5000, 512, 0.0),        # one chunk
-    (2, 4096, 1024, 151936, 1024, 0.05),  # the Qwen3 head at the reference's chunk size
-    (2, 4096, 1024, 151936, None, 0.05),  # the same with this build's default (one chunk)
+@pytest.mark.parametrize("b,s,d,v,chunk,ignore_frac,hidden_dtype", [
+    (2, 128, 64, 1000, 64, 0.1, torch.bfloat16),          # uneven chunks
+    (2, 256, 128, 5000, 512, 0.0, torch.bfloat16),        # one chunk
+    (2, 4096, 1024, 151936, 1024, 0.05, torch.bfloat16),  # the Qwen3 head at the reference's chunk size
+    (2, 4096, 1024, 151936, None, 0.05, torch.bfloat16),  # the same with this build's default (one chunk)
+    (2, 4096, 1024, 151936, 4096, 0.05, torch.float32),   # the trainer's call: fp32 hidden, autocast
 ])
-def test_reference_cases_vs_plain_cross_entropy(b, s, d, v, chunk, ignore_frac):
+def test_reference_cases_vs_plain_cross_entropy(b, s, d, v, chunk, ignore_frac, hidden_dtype):
     """The cases and bars of the reference's own test (tests/fused_linear_ce.py:23-56): the
     op against an unfused lm_head + F.cross_entropy on fp32 logits, through autograd, with
     bf16 hidden states and an fp32 head weight: |loss difference| < 2e-3 * max(1, loss) and
-    relative L2 error of both grads < 3e-2. The unfused side uses 2-D products only."""
+    relative L2 error of both grads < 3e-2. The unfused side uses 2-D products only. The
+    last case is the trainer's own call (objectives/autoregressive.py:38-44, ce_chunk_size 4096 from :21):
+    fp32 hidden states with both sides run under bf16 autocast."""
+    import contextlib
+
     import torch.nn.functional as F
 
     from torchure_amd.loss import fused_linear_cross_entropy
 
+    fp32 = hidden_dtype == torch.float32
+    amp = (lambda: torch.autocast("cuda", dtype=torch.bfloat16)) if fp32 else contextlib.nullcontext
     torch.manual_seed(0)
-    hidden = torch.randn(b, s, d, device=DEV, dtype=torch.bfloat16) * 0.5
+    hidden = (torch.randn(b, s, d, device=DEV, dtype=torch.bfloat16) * 0.5).to(hidden_dtype)
     weight = torch.randn(v, d, device=DEV, dtype=torch.float32) * 0.02
     labels = torch.randint(0, v, (b, s), device=DEV)
     labels[torch.rand(b, s, device=DEV) < ignore_frac] = -100
 
     h1 = hidden.clone().requires_grad_(True)
     w1 = weight.clone().requires_grad_(True)
-    logits = h1.reshape(-1, d) @ w1.to(torch.bfloat16).t()
-    loss_ref = F.cross_entropy(logits.float(), labels.reshape(-1), ignore_index=-100)
+    with amp():
+        logits = h1.reshape(-1, d) @ w1.to(torch.bfloat16).t()
+        loss_ref = F.cross_entropy(logits.float(), labels.reshape(-1), ignore_index=-100)
     loss_ref.backward()
     del logits
 
     h2 = hidden.clone().requires_grad_(True)
     w2 = weight.clone().requires_grad_(True)
-    loss = fused_linear_cross_entropy(h2, w2, labels, -100, chunk)
+    with amp():
+        loss = fused_linear_cross_entropy(h2, w2, labels, -100, chunk)
     loss.backward()
 
     def rel(a, b_):
@@ -321,7 +330,7 @@ def test_reference_cases_vs_plain_cross_entropy(b, s, d, v, chunk, ignore_frac):
     assert abs(loss_ref.item() - loss.item()) < 2e-3 * max(1.0, loss_ref.item())
     assert dh < 3e-2
     assert dw < 3e-2
-    assert h2.grad.dtype == torch.bfloat16 and w2.grad.dtype == torch.float32
+    assert h2.grad.dtype == hidden_dtype and h1.grad.dtype == hidden_dtype and w2.grad.dtype == torch.float32
 
 
 @pytest.mark.parametrize("vocab", [4096, 1001, 200000])
@@ -384,3 +393,67 @@ def test_loss_without_grad_and_partial_grads(chunk):
     l2 = fused_linear_cross_entropy(h_only, weight, labels, -100, chunk)
     l2.backward()
     assert torch.equal(h_only.grad.view(torch.int16), h.grad.view(torch.int16))
+
+
+@pytest.mark.parametrize("chunk", [None, 300])
+def test_fp32_hidden_under_autocast(chunk):
+    """fp32 hidden states inside bf16 autocast, the reference trainer's call: the products
+    run on autocast's bf16 casts and grad_hidden is fp32 = float(bf16 GEMM result) * scale
+    (fused_linear_ce.py:68,80,120). With 512 valid rows the scale is a power of two, so both
+    scalings are exact and the fp32 path's results follow bit for bit from the bf16 path's on
+    hidden.to(bf16): the same loss, the same grad_W, and grad_h widened exactly. Against the
+    reference composition run under autocast the bars of the composition test hold, and fp32
+    hidden without bf16 autocast is refused."""
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(11)
+    n, d, v = 1000, 256, 4096
+    hidden = torch.randn(n, d, device=DEV, generator=g)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[torch.randperm(n, device=DEV, generator=g)[:n - 512]] = -100
+
+    hb = hidden.to(torch.bfloat16).requires_grad_(True)
+    wb = weight.clone().requires_grad_(True)
+    loss_b = fused_linear_cross_entropy(hb, wb, labels, -100, chunk)
+    loss_b.backward()
+
+    hf = hidden.clone().requires_grad_(True)
+    wf = weight.clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss_f = fused_linear_cross_entropy(hf, wf, labels, -100, chunk)
+    loss_f.backward()
+    assert hf.grad.dtype == torch.float32 and wf.grad.dtype == torch.float32
+    assert loss_f.dtype == torch.float32
+    assert loss_f.detach().view(torch.int32).item() == loss_b.detach().view(torch.int32).item()
+    assert torch.equal(wf.grad.view(torch.int32), wb.grad.view(torch.int32))
+    assert torch.equal(hf.grad.view(torch.int32), hb.grad.float().view(torch.int32))
+
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        eval_loss = fused_linear_cross_entropy(hidden, weight, labels, -100, chunk)
+    assert eval_loss.view(torch.int32).item() == loss_b.detach().view(torch.int32).item()
+
+    # a scale that is not a power of two, against the reference composition under autocast
+    labels2 = labels.clone()
+    labels2[::37] = -100
+    h2 = hidden.clone().requires_grad_(True)
+    w2 = weight.clone().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss2 = fused_linear_cross_entropy(h2, w2, labels2, -100, chunk)
+        ref_loss, ref_gh, ref_gw = fused_linear_ce_reference(hidden, weight, labels2, -100,
+                                                             chunk_size=chunk or 1024)
+    loss2.backward()
+    torch.cuda.synchronize()
+    assert ref_gh.dtype == torch.float32
+    assert abs(loss2.item() - ref_loss.item()) <= 1e-5 * abs(ref_loss.item())
+    gh_err = (h2.grad - ref_gh).abs().max().item()
+    gw_err = (w2.grad - ref_gw).abs().max().item()
+    print(f"fp32 hidden, chunk {chunk}: loss {loss2.item():.6f} ref {ref_loss.item():.6f}, "
+          f"max |d grad_h| {gh_err:.3e}, max |d grad_w| {gw_err:.3e}")
+    assert gh_err <= 1e-2 * ref_gh.abs().max().item()
+    assert gw_err <= 1e-2 * ref_gw.abs().max().item()
+
+    with pytest.raises(NotImplementedError, match="autocast"):
+        fused_linear_cross_entropy(hidden.clone().requires_grad_(True), weight, labels)
+    with pytest.raises(NotImplementedError, match="autocast"), torch.autocast("cuda", dtype=torch.float16):
+        fused_linear_cross_entropy(hidden, weight, labels)

@@ -485,6 +485,32 @@ __global__ __launch_bounds__(256) void ce_grad_w_kernel(float* __restrict__ acc,
   }
 }
 
+// Backward of fp32 hidden states, fused_linear_ce.py:68,80,120: the reference keeps grad_hidden
+// in the hidden states' dtype, so under autocast its fp32 buffer holds the widened bf16 GEMM
+// result (`grad_hidden[s:e] = gh`, -0 kept) and is scaled in fp32 (`mul_(scale)`):
+// dst = float(src) * (g / n_valid).
+__global__ __launch_bounds__(256) void ce_widen_scale_kernel(float* __restrict__ dst,
+                                                             const uint16_t* __restrict__ src, int64_t n,
+                                                             const float* __restrict__ grad_out,
+                                                             const float* __restrict__ n_valid) {
+  const float scale = *grad_out / *n_valid;
+  const bool vec = ((reinterpret_cast<uint64_t>(dst) | reinterpret_cast<uint64_t>(src)) & 15u) == 0;
+  const int64_t vend = vec ? (n & ~int64_t(7)) : 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * 8;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8; i < vend; i += stride) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(src + i);
+    f32x4 a = {lo16(w.x), hi16(w.x), lo16(w.y), hi16(w.y)};
+    f32x4 b = {lo16(w.z), hi16(w.z), lo16(w.w), hi16(w.w)};
+    a.x = a.x * scale; a.y = a.y * scale; a.z = a.z * scale; a.w = a.w * scale;
+    b.x = b.x * scale; b.y = b.y * scale; b.z = b.z * scale; b.w = b.w * scale;
+    *reinterpret_cast<f32x4*>(dst + i) = a;
+    *reinterpret_cast<f32x4*>(dst + i + 4) = b;
+  }
+  for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    dst[i] = __uint_as_float(static_cast<uint32_t>(src[i]) << 16) * scale;
+}
+
 int ce_check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return ce_fail(TM_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -586,6 +612,18 @@ int tm_ce_grad_w(float* d_grad_w, const uint16_t* d_chunk, int64_t nw, int accum
     hipLaunchKernelGGL((ce_grad_w_kernel<false, false>), grid, block, 0, s, d_grad_w, d_chunk, nw,
                        d_grad_out, d_n_valid);
   return ce_check_launch("ce_grad_w_kernel");
+}
+
+int tm_ce_widen_scale(float* d_dst, const uint16_t* d_src, int64_t n, const float* d_grad_out,
+                      const float* d_n_valid, void* stream) {
+  if (n < 0) return ce_fail(TM_EINVAL, "tm_ce_widen_scale: negative size");
+  if (n == 0) return TM_OK;
+  if (!d_dst || !d_src || !d_grad_out || !d_n_valid) return ce_fail(TM_EINVAL, "tm_ce_widen_scale: null pointer");
+  int64_t blocks = (n + 256 * 8 - 1) / (256 * 8);
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(ce_widen_scale_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), d_dst, d_src, n, d_grad_out, d_n_valid);
+  return ce_check_launch("ce_widen_scale_kernel");
 }
 
 }  // extern "C"

@@ -28,6 +28,13 @@ write, so the loss bits are those of the training path. When only one input requ
 gradient, the other's GEMM is skipped. The reference computes both gradients whenever
 the weight requires one (fused_linear_ce.py:63-93) and lets autograd drop them.
 
+Hidden states are bf16, or fp32 inside bf16 CUDA autocast: the trainer's call
+(objectives/autoregressive.py:38-44) passes the final norm's fp32 output, for which the
+reference's buffers take fp32 (:65,68) and autocast runs the products on bf16 casts. Here
+hidden is cast to bf16 once (RNE, as autocast does), grad_hidden stays a bf16 GEMM output
+until backward, and tm_ce_widen_scale writes the fp32 gradient float(gh) * grad_out / n_valid
+(the reference's fp32 copy and mul_, :80,120).
+
 MI355X sizing: the chunk is chosen so that the bf16 logits of a chunk take up to
 ``logits_bytes`` (4 GiB by default) instead of 1024 rows: with 288 GB of HBM the
 whole Qwen3 vocabulary for 8K-16K tokens fits in one chunk, so the fp32 grad_W
@@ -50,13 +57,24 @@ def auto_chunk_rows(n_rows: int, vocab: int, logits_bytes: int = DEFAULT_LOGITS_
     return max(1, min(n_rows, rows))
 
 
+def _fp32_hidden_under_autocast(hidden) -> bool:
+    """fp32 hidden states inside bf16 CUDA autocast: the reference trainer's call (its final
+    RMSNorm leaves the fp32 residual stream in fp32), where autocast runs the op's products as
+    bf16 GEMMs and the hidden-state gradient stays fp32."""
+    return (hidden.dtype == torch.float32 and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == torch.bfloat16)
+
+
 def _checked(hidden, weight, labels, chunk_size):
-    """Argument checks shared by both paths; returns (n, v, chunk rows)."""
+    """Argument checks shared by both paths; returns (n, v, chunk rows, fp32 hidden)."""
     who = "fused_linear_cross_entropy"
     for t, what in ((hidden, "hidden"), (weight, "weight"), (labels, "labels")):
         tables.require_device_tensor(t, who, what)
-    if hidden.dtype != torch.bfloat16:
-        raise NotImplementedError(f"{who}: hidden must be bfloat16 (the autocast activation dtype)")
+    fp32 = _fp32_hidden_under_autocast(hidden)
+    if hidden.dtype != torch.bfloat16 and not fp32:
+        raise NotImplementedError(
+            f"{who}: hidden must be bfloat16, or float32 inside bf16 CUDA autocast (got {hidden.dtype}, "
+            "autocast " + ("on" if torch.is_autocast_enabled("cuda") else "off") + "); the products run as bf16 GEMMs")
     if labels.dtype != torch.int64:
         raise RuntimeError(f"{who}: labels must be int64")
     n, d = hidden.shape
@@ -69,7 +87,7 @@ def _checked(hidden, weight, labels, chunk_size):
     chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
     if chunk < 1:
         raise ValueError(f"{who}: chunk_size must be positive, got {chunk_size}")
-    return n, v, chunk
+    return n, v, chunk, fp32
 
 
 def _mean_loss(row_loss, labels, n, ignore_index, lib, stream):
@@ -85,14 +103,15 @@ def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
     same logits GEMM and the same per-row arithmetic as the training path, so the same
     bits, without the two gradient GEMMs or the gradient write. The reference's forward
     computes and drops the gradients in this case (fused_linear_ce.py:63-93)."""
-    n, v, chunk = _checked(hidden, weight, labels, chunk_size)
+    n, v, chunk, fp32 = _checked(hidden, weight, labels, chunk_size)
     lib = _native.lib()
     stream = _native.stream_handle(hidden.device)
-    w = weight.to(hidden.dtype).contiguous()
+    hb = hidden.to(torch.bfloat16) if fp32 else hidden  # autocast's cast (RNE)
+    w = weight.to(torch.bfloat16).contiguous()
     row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
     for s in range(0, n, chunk):
         e = min(s + chunk, n)
-        logits = torch.matmul(hidden[s:e], w.t())
+        logits = torch.matmul(hb[s:e], w.t())
         _native.check(lib.tm_ce_rows_loss_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
                                                int(ignore_index), row_loss[s:].data_ptr(), stream),
                       "tm_ce_rows_loss_bf16")
@@ -103,12 +122,14 @@ def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
 class _FusedLinearCE(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, labels, ignore_index, chunk_size):
-        n, v, chunk = _checked(hidden, weight, labels, chunk_size)
+        n, v, chunk, fp32 = _checked(hidden, weight, labels, chunk_size)
         lib = _native.lib()
         stream = _native.stream_handle(hidden.device)
-        w = weight.to(hidden.dtype).contiguous()  # cast once, not per chunk
+        hb = hidden.to(torch.bfloat16) if fp32 else hidden  # autocast's cast (RNE)
+        w = weight.to(torch.bfloat16).contiguous()  # cast once, not per chunk
         want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        grad_hidden = torch.empty_like(hidden) if want_h else None
+        # bf16 GEMM output either way; for fp32 hidden it is widened and scaled in backward
+        grad_hidden = torch.empty(hidden.shape, dtype=torch.bfloat16, device=hidden.device) if want_h else None
         # fp32 grad_W holds chunks 0..k-2; chunk k-1 stays bf16 until backward
         grad_weight = None
         if want_w and n > chunk:
@@ -117,7 +138,7 @@ class _FusedLinearCE(torch.autograd.Function):
         row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
         for s in range(0, n, chunk):
             e = min(s + chunk, n)
-            h = hidden[s:e]
+            h = hb[s:e]
             logits = torch.matmul(h, w.t())  # (C, V) bf16
             _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
@@ -136,6 +157,7 @@ class _FusedLinearCE(torch.autograd.Function):
             del logits
         loss, ctx.n_valid = _mean_loss(row_loss, labels, n, ignore_index, lib, stream)
         ctx.grad_hidden = grad_hidden
+        ctx.fp32_hidden = fp32
         ctx.want_w = want_w
         ctx.grad_weight = grad_weight
         ctx.last_gw = last_gw
@@ -167,9 +189,19 @@ class _FusedLinearCE(torch.autograd.Function):
                 del last_gw
             else:  # no rows at all: the reference scales its zero-filled buffer
                 grad_weight = scale_w = torch.zeros(shape, dtype=torch.float32, device=device)
+        if ctx.fp32_hidden and grad_hidden is not None:
+            # fp32 hidden: the gradient is fp32 = float(bf16 GEMM result) * scale
+            wide = torch.empty(grad_hidden.shape, dtype=torch.float32, device=grad_hidden.device)
+            _native.check(lib.tm_ce_widen_scale(wide.data_ptr(), grad_hidden.data_ptr(), grad_hidden.numel(),
+                                                g.data_ptr(), n_valid.data_ptr(), stream), "tm_ce_widen_scale")
+            grad_hidden, wide = wide, grad_hidden
+            del wide
+            scale_h = None
+        else:
+            scale_h = grad_hidden
         rc = lib.tm_ce_scale_grads(
-            grad_hidden.data_ptr() if grad_hidden is not None else None,
-            grad_hidden.numel() if grad_hidden is not None else 0,
+            scale_h.data_ptr() if scale_h is not None else None,
+            scale_h.numel() if scale_h is not None else 0,
             scale_w.data_ptr() if scale_w is not None else None,
             scale_w.numel() if scale_w is not None else 0,
             g.data_ptr(), n_valid.data_ptr(), stream)
@@ -178,7 +210,7 @@ class _FusedLinearCE(torch.autograd.Function):
 
 
 def fused_linear_cross_entropy(
-    hidden: torch.Tensor,  # (B, S, D) or (N, D), bf16
+    hidden: torch.Tensor,  # (B, S, D) or (N, D), bf16 (fp32 inside bf16 autocast)
     weight: torch.Tensor,  # (V, D) lm_head weight
     labels: torch.Tensor,  # (B, S) or (N,), already shifted, int64
     ignore_index: int = -100,
