@@ -1100,6 +1100,54 @@ def test_materialize_clip_equals_eager_clip():
         assert torch.equal(a.grad, b.grad)
 
 
+@pytest.mark.parametrize("route", ["eager", "materialize"])
+def test_bf16_grads_deferred_and_in_place_clip(route):
+    """bf16 working-copy grads take one of two clip routes, each checked against its own
+    definition. The deferred clip multiplies float(g) by the fp32 coefficient inside the
+    update. That is the oracle's step on bf16 grads and the reference trainer's arithmetic:
+    autocast makes its fp32 grads float(bf16 grad), and _foreach_mul_ scales them in fp32
+    (grad_helper.py:33). An in-place scale of bf16 grads (defer_clip=False, or
+    materialize_clip()) has to store bf16. It is torch._foreach_mul_ on the bf16 list, which
+    rounds the coefficient and the product to bf16, and the step then reads those grads
+    unscaled. Both routes give the same norm; their params differ by that rounding."""
+    import torchure_amd as ta
+
+    host = H.make_host_set([(256, 192), (1000,), (77,)], seed=41, grad_std=0.05)
+    pa, wa, oa = H.device_setup(host, DEV)
+    norm_a = ta.clip_grad_norm(pa, None, 1.0)
+    coef = oa._pending[0].clone()
+    assert float(coef.item()) < 1.0  # the clip is active
+    oa.step()
+    tens = H.oracle_tensors(host)
+    oracle.reference_step(tens, H.HYPER, 1.0, clip_override=float(coef.item()))
+    w = H.compare_state(pa, wa, oa, tens)
+    assert w["p"] <= 2 and w["m"] <= 2 and w["v"] <= 2 and w["bf16"] == 0, w
+
+    pb, wb, ob = H.device_setup(host, DEV)
+    if route == "eager":
+        ob.defer_clip = False
+    grads0 = [x.grad.clone() for x in wb]
+    norm_b = ta.clip_grad_norm(pb, None, 1.0)
+    if route == "materialize":
+        assert ob._pending is not None
+        ob.materialize_clip()
+    assert ob._pending is None
+    assert norm_b.view(torch.int32).item() == norm_a.view(torch.int32).item()
+    ref = [g.clone() for g in grads0]
+    torch._foreach_mul_(ref, coef)
+    for x, r in zip(wb, ref):
+        assert torch.equal(x.grad.view(torch.int16), r.view(torch.int16))
+    ob.step()
+    tens_b = H.oracle_tensors(host)
+    for t, r in zip(tens_b, ref):
+        t["g"] = H.from_dev_bf16(r)
+    oracle.reference_step(tens_b, H.HYPER, None)
+    w = H.compare_state(pb, wb, ob, tens_b)
+    assert w["p"] <= 2 and w["m"] <= 2 and w["v"] <= 2 and w["bf16"] == 0, w
+    torch.cuda.synchronize()
+    assert any(not torch.equal(a, b) for a, b in zip(pa, pb))
+
+
 def test_step_bumps_autograd_versions():
     """The kernels write through raw pointers; the step bumps the version counters of
     everything it wrote, as torch's in-place fused AdamW does, so autograd still

@@ -15,8 +15,13 @@ Deferred clip. When every grad passed in belongs to one torchure_amd AdamW
 built with ``defer_clip=True`` (the default), the in-place multiply of
 grad_helper.py:33 is not run as a separate pass: the coefficient is handed to
 that optimizer, whose next ``step()`` multiplies each grad by it inside the
-fused update kernel (the same single fp32 multiply, so the update is bitwise
-the same). Until that step, ``p.grad`` holds the unscaled values;
+fused update kernel (the same single fp32 multiply, so for fp32 grads the update
+is bitwise the same). For bf16 grads the fused multiply keeps float(g) * coef in
+fp32, as the reference trainer does with its fp32 grads (float of the bf16 grads
+under autocast); an in-place scale of a bf16 grad has to round the product to
+bf16, as torch._foreach_mul_ on a bf16 list does (coefficient rounded too), so
+the in-place route steps on those rounded grads. Until that step, ``p.grad``
+holds the unscaled values;
 ``AdamW.materialize_clip()`` applies the pending scale in place if a caller
 needs the clipped grads before stepping. A grad modified in place between the
 clip and the step makes the step raise (scaling it afterwards would not give
