@@ -44,7 +44,9 @@ def parse():
     ap.add_argument("--chunk-elems", type=int, default=None)
     ap.add_argument("--cpu-sample-blocks", type=int, default=2,
                     help="transformer blocks of the config timed for the CPU baseline (0 = skip)")
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=3, help="at least this many timed CPU steps")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="keep timing CPU steps until this much CPU work has been timed (at most 500 steps)")
     ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,qwen3-4b-dropin,"
                                       "qwen3-4b-ddpbuckets,ragged",
                     help="comma list of extra configs reported under 'extra' (empty = none)")
@@ -478,9 +480,11 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
     return out
 
 
-def run_cpu_baseline(config: str, blocks: int, steps: int):
+def run_cpu_baseline(config: str, blocks: int, steps: int, seconds: float = 10.0):
     """Reference composition on torch CPU over the first ``blocks`` transformer
-    blocks of ``config`` (the sample), bf16 grads widened to fp32."""
+    blocks of ``config`` (the sample), bf16 grads widened to fp32: at least ``steps``
+    timed steps, and more until ``seconds`` of CPU work have been timed; the median
+    step is reported."""
     import torch
 
     from oracle.torch_composition import make_reference_optimizer, reference_step
@@ -504,7 +508,7 @@ def run_cpu_baseline(config: str, blocks: int, steps: int):
     n = sum(p.numel() for p in params)
     reference_step(params, opt, 1.0, bf16)  # warm-up
     times = []
-    for _ in range(steps):
+    while len(times) < steps or (sum(times) < seconds and len(times) < 500):
         t0 = time.perf_counter()
         reference_step(params, opt, 1.0, bf16)
         times.append(time.perf_counter() - t0)
@@ -515,7 +519,8 @@ def run_cpu_baseline(config: str, blocks: int, steps: int):
         cores=threads,
         kind="port",
         sample=(f"{config} blocks 0..{blocks - 1} ({len(params)} tensors, {n} params), median of "
-                f"{steps} steps after 1 warm-up, {med * 1e3:.1f} ms/step; torch CPU foreach-norm clip + "
+                f"{len(times)} steps ({sum(times):.1f} s of timed CPU work) after 1 warm-up, "
+                f"{med * 1e3:.1f} ms/step; torch CPU foreach-norm clip + "
                 f"AdamW(fused=True) + bf16 cast; GB/s on the same 30 B/param basis; "
                 f"{threads} threads of {os.cpu_count()} logical CPUs, host RAM {_host_ram_gib()} GiB"),
     )
@@ -607,7 +612,7 @@ def main():
     upd_gbs = n * UPDATE_BYTES_PER_PARAM / (main_res["update_ms_mean"] * 1e-3) / 1e9
     cpu = None
     if args.cpu_sample_blocks > 0:
-        cpu = run_cpu_baseline(args.config, args.cpu_sample_blocks, args.cpu_steps)
+        cpu = run_cpu_baseline(args.config, args.cpu_sample_blocks, args.cpu_steps, args.cpu_seconds)
     line = {
         "metric": "optimizer step ms + achieved HBM GB/s (% of peak), Qwen3-0.6B & 4B shapes",
         "value": round(value, 1),
