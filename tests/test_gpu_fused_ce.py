@@ -457,3 +457,39 @@ def test_fp32_hidden_under_autocast(chunk):
         fused_linear_cross_entropy(hidden.clone().requires_grad_(True), weight, labels)
     with pytest.raises(NotImplementedError, match="autocast"), torch.autocast("cuda", dtype=torch.float16):
         fused_linear_cross_entropy(hidden, weight, labels)
+
+
+@pytest.mark.parametrize("ignore_index", [7, 0])
+def test_ignore_index_inside_the_vocabulary(ignore_index):
+    """ignore_index may be a real class id (F.cross_entropy semantics, fused_linear_ce.py:40,86):
+    rows labelled with it are left out of the loss, the mean and both gradients, and the class
+    is still scored for the other rows. Checked against the reference composition with the same
+    ignore_index, in one chunk and in several, at that test's bars."""
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(100 + ignore_index)
+    n, d, v = 700, 128, 1000
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[labels == ignore_index] = (ignore_index + 2) % v  # only the rows set below are ignored
+    labels[1::9] = (ignore_index + 1) % v  # the neighbouring class, scored as usual
+    labels[::5] = ignore_index
+    for chunk in (None, 128):
+        h = hidden.clone().requires_grad_(True)
+        w = weight.clone().requires_grad_(True)
+        loss = fused_linear_cross_entropy(h, w, labels, ignore_index, chunk)
+        loss.backward()
+        ref_loss, ref_gh, ref_gw = fused_linear_ce_reference(hidden, weight, labels, ignore_index,
+                                                             chunk_size=chunk or 1024)
+        torch.cuda.synchronize()
+        assert abs(loss.item() - ref_loss.item()) <= 1e-5 * abs(ref_loss.item())
+        assert (h.grad[::5] == 0).all()  # ignored rows get no gradient
+        assert (h.grad[1::5].abs().sum(dim=1) > 0).all()
+        gh_err = (h.grad.float() - ref_gh.float()).abs().max().item()
+        gw_err = (w.grad - ref_gw).abs().max().item()
+        assert gh_err <= 1e-2 * ref_gh.float().abs().max().item()
+        assert gw_err <= 1e-2 * ref_gw.abs().max().item()
+        with torch.no_grad():
+            ev = fused_linear_cross_entropy(hidden, weight, labels, ignore_index, chunk)
+        assert ev.view(torch.int32).item() == loss.detach().view(torch.int32).item()
