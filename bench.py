@@ -452,6 +452,18 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
 
     out["loss_only_ms"] = round(timed(evaluate), 4)
     out["loss_only_TFLOPs"] = round(2.0 * n * d * v / (out["loss_only_ms"] * 1e-3) / 1e12, 1)
+
+    hidden32 = hidden.float()
+
+    def ours_fp32_hidden():  # the trainer's call: fp32 hidden states inside bf16 autocast
+        h = hidden32.detach().requires_grad_(True)
+        w = weight.detach().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = fused_linear_cross_entropy(h, w, labels, -100, 4096)
+        loss.backward()
+
+    out["fp32_hidden_autocast_chunk4096_ms"] = round(timed(ours_fp32_hidden), 4)
+    del hidden32
     if with_reference:
         comp = torch.compile(_ce_chunk_reference, dynamic=False)
 
@@ -470,11 +482,33 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
             gh_all.mul_((1.0 / nv).to(gh_all.dtype))
             gw_all.mul_(1.0 / nv)
 
+        hidden32 = hidden.float()
+
+        def ref_fp32_hidden():  # the trainer's call on the reference side (chunk 4096, autocast)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                w = weight.to(hidden32.dtype)
+                loss_sum = torch.zeros((), dtype=torch.float32, device=dev)
+                gh_all = torch.empty_like(hidden32)
+                gw_all = torch.zeros_like(weight)
+                for s in range(0, n, 4096):
+                    e = min(s + 4096, n)
+                    cl, gh, gw = comp(hidden32[s:e], w, labels[s:e], -100)
+                    loss_sum += cl
+                    gh_all[s:e] = gh
+                    gw_all += gw
+                nv = (labels != -100).sum().clamp_min(1)
+                gh_all.mul_((1.0 / nv).to(gh_all.dtype))
+                gw_all.mul_(1.0 / nv)
+
         try:
             out["reference_compiled_ms"] = round(timed(ref), 4)
             out["speedup_vs_reference_compiled"] = round(out["reference_compiled_ms"] / out["ms"], 3)
+            out["reference_compiled_fp32_hidden_autocast_chunk4096_ms"] = round(timed(ref_fp32_hidden), 4)
+            out["speedup_fp32_hidden_autocast_chunk4096"] = round(
+                out["reference_compiled_fp32_hidden_autocast_chunk4096_ms"] / out["fp32_hidden_autocast_chunk4096_ms"], 3)
         except Exception as e:  # torch.compile unavailable: report, do not fail the bench
             out["reference_compiled_error"] = repr(e)[:200]
+        del hidden32
     del hidden, weight, labels
     torch.cuda.empty_cache()
     return out
