@@ -251,6 +251,16 @@ int tm_ce_grad_w(float* d_grad_w, const uint16_t* d_chunk, int64_t nw, int accum
                  const float* d_grad_out, const float* d_n_valid, void* stream);
 
 /*
+ * The same hand-over for two consecutive chunks in one pass (fused_linear_ce.py:80-81 run
+ * for chunk k and then chunk k+1, and :126 when d_grad_out is given):
+ *   d_grad_w[i] = (((accumulate ? d_grad_w[i] : +0.0f) + float(d_chunk[i])) + float(d_chunk2[i])) [* scale]
+ * the reference's fp32 additions in its order, reading and writing the accumulator once
+ * for both chunks.
+ */
+int tm_ce_grad_w2(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d_chunk2, int64_t nw,
+                  int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream);
+
+/*
  * grad_hidden of fp32 hidden states (fused_linear_ce.py:68,80,120 under autocast: the
  * buffer has the hidden states' dtype, holds the widened bf16 GEMM result and is scaled
  * in place in fp32): d_dst[i] = float(d_src[i]) * (*d_grad_out / *d_n_valid), -0 kept.

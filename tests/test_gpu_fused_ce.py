@@ -195,17 +195,58 @@ def test_ce_grad_w_handover_bit_exact(accumulate, scaled, n, offset):
     assert np.array_equal(a, b), np.argwhere(a != b)[:5]
 
 
-def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops():
-    """The deferred last chunk changes nothing: grad_W of the op with three chunks
-    equals, bit for bit, the reference's chunk loop run on the same kernels -- zero
-    buffer, `+=` of each chunk's bf16 grad_W, then `mul_(grad_out / n_valid)`
-    (fused_linear_ce.py:67-91,117-126) -- and grad_h likewise
+@pytest.mark.parametrize("accumulate,scaled,n,offset", [
+    (0, 0, 4096, 0), (1, 0, 4096, 0), (0, 1, 4096, 0), (1, 1, 4096, 0), (1, 1, 1003, 0), (0, 1, 777, 3)])
+def test_ce_grad_w2_handover_bit_exact(accumulate, scaled, n, offset):
+    """tm_ce_grad_w2 (two chunks in one pass) vs the reference's torch ops on the same data:
+    `grad_weight += gw` for one chunk and then the next, on a zero-filled (or given) fp32
+    buffer, then `mul_(grad_out / n_valid)` (fused_linear_ce.py:80-81,126), bit for bit,
+    with -0, +-inf, NaN and subnormal bf16 inputs, odd sizes and unaligned buffers."""
+    from torchure_amd import _native
+
+    r = H.rng(3 * n + 11 * offset + accumulate + 5)
+    bits = []
+    for k in range(2):
+        b = oracle.bf16_rne((r.standard_normal(n + offset) * 0.3).astype(np.float32))
+        b[offset + 3 * k:offset + 3 * k + 6] = [0x8000, 0x0000, 0x7F80, 0xFF80, 0x7FC0, 0x0001]
+        bits.append(torch.from_numpy(b.view(np.int16).copy()).to(DEV)[offset:])
+    acc0 = torch.from_numpy((r.standard_normal(n + offset) * 0.1).astype(np.float32)).to(DEV)[offset:]
+    acc0[0] = acc0[9] = -0.0
+    grad_out = torch.tensor([0.37], dtype=torch.float32, device=DEV)
+    n_valid = torch.tensor([977.0], dtype=torch.float32, device=DEV)
+
+    want = acc0.clone() if accumulate else torch.zeros(n, dtype=torch.float32, device=DEV)
+    want += bits[0].view(torch.bfloat16).float()
+    want += bits[1].view(torch.bfloat16).float()
+    if scaled:
+        want.mul_(grad_out[0] / n_valid[0])
+
+    got_base = torch.full((n + offset,), 123.0, dtype=torch.float32, device=DEV)
+    got = got_base[offset:]
+    if accumulate:
+        got.copy_(acc0)
+    rc = _native.lib().tm_ce_grad_w2(got.data_ptr(), bits[0].data_ptr(), bits[1].data_ptr(), n, accumulate,
+                                     grad_out.data_ptr() if scaled else None,
+                                     n_valid.data_ptr() if scaled else None, _native.stream_handle(DEV))
+    _native.check(rc, "tm_ce_grad_w2")
+    torch.cuda.synchronize()
+    a = got.cpu().numpy().view(np.uint32)
+    b = want.cpu().numpy().view(np.uint32)
+    assert np.array_equal(a, b), np.argwhere(a != b)[:5]
+
+
+@pytest.mark.parametrize("chunk", [700, 350, 256, 175, 100])
+def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops(chunk):
+    """Pairing the chunks' hand-overs and deferring the last chunk change nothing: grad_W of
+    the op with 1, 2, 3, 4 and 7 chunks equals, bit for bit, the reference's chunk loop run
+    on the same kernels -- zero buffer, `+=` of each chunk's bf16 grad_W, then
+    `mul_(grad_out / n_valid)` (fused_linear_ce.py:67-91,117-126) -- and grad_h likewise
     (`grad_hidden[s:e] = gh`, then `mul_(scale.to(bf16))`)."""
     from torchure_amd import _native
     from torchure_amd.loss import fused_linear_cross_entropy
 
     g = torch.Generator(device=DEV).manual_seed(11)
-    n, d, v, chunk = 700, 128, 2048, 256
+    n, d, v = 700, 128, 2048
     hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
     weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
     labels = torch.randint(0, v, (n,), device=DEV, generator=g)

@@ -93,6 +93,7 @@ _SIGNATURES = {
     "tm_ce_loss": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "tm_ce_scale_grads": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp]),
     "tm_ce_grad_w": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_int, _vp, _vp, _vp]),
+    "tm_ce_grad_w2": (ctypes.c_int, [_vp, _vp, _vp, _i64, ctypes.c_int, _vp, _vp, _vp]),
     "tm_ce_widen_scale": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp]),
 }
 

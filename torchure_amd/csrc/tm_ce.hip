@@ -448,28 +448,41 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(uint16_t* __restrict__ gh
 
 // grad_W hand-over, fused_linear_ce.py:80-81,126: the fp32 accumulator gets one more
 // chunk, acc = acc + float(chunk) (kAccumulate) or acc = 0 + float(chunk) (first chunk:
-// the reference adds into a zero-filled buffer, and +0 + x also maps -0 to +0), then,
-// with kScale (the backward of the last chunk), acc *= g / n_valid. Each element sees
-// the same fp32 operations in the same order as the reference's `+=` then `mul_`.
+// the reference adds into a zero-filled buffer, and +0 + x also maps -0 to +0), and with
+// kTwo a second chunk after it, acc = (acc + float(chunk)) + float(chunk2), so two chunks
+// cost one pass over the accumulator. Then, with kScale (the backward of the last chunk),
+// acc *= g / n_valid. Each element sees the same fp32 operations in the same order as the
+// reference's `+=` per chunk, then `mul_`.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <bool kAccumulate, bool kScale>
+template <bool kAccumulate, bool kScale, bool kTwo>
 __global__ __launch_bounds__(256) void ce_grad_w_kernel(float* __restrict__ acc,
-                                                        const uint16_t* __restrict__ chunk, int64_t n,
+                                                        const uint16_t* __restrict__ chunk,
+                                                        const uint16_t* __restrict__ chunk2, int64_t n,
                                                         const float* __restrict__ grad_out,
                                                         const float* __restrict__ n_valid) {
   const float scale = kScale ? *grad_out / *n_valid : 1.0f;
-  const bool vec = ((reinterpret_cast<uint64_t>(acc) | reinterpret_cast<uint64_t>(chunk)) & 15u) == 0;
+  const uint64_t addr_bits = reinterpret_cast<uint64_t>(acc) | reinterpret_cast<uint64_t>(chunk) |
+                             (kTwo ? reinterpret_cast<uint64_t>(chunk2) : 0u);
+  const bool vec = (addr_bits & 15u) == 0;
   const int64_t vend = vec ? (n & ~int64_t(7)) : 0;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * 8;
   for (int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8; i < vend; i += stride) {
     const u32x4 w = *reinterpret_cast<const u32x4*>(chunk + i);
+    u32x4 w2 = {0u, 0u, 0u, 0u};
+    if constexpr (kTwo) w2 = *reinterpret_cast<const u32x4*>(chunk2 + i);
     f32x4 a = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 b = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i + 4) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     a.x = a.x + lo16(w.x); a.y = a.y + hi16(w.x);
     a.z = a.z + lo16(w.y); a.w = a.w + hi16(w.y);
     b.x = b.x + lo16(w.z); b.y = b.y + hi16(w.z);
     b.z = b.z + lo16(w.w); b.w = b.w + hi16(w.w);
+    if constexpr (kTwo) {
+      a.x = a.x + lo16(w2.x); a.y = a.y + hi16(w2.x);
+      a.z = a.z + lo16(w2.y); a.w = a.w + hi16(w2.y);
+      b.x = b.x + lo16(w2.z); b.y = b.y + hi16(w2.z);
+      b.z = b.z + lo16(w2.w); b.w = b.w + hi16(w2.w);
+    }
     if (kScale) {
       a.x = a.x * scale; a.y = a.y * scale; a.z = a.z * scale; a.w = a.w * scale;
       b.x = b.x * scale; b.y = b.y * scale; b.z = b.z * scale; b.w = b.w * scale;
@@ -480,6 +493,7 @@ __global__ __launch_bounds__(256) void ce_grad_w_kernel(float* __restrict__ acc,
   for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * 256) {
     float x = (kAccumulate ? acc[i] : 0.0f) + __uint_as_float(static_cast<uint32_t>(chunk[i]) << 16);
+    if constexpr (kTwo) x = x + __uint_as_float(static_cast<uint32_t>(chunk2[i]) << 16);
     if (kScale) x = x * scale;
     acc[i] = x;
   }
@@ -546,6 +560,34 @@ int ce_rows_launch(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int6
   return TM_OK;
 }
 
+template <bool kTwo>
+int ce_grad_w_launch(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d_chunk2, int64_t nw,
+                     int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream,
+                     const char* who) {
+  if (nw < 0) return ce_fail(TM_EINVAL, "%s: negative size", who);
+  if (nw == 0) return TM_OK;
+  if (!d_grad_w || !d_chunk || (kTwo && !d_chunk2) || (d_grad_out != nullptr) != (d_n_valid != nullptr))
+    return ce_fail(TM_EINVAL, "%s: null pointer", who);
+  int64_t blocks = (nw + 256 * 8 - 1) / (256 * 8);
+  if (blocks > 65536) blocks = 65536;
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool scale = d_grad_out != nullptr;
+  if (accumulate && scale)
+    hipLaunchKernelGGL((ce_grad_w_kernel<true, true, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
+                       nw, d_grad_out, d_n_valid);
+  else if (accumulate)
+    hipLaunchKernelGGL((ce_grad_w_kernel<true, false, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
+                       nw, d_grad_out, d_n_valid);
+  else if (scale)
+    hipLaunchKernelGGL((ce_grad_w_kernel<false, true, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
+                       nw, d_grad_out, d_n_valid);
+  else
+    hipLaunchKernelGGL((ce_grad_w_kernel<false, false, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
+                       nw, d_grad_out, d_n_valid);
+  return ce_check_launch("ce_grad_w_kernel");
+}
+
 }  // namespace
 
 extern "C" {
@@ -590,28 +632,14 @@ int tm_ce_scale_grads(uint16_t* d_grad_h, int64_t nh, float* d_grad_w, int64_t n
 
 int tm_ce_grad_w(float* d_grad_w, const uint16_t* d_chunk, int64_t nw, int accumulate,
                  const float* d_grad_out, const float* d_n_valid, void* stream) {
-  if (nw < 0) return ce_fail(TM_EINVAL, "tm_ce_grad_w: negative size");
-  if (nw == 0) return TM_OK;
-  if (!d_grad_w || !d_chunk || (d_grad_out != nullptr) != (d_n_valid != nullptr))
-    return ce_fail(TM_EINVAL, "tm_ce_grad_w: null pointer");
-  int64_t blocks = (nw + 256 * 8 - 1) / (256 * 8);
-  if (blocks > 65536) blocks = 65536;
-  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool scale = d_grad_out != nullptr;
-  if (accumulate && scale)
-    hipLaunchKernelGGL((ce_grad_w_kernel<true, true>), grid, block, 0, s, d_grad_w, d_chunk, nw,
-                       d_grad_out, d_n_valid);
-  else if (accumulate)
-    hipLaunchKernelGGL((ce_grad_w_kernel<true, false>), grid, block, 0, s, d_grad_w, d_chunk, nw,
-                       d_grad_out, d_n_valid);
-  else if (scale)
-    hipLaunchKernelGGL((ce_grad_w_kernel<false, true>), grid, block, 0, s, d_grad_w, d_chunk, nw,
-                       d_grad_out, d_n_valid);
-  else
-    hipLaunchKernelGGL((ce_grad_w_kernel<false, false>), grid, block, 0, s, d_grad_w, d_chunk, nw,
-                       d_grad_out, d_n_valid);
-  return ce_check_launch("ce_grad_w_kernel");
+  return ce_grad_w_launch<false>(d_grad_w, d_chunk, nullptr, nw, accumulate, d_grad_out, d_n_valid, stream,
+                                 "tm_ce_grad_w");
+}
+
+int tm_ce_grad_w2(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d_chunk2, int64_t nw,
+                  int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream) {
+  return ce_grad_w_launch<true>(d_grad_w, d_chunk, d_chunk2, nw, accumulate, d_grad_out, d_n_valid, stream,
+                                "tm_ce_grad_w2");
 }
 
 int tm_ce_widen_scale(float* d_dst, const uint16_t* d_src, int64_t n, const float* d_grad_out,

@@ -18,8 +18,11 @@ The last chunk's bf16 grad_W is not added in forward: it waits for backward, whe
 tm_ce_grad_w adds it and applies grad_out / n_valid in the same pass. With a single
 chunk (the usual case at 4 GiB of logits) the fp32 grad_W is then written once,
 straight from the bf16 GEMM output (6 B per element), instead of a zero fill, an
-accumulate and a scaling pass (22 B per element); the fp32 additions and the scaling
-are the reference's, in the reference's order, so the bits are unchanged.
+accumulate and a scaling pass (22 B per element). With several chunks, the chunks'
+bf16 grad_W are added two at a time (tm_ce_grad_w2: one read and one write of the fp32
+grad_W per pair), and an unpaired chunk before the last is added together with the last
+in backward. The fp32 additions and the scaling are the reference's, in the reference's
+order, so the bits are unchanged.
 
 Only the gradients autograd needs are computed. With grad mode off, or no input that
 requires a gradient (evaluation), the call returns the loss from the logits GEMM and
@@ -130,11 +133,11 @@ class _FusedLinearCE(torch.autograd.Function):
         want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         # bf16 GEMM output either way; for fp32 hidden it is widened and scaled in backward
         grad_hidden = torch.empty(hidden.shape, dtype=torch.bfloat16, device=hidden.device) if want_h else None
-        # fp32 grad_W holds chunks 0..k-2; chunk k-1 stays bf16 until backward
+        # Chunks' bf16 grad_W are added to the fp32 grad_W two at a time (one pass for each
+        # pair); the last chunk, and an unpaired one before it, wait for backward.
         grad_weight = None
-        if want_w and n > chunk:
-            grad_weight = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
-        last_gw, accumulated = None, False
+        pending = last_gw = None
+        accumulated = False
         row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
         for s in range(0, n, chunk):
             e = min(s + chunk, n)
@@ -147,19 +150,26 @@ class _FusedLinearCE(torch.autograd.Function):
                 torch.matmul(logits, w, out=grad_hidden[s:e])
             if want_w:
                 gw = torch.matmul(logits.t(), h)  # (V, D) bf16
-                if e < n:
-                    _native.check(lib.tm_ce_grad_w(grad_weight.data_ptr(), gw.data_ptr(), gw.numel(),
-                                                   int(accumulated), None, None, stream), "tm_ce_grad_w")
-                    accumulated = True
-                    del gw
-                else:
+                if e == n:
                     last_gw = gw
+                elif pending is None:
+                    pending = gw
+                else:
+                    if grad_weight is None:
+                        grad_weight = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
+                    _native.check(lib.tm_ce_grad_w2(grad_weight.data_ptr(), pending.data_ptr(), gw.data_ptr(),
+                                                    gw.numel(), int(accumulated), None, None, stream),
+                                  "tm_ce_grad_w2")
+                    accumulated = True
+                    pending = None
+                    del gw
             del logits
         loss, ctx.n_valid = _mean_loss(row_loss, labels, n, ignore_index, lib, stream)
         ctx.grad_hidden = grad_hidden
         ctx.fp32_hidden = fp32
         ctx.want_w = want_w
         ctx.grad_weight = grad_weight
+        ctx.pending_gw = pending
         ctx.last_gw = last_gw
         ctx.accumulated = accumulated
         ctx.weight_meta = (weight.shape, weight.device)
@@ -172,8 +182,8 @@ class _FusedLinearCE(torch.autograd.Function):
                 "fused_linear_cross_entropy: backward called twice. the stashed grads are "
                 "consumed in place on the first call, so retain_graph does not work through this op")
         grad_hidden, grad_weight, n_valid = ctx.grad_hidden, ctx.grad_weight, ctx.n_valid
-        last_gw = ctx.last_gw
-        ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = ctx.last_gw = None
+        last_gw, pending = ctx.last_gw, ctx.pending_gw
+        ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = ctx.last_gw = ctx.pending_gw = None
         lib = _native.lib()
         stream = _native.stream_handle(n_valid.device)
         g = grad_out.detach().to(torch.float32).contiguous()
@@ -183,10 +193,15 @@ class _FusedLinearCE(torch.autograd.Function):
             if last_gw is not None:
                 if grad_weight is None:
                     grad_weight = torch.empty(shape, dtype=torch.float32, device=device)
-                _native.check(lib.tm_ce_grad_w(grad_weight.data_ptr(), last_gw.data_ptr(), last_gw.numel(),
-                                               int(ctx.accumulated), g.data_ptr(), n_valid.data_ptr(),
-                                               stream), "tm_ce_grad_w")
-                del last_gw
+                if pending is not None:  # the unpaired chunk before the last, then the last
+                    _native.check(lib.tm_ce_grad_w2(grad_weight.data_ptr(), pending.data_ptr(),
+                                                    last_gw.data_ptr(), last_gw.numel(), int(ctx.accumulated),
+                                                    g.data_ptr(), n_valid.data_ptr(), stream), "tm_ce_grad_w2")
+                else:
+                    _native.check(lib.tm_ce_grad_w(grad_weight.data_ptr(), last_gw.data_ptr(), last_gw.numel(),
+                                                   int(ctx.accumulated), g.data_ptr(), n_valid.data_ptr(),
+                                                   stream), "tm_ce_grad_w")
+                del last_gw, pending
             else:  # no rows at all: the reference scales its zero-filled buffer
                 grad_weight = scale_w = torch.zeros(shape, dtype=torch.float32, device=device)
         if ctx.fp32_hidden and grad_hidden is not None:
