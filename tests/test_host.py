@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import os
+
 import pytest
 import torch
 
@@ -291,3 +293,15 @@ def test_bench_ddp_bucket_layout():
     assert g50.untyped_storage().data_ptr() == g200.untyped_storage().data_ptr()
     assert g200.data_ptr() == g50.data_ptr() + 4 * 50_000
     assert torch.equal(g50, torch.full((50_000,), 2.0)) and torch.equal(g200, torch.full((200_000,), 1.0))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits with a message: this build has no cross-GPU path."""
+    import subprocess
+    import sys as _sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    p = subprocess.run([_sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120, cwd=root)
+    assert p.returncode == 2
+    assert "one GPU only" in p.stderr and not p.stdout.strip()
