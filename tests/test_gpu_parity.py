@@ -1651,3 +1651,34 @@ def test_training_loop_with_clip_tracks_torch():
     torch.testing.assert_close(loss_a, loss_b, rtol=1e-5, atol=0)
     for (name, p), q in zip(mine.named_parameters(), model_r.parameters()):
         torch.testing.assert_close(p, q, rtol=1e-4, atol=2e-6, msg=name)
+
+
+def test_launch_planned_on_one_stream_runs_on_another():
+    """A step planned (tables uploaded, workspace allocated) on the default stream and launched
+    on a side stream waits for the upload and keeps its buffers alive there: it gives the bits
+    of the same step run on one stream. The same for a norm launch."""
+    from torchure_amd.core.grad_helper import NormLaunch
+
+    host = H.make_host_set([(300, 200), (1000,), (33,)], seed=44, grad_std=0.01)
+    pa, wa, oa = H.device_setup(host, DEV)
+    pb, wb, ob = H.device_setup(host, DEV)
+    for launch in oa.plan_step():
+        launch()
+    side = torch.cuda.Stream(device=DEV)
+    launches = ob.plan_step()
+    norm_a = NormLaunch([w.grad for w in wa], 1.0)
+    norm_a()
+    norm_b = NormLaunch([w.grad for w in wb], 1.0)
+    with torch.cuda.stream(side):
+        for launch in launches:
+            launch()
+        norm_b()
+    torch.cuda.current_stream(DEV).wait_stream(side)
+    torch.cuda.synchronize()
+    for x, y, u, v in zip(pa, pb, wa, wb):
+        assert torch.equal(x, y)
+        assert torch.equal(u.view(torch.int16), v.view(torch.int16))
+        for k in ("step", "exp_avg", "exp_avg_sq"):
+            assert torch.equal(oa.state[x][k], ob.state[y][k])
+    assert norm_a.norm.view(torch.int32).item() == norm_b.norm.view(torch.int32).item()
+    assert norm_a.coef.view(torch.int32).item() == norm_b.coef.view(torch.int32).item()

@@ -79,8 +79,11 @@ class NormLaunch:
         self.clip = max_norm is not None
         self.max_norm = float(max_norm) if self.clip else 0.0
         self.coef = torch.empty((), dtype=torch.float32, device=device) if self.clip else None
+        self.home = torch.cuda.current_stream(device)
 
     def __call__(self) -> None:
+        tables.follow_home_stream(self.home, self.device,
+                                  (self.d_rows, self.chunks, self.ws, self.norm, self.coef))
         rc = _native.lib().tm_grad_norm(
             self.d_rows.data_ptr(),
             self.n,

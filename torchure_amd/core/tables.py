@@ -114,6 +114,20 @@ class ChunkTableCache:
 CHUNKS = ChunkTableCache()
 
 
+def follow_home_stream(home, device: torch.device, tensors) -> None:
+    """Before a launch that was planned on stream ``home`` runs on the device's current stream:
+    if the two differ, the current stream waits for ``home`` (the tables were uploaded there,
+    asynchronously) and each tensor is marked as used on the current stream, so the caching
+    allocator does not hand its block to other work before this stream is done with it."""
+    cur = torch.cuda.current_stream(device)
+    if cur == home:
+        return
+    cur.wait_stream(home)
+    for t in tensors:
+        if t is not None:
+            t.record_stream(cur)
+
+
 def check_chunk_elems(chunk_elems: int) -> int:
     chunk_elems = int(chunk_elems)
     if chunk_elems <= 0 or chunk_elems % _native.TM_CHUNK_ALIGN:

@@ -580,6 +580,8 @@ class StepLaunch:
     Calling it enqueues the prep + update kernels on the device's current
     stream. Calling it again re-applies one more AdamW step to the same
     tensors with the same grads (used to time the kernels back to back).
+    A call on a stream other than the one it was planned on first waits for
+    that stream, where its table was uploaded.
     """
 
     def __init__(self, device, d_rows, n, chunks, n_chunks, chunk_elems, groups_c, n_groups, coef,
@@ -597,8 +599,10 @@ class StepLaunch:
         self.n_groups = n_groups
         self.coef = coef
         self.ws = torch.empty(_native.workspace_bytes(n), dtype=torch.uint8, device=device)
+        self.home = torch.cuda.current_stream(device)  # where the table was uploaded
 
     def __call__(self) -> None:
+        tables.follow_home_stream(self.home, self.device, (self.d_rows, self.chunks, self.ws))
         rc = _native.lib().tm_adamw_step(
             self.d_rows.data_ptr(),
             self.n,
