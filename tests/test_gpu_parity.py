@@ -1205,9 +1205,17 @@ def test_deferred_clip_rejects_grads_modified_in_place():
     """The reference scales at clip time; a grad changed in place before the step cannot
     be reproduced by scaling later, so the deferred path raises instead of diverging."""
     params, opt, _ = _clip_setup(True)
+    before = [p.detach().clone() for p in params]
     params[1].grad.add_(1.0)
     with pytest.raises(RuntimeError, match="modified in place"):
         opt.step()
+    # the clip stays pending: a second step is refused too, not run on unscaled grads
+    with pytest.raises(RuntimeError, match="modified in place"):
+        opt.step()
+    torch.cuda.synchronize()
+    assert all(torch.equal(p, b) for p, b in zip(params, before))
+    opt.zero_grad()  # drops the pending clip with the grads
+    assert opt._pending is None
     params, opt, _ = _clip_setup(True)
     params[0].grad.mul_(2.0)
     with pytest.raises(RuntimeError, match="modified in place"):

@@ -230,9 +230,12 @@ class AdamW(torch.optim.Optimizer):
                 loss = closure()
 
         pending = self._pending
-        self._pending = None
         coef, clip_ids = pending if pending is not None else (None, ())
-        for launch in self.plan_step(coef, clip_ids):
+        # a refused step (a grad changed in place since the clip) keeps the clip pending, so
+        # a second step() refuses too instead of stepping on unscaled grads; zero_grad() drops it
+        launches = self.plan_step(coef, clip_ids)
+        self._pending = None
+        for launch in launches:
             launch()
         return loss
 
