@@ -1220,6 +1220,8 @@ def test_deferred_clip_rejects_grads_modified_in_place():
     params[0].grad.mul_(2.0)
     with pytest.raises(RuntimeError, match="modified in place"):
         opt.materialize_clip()
+    with pytest.raises(RuntimeError, match="modified in place"):
+        opt.step()
 
 
 def test_deferred_clip_with_replaced_grad_matches_eager():

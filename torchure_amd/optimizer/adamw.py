@@ -213,11 +213,11 @@ class AdamW(torch.optim.Optimizer):
         if self._pending is None:
             return
         coef, rec = self._pending
-        self._pending = None
         from torchure_amd.core.grad_helper import scale_grads_
 
         if not np.array_equal(_native.host().versions(rec.grads), rec.versions):
-            raise self._modified_error()
+            raise self._modified_error()  # the clip stays pending, as after a refused step()
+        self._pending = None
         scale_grads_(rec.grads, coef)
 
     # ------------------------------------------------------------ step
