@@ -534,3 +534,36 @@ def test_ignore_index_inside_the_vocabulary(ignore_index):
         with torch.no_grad():
             ev = fused_linear_cross_entropy(hidden, weight, labels, ignore_index, chunk)
         assert ev.view(torch.int32).item() == loss.detach().view(torch.int32).item()
+
+
+def test_non_contiguous_inputs_give_the_contiguous_bits():
+    """hidden as a transposed view and a strided weight slice: the op works on contiguous
+    copies (as torch's products accept any strides), so loss and both gradients equal the
+    contiguous call bit for bit, and the gradients reach the views' bases."""
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(21)
+    n, d, v = 600, 128, 3000
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::11] = -100
+
+    h1 = hidden.clone().requires_grad_(True)
+    w1 = weight.clone().requires_grad_(True)
+    l1 = fused_linear_cross_entropy(h1, w1, labels, -100, 256)
+    l1.backward()
+
+    hbase = hidden.t().contiguous().requires_grad_(True)  # (d, n); its transpose is (n, d), strided
+    wbase = torch.zeros(v, 2 * d, device=DEV)
+    wbase[:, ::2] = weight
+    wbase.requires_grad_(True)
+    h2, w2 = hbase.t(), wbase[:, ::2]
+    assert not h2.is_contiguous() and not w2.is_contiguous()
+    l2 = fused_linear_cross_entropy(h2, w2, labels, -100, 256)
+    l2.backward()
+    torch.cuda.synchronize()
+    assert l1.detach().view(torch.int32).item() == l2.detach().view(torch.int32).item()
+    assert torch.equal(hbase.grad.t().contiguous().view(torch.int16), h1.grad.view(torch.int16))
+    assert torch.equal(wbase.grad[:, ::2].contiguous().view(torch.int32), w1.grad.view(torch.int32))
+    assert torch.count_nonzero(wbase.grad[:, 1::2]).item() == 0

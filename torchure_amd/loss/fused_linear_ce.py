@@ -71,8 +71,11 @@ def _fp32_hidden_under_autocast(hidden) -> bool:
 def _checked(hidden, weight, labels, chunk_size):
     """Argument checks shared by both paths; returns (n, v, chunk rows, fp32 hidden)."""
     who = "fused_linear_cross_entropy"
-    for t, what in ((hidden, "hidden"), (weight, "weight"), (labels, "labels")):
+    for t, what in ((hidden, "hidden"), (labels, "labels")):  # made contiguous by the caller
         tables.require_device_tensor(t, who, what)
+    if weight.device.type != "cuda":  # any strides: the op works on its contiguous bf16 cast
+        raise RuntimeError(f"{who}: weight must be on a ROCm GPU device, got {weight.device} "
+                           "(torchure_amd has no CPU path)")
     fp32 = _fp32_hidden_under_autocast(hidden)
     if hidden.dtype != torch.bfloat16 and not fp32:
         raise NotImplementedError(
