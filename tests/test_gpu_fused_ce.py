@@ -10,7 +10,12 @@ Checks:
   device: same GEMMs, so the loss agrees within 1e-5 relative and the grads
   within bf16 resolution;
 - the reference's own test cases (tests/fused_linear_ce.py), against an unfused
-  lm_head + F.cross_entropy at that test's bars.
+  lm_head + F.cross_entropy at that test's bars, plus the trainer's own call (fp32 hidden
+  under bf16 autocast, 4096-row chunks);
+- the grad_W hand-over (one chunk, or two in one pass) bit for bit against torch's `+=` and
+  `mul_`, and the whole chunk loop bit for bit for 1, 2, 3, 4 and 7 chunks;
+- fp32 hidden under autocast, ignore_index values inside the vocabulary, non-contiguous
+  inputs, the loss-only path and gradients for only one input.
 """
 
 from __future__ import annotations
