@@ -1692,3 +1692,55 @@ def test_launch_planned_on_one_stream_runs_on_another():
             assert torch.equal(oa.state[x][k], ob.state[y][k])
     assert norm_a.norm.view(torch.int32).item() == norm_b.norm.view(torch.int32).item()
     assert norm_a.coef.view(torch.int32).item() == norm_b.coef.view(torch.int32).item()
+
+
+def test_two_optimizers_stepped_from_two_threads():
+    """Two optimizers, each clipped and stepped three times from its own host thread on its own
+    stream (the library's shared upload buffers are then used concurrently), give the bits of
+    the same sequence run on one thread."""
+    import threading
+
+    import torchure_amd as ta
+
+    def setup(seed):
+        host = H.make_host_set([(256, 128), (777,), (64, 64)], seed=seed, grad_std=0.02)
+        return H.device_setup(host, DEV)
+
+    def run(params, opt, stream):
+        with torch.cuda.stream(stream):
+            norms = []
+            for _ in range(3):
+                norms.append(ta.clip_grad_norm(params, None, 1.0))
+                opt.step()
+            return norms
+
+    seq = [setup(50), setup(51)]
+    seq_norms = [run(p, o, torch.cuda.current_stream(DEV)) for p, _, o in seq]
+    torch.cuda.synchronize()
+
+    thr = [setup(50), setup(51)]
+    streams = [torch.cuda.Stream(device=DEV), torch.cuda.Stream(device=DEV)]
+    out, errors = [None, None], []
+
+    def worker(i):
+        try:
+            p, _, o = thr[i]
+            out[i] = run(p, o, streams[i])
+            streams[i].synchronize()
+        except Exception as e:  # reported below
+            errors.append(e)
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for (pa, wa, oa), (pb, wb, ob), na, nb in zip(seq, thr, seq_norms, out):
+        for x, y, u, v in zip(pa, pb, wa, wb):
+            assert torch.equal(x, y)
+            assert torch.equal(u.view(torch.int16), v.view(torch.int16))
+            for k in ("step", "exp_avg", "exp_avg_sq"):
+                assert torch.equal(oa.state[x][k], ob.state[y][k])
+        assert [n.view(torch.int32).item() for n in na] == [n.view(torch.int32).item() for n in nb]

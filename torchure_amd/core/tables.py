@@ -15,6 +15,7 @@ grads, so it is rebuilt per call (a few KB over PCIe, stream-ordered).
 
 from __future__ import annotations
 
+import threading
 from collections import OrderedDict
 
 import numpy as np
@@ -48,14 +49,20 @@ class TableUploader:
     reused only after the copy that last read it has completed, and copied
     asynchronously on the current stream. No per-step pinned allocation, and the
     host blocks only if it runs more than ``slots`` uploads ahead of the device.
+    Calls from several host threads are serialised, so two uploads never share a slot.
     """
 
     def __init__(self, slots: int = 4):
         self._slots: list = [None] * slots  # (pinned uint8 tensor, event or None)
         self._next = 0
         self._last = None  # (bytes, device tensor, stream handle)
+        self._lock = threading.Lock()
 
     def __call__(self, arr: np.ndarray, device: torch.device) -> torch.Tensor:
+        with self._lock:
+            return self._upload(arr, device)
+
+    def _upload(self, arr: np.ndarray, device: torch.device) -> torch.Tensor:
         raw = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
         stream = torch.cuda.current_stream(device)
         last = self._last
