@@ -503,6 +503,12 @@ def test_fp32_hidden_under_autocast(chunk):
         fused_linear_cross_entropy(hidden.clone().requires_grad_(True), weight, labels)
     with pytest.raises(NotImplementedError, match="autocast"), torch.autocast("cuda", dtype=torch.float16):
         fused_linear_cross_entropy(hidden, weight, labels)
+    # bf16 hidden under fp16 autocast: autocast would make the logits fp16, so it is refused too
+    with pytest.raises(NotImplementedError, match="autocast"), torch.autocast("cuda", dtype=torch.float16):
+        fused_linear_cross_entropy(hidden.to(torch.bfloat16).requires_grad_(True), weight, labels)
+    with pytest.raises(NotImplementedError, match="autocast"), torch.autocast("cuda", dtype=torch.float16):
+        with torch.no_grad():
+            fused_linear_cross_entropy(hidden.to(torch.bfloat16), weight, labels)
 
 
 @pytest.mark.parametrize("ignore_index", [7, 0])

@@ -76,6 +76,12 @@ def _checked(hidden, weight, labels, chunk_size):
     if weight.device.type != "cuda":  # any strides: the op works on its contiguous bf16 cast
         raise RuntimeError(f"{who}: weight must be on a ROCm GPU device, got {weight.device} "
                            "(torchure_amd has no CPU path)")
+    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") != torch.bfloat16:
+        # autocast would run the products in its dtype (the reference's GEMMs too), and the
+        # row kernel reads bf16 logits
+        raise NotImplementedError(
+            f"{who}: CUDA autocast with {torch.get_autocast_dtype('cuda')} is not supported; the "
+            "products run as bf16 GEMMs (bf16 autocast, or none)")
     fp32 = _fp32_hidden_under_autocast(hidden)
     if hidden.dtype != torch.bfloat16 and not fp32:
         raise NotImplementedError(
