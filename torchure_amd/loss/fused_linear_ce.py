@@ -11,7 +11,7 @@ Per chunk of rows:
   tm_ce_rows_bf16                   one fused kernel: logsumexp, per-row loss and
                                     grad_logits = bf16(softmax - onehot), in place
   grad_h = grad_logits @ W          bf16 GEMM
-  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_ce_grad_w into fp32
+  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_ce_grad_w(2) into fp32
 then tm_ce_loss sums the per-row losses in a fixed order (deterministic).
 
 The last chunk's bf16 grad_W is not added in forward: it waits for backward, where
@@ -41,8 +41,8 @@ until backward, and tm_ce_widen_scale writes the fp32 gradient float(gh) * grad_
 MI355X sizing: the chunk is chosen so that the bf16 logits of a chunk take up to
 ``logits_bytes`` (4 GiB by default) instead of 1024 rows: with 288 GB of HBM the
 whole Qwen3 vocabulary for 8K-16K tokens fits in one chunk, so the fp32 grad_W
-accumulation (a full read+write of V x D fp32 per chunk) runs once or twice
-instead of once per 1024 rows, and the GEMMs get large M.
+is written once, by the backward hand-over, instead of being read and written for
+every pair of 1024-row chunks, and the GEMMs get large M.
 """
 
 from __future__ import annotations
@@ -102,6 +102,14 @@ def _checked(hidden, weight, labels, chunk_size):
     return n, v, chunk, fp32
 
 
+def _bf16(logits: torch.Tensor) -> torch.Tensor:
+    """The row kernels read bf16 bits: refuse anything else loudly."""
+    if logits.dtype != torch.bfloat16 or not logits.is_contiguous():
+        raise RuntimeError(f"fused_linear_cross_entropy: the logits GEMM returned {logits.dtype} "
+                           f"(contiguous: {logits.is_contiguous()}), the row kernels need contiguous bf16")
+    return logits
+
+
 def _mean_loss(row_loss, labels, n, ignore_index, lib, stream):
     """(mean loss as a 0-d tensor, n_valid as a 1-element view) from the per-row losses."""
     out3 = torch.empty(3, dtype=torch.float32, device=row_loss.device)
@@ -123,7 +131,7 @@ def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
     row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
     for s in range(0, n, chunk):
         e = min(s + chunk, n)
-        logits = torch.matmul(hb[s:e], w.t())
+        logits = _bf16(torch.matmul(hb[s:e], w.t()))
         _native.check(lib.tm_ce_rows_loss_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
                                                int(ignore_index), row_loss[s:].data_ptr(), stream),
                       "tm_ce_rows_loss_bf16")
@@ -151,7 +159,7 @@ class _FusedLinearCE(torch.autograd.Function):
         for s in range(0, n, chunk):
             e = min(s + chunk, n)
             h = hb[s:e]
-            logits = torch.matmul(h, w.t())  # (C, V) bf16
+            logits = _bf16(torch.matmul(h, w.t()))  # (C, V) bf16
             _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
                           "tm_ce_rows_bf16")
