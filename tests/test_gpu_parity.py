@@ -1694,6 +1694,37 @@ def test_launch_planned_on_one_stream_runs_on_another():
     assert norm_a.coef.view(torch.int32).item() == norm_b.coef.view(torch.int32).item()
 
 
+def test_chunk_table_built_on_busy_stream_hit_on_another():
+    """Chunk tables first built on a side stream whose uploads still wait behind a long kernel,
+    then fetched from the cache for a clip + step on another stream: that stream waits for the
+    uploads, so the step gives the bits of the same step run on the default stream."""
+    import torchure_amd as ta
+
+    shapes = [(1234, 77), (4099,), (55, 3)]  # sizes no other test uses: the first fetch builds
+    host = H.make_host_set(shapes, seed=71, grad_std=0.02)
+    pa, wa, oa = H.device_setup(host, DEV)
+    pb, wb, ob = H.device_setup(host, DEV)
+    pc, _, oc = H.device_setup(host, DEV)
+    torch.cuda.synchronize()
+    busy, other = torch.cuda.Stream(device=DEV), torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(busy):
+        torch.cuda._sleep(100_000_000)  # a bounded spin; the table uploads queue behind it
+        ta.clip_grad_norm(pc, None, 1.0)
+        oc.step()
+    with torch.cuda.stream(other):
+        ta.clip_grad_norm(pb, None, 1.0)
+        ob.step()
+    torch.cuda.synchronize()
+    ta.clip_grad_norm(pa, None, 1.0)
+    oa.step()
+    torch.cuda.synchronize()
+    for x, y, u, v in zip(pa, pb, wa, wb):
+        assert torch.equal(x, y)
+        assert torch.equal(u.view(torch.int16), v.view(torch.int16))
+        for k in ("step", "exp_avg", "exp_avg_sq"):
+            assert torch.equal(oa.state[x][k], ob.state[y][k])
+
+
 def test_two_optimizers_stepped_from_two_threads():
     """Two optimizers, each clipped and stepped three times from its own host thread on its own
     stream (the library's shared upload buffers are then used concurrently), give the bits of

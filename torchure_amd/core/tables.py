@@ -88,6 +88,23 @@ class TableUploader:
         return dev
 
 
+def make_ready(table: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Makes a cached device table safe to read on the device's current stream.
+
+    A cached table was uploaded asynchronously on the stream current at the time
+    (``_tm_home``), and its upload is marked by ``_tm_ready``, an event recorded there
+    after the copy. On any other stream, the current stream first waits for that
+    event, so a launch there never reads a table whose copy has not run yet, and
+    record_stream keeps the caching allocator from reusing its block before that
+    stream's work has run, should the table be evicted and freed."""
+    cur = torch.cuda.current_stream(device)
+    home = getattr(table, "_tm_home", None)
+    if home is not None and cur != home:
+        cur.wait_event(table._tm_ready)
+        table.record_stream(cur)
+    return table
+
+
 class ChunkTableCache:
     """Device chunk tables keyed by (sizes, chunk_elems, device)."""
 
@@ -96,21 +113,23 @@ class ChunkTableCache:
         self._d: OrderedDict = OrderedDict()
 
     def get(self, numels, chunk_elems: int, device: torch.device):
-        """The table for these sizes (any int sequence), for a launch on the device's
-        current stream.
-
-        A cached table may be read on a stream other than the one it was allocated
-        on; record_stream keeps the caching allocator from reusing its block before
-        that stream's work has run, should the table be evicted and freed."""
+        """``(table, n_chunks)`` for these sizes (any int sequence), ready for a launch
+        on the device's current stream (``make_ready``: a hit from a stream other than
+        the one that uploaded the table waits for its upload)."""
         numels = np.ascontiguousarray(numels, dtype=np.int64)
         key = (numels.tobytes(), chunk_elems, str(device))
         hit = self._d.get(key)
         if hit is not None:
             self._d.move_to_end(key)
-            hit[0].record_stream(torch.cuda.current_stream(device))
+            make_ready(hit[0], device)
             return hit
         table = _native.fill_chunks(numels, chunk_elems)
         dev = upload(table, device) if len(table) else torch.empty(8, dtype=torch.uint8, device=device)
+        home = torch.cuda.current_stream(device)
+        ready = torch.cuda.Event()
+        ready.record(home)
+        dev._tm_home = home
+        dev._tm_ready = ready
         val = (dev, len(table))
         self._d[key] = val
         if len(self._d) > self._cap:

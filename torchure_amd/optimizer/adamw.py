@@ -407,7 +407,7 @@ class AdamW(torch.optim.Optimizer):
         rows = plan.rows.copy()
         rows["grad"] = host.ptrs(gl)
         rows["flags"] = flags
-        plan.chunks.record_stream(torch.cuda.current_stream(device))
+        tables.make_ready(plan.chunks, device)
         return [StepLaunch(device, self._uploader(rows, device), plan.n, plan.chunks, plan.n_chunks,
                            self.chunk_elems, _native.hyper_array(hyper), len(hyper), coef,
                            plan.written, plan.wents)]
