@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -42,18 +43,35 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="qwen3-4b")
     ap.add_argument("--chunk-elems", type=int, default=None)
-    ap.add_argument("--cpu-sample-blocks", type=int, default=2,
-                    help="transformer blocks of the config timed for the CPU baseline (0 = skip)")
-    ap.add_argument("--cpu-steps", type=int, default=3, help="at least this many timed CPU steps")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="keep timing CPU steps until this much CPU work has been timed (at most 500 steps)")
-    ap.add_argument("--also", default="qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,qwen3-4b-dropin,"
-                                      "qwen3-4b-ddpbuckets,ragged",
-                    help="comma list of extra configs reported under 'extra' (empty = none)")
+    ap.add_argument("--alloc-conf", default="expandable_segments:True",
+                    help="PYTORCH_CUDA_ALLOC_CONF for the run, set before torch starts; the default is "
+                         "the reference trainer's own setting (torchure/train/trainer.py:39); '' keeps "
+                         "the environment's")
+    ap.add_argument("--cpu-configs", default="qwen3-4b,qwen3-0.6b,qwen3-0.6b-ref",
+                    help="full parameter sets timed for the CPU baseline; the first is the headline "
+                         "(empty = skip)")
+    ap.add_argument("--cpu-steps", type=int, default=3, help="at least this many timed CPU steps per set")
+    ap.add_argument("--cpu-seconds", type=float, default=4.0,
+                    help="keep timing CPU steps of a set until this much CPU work has been timed "
+                         "(at most 100 steps)")
+    ap.add_argument("--also", default="qwen3-4b-noexpand,qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,"
+                                      "qwen3-4b-dropin,qwen3-4b-ddpbuckets,ragged",
+                    help="comma list of extra configs reported under 'extra' (empty = none); "
+                         "'<config>-noexpand' runs that config with expandable segments off")
     ap.add_argument("--mode", choices=("bench", "kernels", "ce"), default="bench",
-                    help="kernels: only the norm and update launches, --reps times each, plus a "
-                         "2 GiB device copy for calibrating HBM byte counters (for rocprofv3 --pmc)")
+                    help="kernels: only the norm and update launches (for an -fp32acc config, the "
+                         "accumulation launches), --reps times each, plus a 2 GiB device copy for "
+                         "calibrating HBM byte counters (for rocprofv3 --pmc)")
     ap.add_argument("--reps", type=int, default=3)
+    ap.add_argument("--states", type=int, default=1,
+                    help="kernels mode: build this many copies of the state, each its own set of "
+                         "allocations held at once, and launch the norm and update on each in turn "
+                         "(placement in HBM differs between them)")
+    ap.add_argument("--state-layouts", default="",
+                    help="kernels mode: comma list of state layouts built in this order and held at "
+                         "once: 'sep' (every tensor its own allocation), 'pool' (one allocation per "
+                         "role, tensors are views), 'mv' (separate masters and grads, exp_avg and "
+                         "exp_avg_sq pooled); overrides --states")
     ap.add_argument("--fused-ce", type=int, default=1,
                     help="also time the chunked fused linear + CE on the Qwen3-0.6B head (1 = yes)")
     ap.add_argument("--torch-reference", type=int, default=1,
@@ -62,34 +80,89 @@ def parse():
     return ap.parse_args()
 
 
-def run_kernels_only(config: str, reps: int, chunk_elems, dev):
+def run_kernels_only(config: str, reps: int, chunk_elems, dev, states: int = 1, layouts=()):
     """Launch sequence profiled by rocprofv3 --pmc: `reps` x (norm, update), then a
-    plain copy of 2 GiB (512 Mi fp32) whose FETCH_SIZE/WRITE_SIZE calibrate the counters."""
+    plain copy of 2 GiB (512 Mi fp32) whose FETCH_SIZE/WRITE_SIZE calibrate the counters.
+    For an ``-fp32acc`` config: `reps` x a middle micro-step's accumulation
+    (accumulate_list_kernel), then `reps` x the last micro-step's (accumulate_list_norm_kernel).
+    The state is built from a few pooled buffers (every tensor a view), so setting it up
+    takes a handful of device dispatches however many tensors the config has."""
     import torch
 
     from torchure_amd.core.grad_helper import NormLaunch
 
-    params, work, opt, n_params = build_state(config, chunk_elems, dev)
-    norm_l = NormLaunch([w.grad for w in work], 1.0)
-    norm_l()
-    upd = opt.plan_step(norm_l.coef, {id(p) for p in params})
-    for _ in range(reps):
+    acc_cfg = config.endswith("-fp32acc")
+    base = config[: -len("-fp32acc")] if acc_cfg else config
+    if (states > 1 or layouts) and not acc_cfg:
+        layouts = list(layouts) or ["pool"] * states
+        sets = [build_state(base, chunk_elems, dev, pooled=(lay == "pool"), pooled_state=(lay == "mv"))
+                for lay in layouts]
+        times = []
+        for params, work, opt, n_params in sets:
+            norm_l = NormLaunch([w.grad for w in work], 1.0)
+            norm_l()
+            upd = opt.plan_step(norm_l.coef, {id(p) for p in params})
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            for _ in range(reps):
+                norm_l()
+                a.record()
+                upd[0]()
+                b.record()
+            torch.cuda.synchronize()
+            times.append(round(a.elapsed_time(b), 3))
+            del upd, norm_l
+        print(json.dumps({"mode": "kernels", "config": config, "layouts": layouts,
+                          "last_update_ms_per_state": times}), flush=True)
+        del sets, params, work, opt
+        torch.cuda.empty_cache()
+        return
+    params, work, opt, n_params = build_state(base, chunk_elems, dev, pooled=True)
+    if acc_cfg:
+        from torchure_amd.optimizer.working import accumulate_grads_
+
+        micro = [w.grad for w in work]
+        accumulate_grads_(params)  # first micro-step: assigns the fp32 accumulators
+        for _ in range(reps):
+            for w, m in zip(work, micro):
+                w.grad = m
+            accumulate_grads_(params)
+        for _ in range(reps):
+            for w, m in zip(work, micro):
+                w.grad = m
+            accumulate_grads_(params, last=True)
+        torch.cuda.synchronize()
+        del micro
+    else:
+        norm_l = NormLaunch([w.grad for w in work], 1.0)
         norm_l()
-        upd[0]()
-    torch.cuda.synchronize()
-    del params, work, opt, upd
+        upd = opt.plan_step(norm_l.coef, {id(p) for p in params})
+        for _ in range(reps):
+            norm_l()
+            upd[0]()
+        torch.cuda.synchronize()
+        del upd, norm_l
+    del params, work, opt
     torch.cuda.empty_cache()
     a = torch.ones(512 * 1024 * 1024, dtype=torch.float32, device=dev)
     b = torch.empty_like(a)
     b.copy_(a)
     torch.cuda.synchronize()
-    print(json.dumps({"mode": "kernels", "config": config, "params": n_params, "reps": reps,
-                      "update_algorithmic_bytes": n_params * UPDATE_BYTES_PER_PARAM,
-                      "norm_algorithmic_bytes": n_params * NORM_BYTES_PER_PARAM,
-                      "copy_bytes_each_way": a.numel() * 4}), flush=True)
+    out = {"mode": "kernels", "config": config, "params": n_params, "reps": reps,
+           "copy_bytes_each_way": a.numel() * 4}
+    if acc_cfg:
+        out["accumulate_algorithmic_bytes"] = n_params * 10  # read bf16 2 + fp32 4, write fp32 4
+    else:
+        out["update_algorithmic_bytes"] = n_params * UPDATE_BYTES_PER_PARAM
+        out["norm_algorithmic_bytes"] = n_params * NORM_BYTES_PER_PARAM
+    print(json.dumps(out), flush=True)
 
 
-def build_state(config: str, chunk_elems, dev):
+def build_state(config: str, chunk_elems, dev, pooled: bool = False, pooled_state: bool = False):
+    """The steady-state inputs, allocated in the trainer's order: the fp32 masters (the
+    model), their bf16 working copies, the grads (backward), then the optimizer state (the
+    first step). Every tensor is its own allocation; with ``pooled`` each role is one
+    buffer filled by one random draw and the tensors are views of it; with
+    ``pooled_state`` only exp_avg and exp_avg_sq are."""
     import torch
 
     import torchure_amd as ta
@@ -98,18 +171,45 @@ def build_state(config: str, chunk_elems, dev):
 
     shapes = shapes_for(config)
     g = torch.Generator(device=dev).manual_seed(1234)
-    params = [torch.nn.Parameter(torch.randn(s, device=dev, generator=g) * 0.02) for s in shapes]
-    work = ta.attach_bf16_working_params(params)
-    for w in work:
-        w.grad = (torch.randn(w.shape, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    sizes = [math.prod(s) for s in shapes]
+    offs = [0]
+    for k in sizes:
+        offs.append(offs[-1] + (k + 63) // 64 * 64)  # 256-byte aligned views
+
+    def pool(scale, dtype=torch.float32, absval=False):
+        flat = torch.randn(offs[-1], device=dev, generator=g).mul_(scale)
+        if absval:
+            flat.abs_()
+        flat = flat.to(dtype)
+        return [flat[o: o + k].view(s) for o, k, s in zip(offs, sizes, shapes)]
+
+    if pooled:
+        params = [torch.nn.Parameter(t) for t in pool(0.02)]
+        work = ta.attach_bf16_working_params(params)
+        for w, t in zip(work, pool(1e-3, torch.bfloat16)):
+            w.grad = t
+    else:
+        params = [torch.nn.Parameter(torch.randn(s, device=dev, generator=g) * 0.02) for s in shapes]
+        work = ta.attach_bf16_working_params(params)
+        for w in work:
+            w.grad = (torch.randn(w.shape, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
     opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
                              {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True,
                               "chunk_elems": chunk_elems or tables.DEFAULT_CHUNK_ELEMS})
-    for p in params:
+    ms = pool(1e-4) if pooled or pooled_state else None
+    vs = pool(1e-8, absval=True) if pooled or pooled_state else None
+    steps = torch.full((len(params),), 1000.0, dtype=torch.float32, device=dev) if pooled else None
+    for i, p in enumerate(params):
         st = opt.state[p]
-        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=dev)
-        st["exp_avg"] = torch.randn(p.shape, device=dev, generator=g) * 1e-4
-        st["exp_avg_sq"] = torch.randn(p.shape, device=dev, generator=g).abs_() * 1e-8
+        if pooled:
+            st["step"], st["exp_avg"], st["exp_avg_sq"] = steps[i], ms[i], vs[i]
+        elif pooled_state:
+            st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=dev)
+            st["exp_avg"], st["exp_avg_sq"] = ms[i], vs[i]
+        else:
+            st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=dev)
+            st["exp_avg"] = torch.randn(p.shape, device=dev, generator=g) * 1e-4
+            st["exp_avg_sq"] = torch.randn(p.shape, device=dev, generator=g).abs_() * 1e-8
     torch.cuda.synchronize()
     n_params = sum(p.numel() for p in params)
     return params, work, opt, n_params
@@ -514,50 +614,126 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
     return out
 
 
-def run_cpu_baseline(config: str, blocks: int, steps: int, seconds: float = 10.0):
-    """Reference composition on torch CPU over the first ``blocks`` transformer
-    blocks of ``config`` (the sample), bf16 grads widened to fp32: at least ``steps``
-    timed steps, and more until ``seconds`` of CPU work have been timed; the median
-    step is reported."""
+def _cpu_topology():
+    """(logical CPUs this process may run on, physical cores among them or None)."""
+    try:
+        cpus = set(os.sched_getaffinity(0))
+    except AttributeError:
+        cpus = set(range(os.cpu_count() or 1))
+    cores, cur = set(), {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in list(f) + [""]:
+                if line.strip():
+                    k, _, v = line.partition(":")
+                    cur[k.strip()] = v.strip()
+                    continue
+                if cur.get("processor", "").isdigit() and int(cur["processor"]) in cpus:
+                    cores.add((cur.get("physical id"), cur.get("core id")))
+                cur = {}
+    except OSError:
+        pass
+    return len(cpus), (len(cores) if cores and (None, None) not in cores else None)
+
+
+def _cpu_one(config: str, steps: int, seconds: float, threads: int):
+    """The reference composition on torch CPU over the whole parameter set of ``config``:
+    fp32 masters and grads (bf16-valued), two param groups, steady state at step 1000.
+    Values are drawn once into small pools and tiled into the tensors (the step's time does
+    not depend on them), so a 4B set is set up in seconds. At least ``steps`` timed steps,
+    more until ``seconds`` of CPU work has been timed; the median step is reported."""
     import torch
 
     from oracle.torch_composition import make_reference_optimizer, reference_step
     from torchure_amd.workloads import shapes_for
 
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    shapes = shapes_for(config)
-    sample = shapes[1:1 + 11 * blocks]
     g = torch.Generator().manual_seed(99)
-    params = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in sample]
+    pools = {k: torch.randn(1 << 22, generator=g) * sc for k, sc in
+             (("p", 0.02), ("g", 1e-3), ("m", 1e-4), ("v", 1e-8))}
+    pools["g"] = pools["g"].to(torch.bfloat16).float()
+    pools["v"].abs_()
+
+    def filled(shape, key):
+        t = torch.empty(shape)
+        flat, src = t.view(-1), pools[key]
+        k = flat.numel() // src.numel()
+        if k:  # one multithreaded copy of the pool, tiled
+            flat[: k * src.numel()].view(k, -1).copy_(src.expand(k, -1))
+        rest = flat.numel() - k * src.numel()
+        if rest:
+            flat[k * src.numel():].copy_(src[:rest])
+        return t
+
+    shapes = shapes_for(config)
+    params = [torch.nn.Parameter(filled(s, "p")) for s in shapes]
     for p in params:
-        p.grad = (torch.randn(p.shape, generator=g) * 1e-3).to(torch.bfloat16).float()
+        p.grad = filled(p.shape, "g")
     opt = make_reference_optimizer(params)
     for p in params:
         st = opt.state[p]
         st["step"] = torch.tensor(1000.0)
-        st["exp_avg"] = torch.randn(p.shape, generator=g) * 1e-4
-        st["exp_avg_sq"] = torch.randn(p.shape, generator=g).abs_() * 1e-8
+        st["exp_avg"] = filled(p.shape, "m")
+        st["exp_avg_sq"] = filled(p.shape, "v")
     bf16 = [torch.empty(p.shape, dtype=torch.bfloat16) for p in params]
     n = sum(p.numel() for p in params)
     reference_step(params, opt, 1.0, bf16)  # warm-up
     times = []
-    while len(times) < steps or (sum(times) < seconds and len(times) < 500):
+    while len(times) < steps or (sum(times) < seconds and len(times) < 100):
         t0 = time.perf_counter()
         reference_step(params, opt, 1.0, bf16)
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
+    del params, opt, bf16
+    return dict(config=config, n_params=n, tensors=len(shapes), ms_per_step=round(med * 1e3, 1),
+                GBps=round(n * STEP_BYTES_PER_PARAM / med / 1e9, 3), timed_steps=len(times),
+                timed_s=round(sum(times), 1))
+
+
+def run_cpu_baseline(configs: list[str], steps: int, seconds: float):
+    """The reference's torch calls composed as its clip + optimizer step + bf16 cast
+    (torchure/core/grad_helper.py:17-33, torchure/optimizer/builder.py:31-46,
+    torchure/train/trainer.py:374; oracle/torch_composition.py), on torch CPU with one
+    thread per logical CPU this process may use, over the whole parameter set of each
+    config. The first config is the headline; the others are reported under ``configs``."""
+    import torch
+
+    logical, physical = _cpu_topology()
+    torch.set_num_threads(logical)
+    runs = [_cpu_one(c, steps, seconds, logical) for c in configs]
+    head = runs[0]
     return dict(
-        value=round(n * STEP_BYTES_PER_PARAM / med / 1e9, 3),
+        value=head["GBps"],
         unit="GB/s",
-        cores=threads,
-        kind="port",
-        sample=(f"{config} blocks 0..{blocks - 1} ({len(params)} tensors, {n} params), median of "
-                f"{len(times)} steps ({sum(times):.1f} s of timed CPU work) after 1 warm-up, "
-                f"{med * 1e3:.1f} ms/step; torch CPU foreach-norm clip + "
-                f"AdamW(fused=True) + bf16 cast; GB/s on the same 30 B/param basis; "
-                f"{threads} threads of {os.cpu_count()} logical CPUs, host RAM {_host_ram_gib()} GiB"),
+        cores=logical,
+        kind="reference",
+        kind_note="the reference's own torch calls (foreach-norm clip, torch.optim.AdamW(fused=True) "
+                  "with its two groups, bf16 cast) composed in oracle/torch_composition.py and run "
+                  "on torch CPU; no code of this build runs in it",
+        ms_per_step=head["ms_per_step"],
+        logical_cpus=logical,
+        physical_cores=physical,
+        host_ram_gib=_host_ram_gib(),
+        sample=(f"{head['config']}: the whole parameter set ({head['tensors']} tensors, "
+                f"{head['n_params']} params), median of {head['timed_steps']} steps "
+                f"({head['timed_s']} s timed) after 1 warm-up, {head['ms_per_step']} ms/step; "
+                f"GB/s on the same 30 B/param basis; {logical} threads on {logical} logical CPUs "
+                f"({physical} physical cores), host RAM {_host_ram_gib()} GiB"),
+        configs={r["config"]: r for r in runs[1:]},
     )
+
+
+def _set_expandable(on: bool) -> bool:
+    """Switches torch's expandable segments for the allocations that follow (cached blocks
+    are released first, so the next leg maps fresh memory); returns the previous setting."""
+    import torch
+
+    prev = "expandable_segments:true" in os.environ.get("PYTORCH_CUDA_ALLOC_CONF", "").replace(" ", "").lower()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    setter = getattr(torch._C, "_accelerator_setAllocatorSettings", None) or torch.cuda.memory._set_allocator_settings
+    setter(f"expandable_segments:{'True' if on else 'False'}")
+    os.environ["PYTORCH_CUDA_ALLOC_CONF"] = f"expandable_segments:{'True' if on else 'False'}"
+    return prev
 
 
 def _host_ram_gib() -> str:
@@ -582,6 +758,8 @@ def load_traffic(config: str):
 
 def main():
     args = parse()
+    if args.alloc_conf:  # read by torch's allocator when it starts, so set before any import
+        os.environ["PYTORCH_CUDA_ALLOC_CONF"] = args.alloc_conf
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
               "optimizer step has no cross-GPU path here", file=sys.stderr)
@@ -596,7 +774,8 @@ def main():
 
     torchure_amd._native.lib()
     if args.mode == "kernels":
-        run_kernels_only(args.config, args.reps, args.chunk_elems, dev)
+        run_kernels_only(args.config, args.reps, args.chunk_elems, dev, args.states,
+                         [x for x in args.state_layouts.split(",") if x])
         return
     if args.mode == "ce":  # fused linear CE only (for rocprofv3)
         print(json.dumps(run_fused_ce(args.reps, dev, with_reference=False)), flush=True)
@@ -606,6 +785,18 @@ def main():
     print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
     extra = {}
     for cfg in [c for c in args.also.split(",") if c and c != args.config]:
+        if cfg.endswith("-noexpand"):
+            base_cfg = cfg[: -len("-noexpand")]
+            prev = _set_expandable(False)
+            r = run_gpu(base_cfg, args.steps, args.warmup, args.chunk_elems, dev)
+            _set_expandable(prev)
+            r["GBps"] = round(r["n_params"] * STEP_BYTES_PER_PARAM / (r["ms_per_step"] * 1e-3) / 1e9, 1)
+            r["frac_of_peak"] = round(r["GBps"] / PEAK_HBM_GBS, 4)
+            r["update_GBps"] = round(r["n_params"] * UPDATE_BYTES_PER_PARAM / (r["update_ms_mean"] * 1e-3) / 1e9, 1)
+            r["alloc_conf"] = "expandable_segments:False"
+            extra[cfg] = r
+            print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
+            continue
         if cfg.endswith("-dropin") or cfg.endswith("-ddpbuckets"):
             bucketed = cfg.endswith("-ddpbuckets")
             base_cfg = cfg.rsplit("-", 1)[0]
@@ -645,8 +836,12 @@ def main():
     value = n * STEP_BYTES_PER_PARAM / (ms * 1e-3) / 1e9
     upd_gbs = n * UPDATE_BYTES_PER_PARAM / (main_res["update_ms_mean"] * 1e-3) / 1e9
     cpu = None
-    if args.cpu_sample_blocks > 0:
-        cpu = run_cpu_baseline(args.config, args.cpu_sample_blocks, args.cpu_steps, args.cpu_seconds)
+    cpu_cfgs = [c for c in args.cpu_configs.split(",") if c]
+    if cpu_cfgs:
+        if cpu_cfgs[0] != args.config:
+            cpu_cfgs = [args.config] + [c for c in cpu_cfgs if c != args.config]
+        torch.cuda.empty_cache()
+        cpu = run_cpu_baseline(cpu_cfgs, args.cpu_steps, args.cpu_seconds)
     line = {
         "metric": "optimizer step ms + achieved HBM GB/s (% of peak), Qwen3-0.6B & 4B shapes",
         "value": round(value, 1),
@@ -662,7 +857,7 @@ def main():
         "data": "synthetic (seeded steady-state optimizer inputs; no dataset)",
         "config": {"workload": f"{args.config} optimizer step: clip 1.0 + AdamW + bf16 refresh",
                    "params": n, "tensors": main_res["n_tensors"], "bytes_per_param": STEP_BYTES_PER_PARAM,
-                   "grad_dtype": "bf16"},
+                   "grad_dtype": "bf16", "alloc_conf": args.alloc_conf or os.environ.get("PYTORCH_CUDA_ALLOC_CONF", "")},
         "frac_of_peak": round(value / PEAK_HBM_GBS, 4),
         "params_per_s": round(n / (ms * 1e-3), 1),
         "roofline": {

@@ -85,8 +85,10 @@ typedef struct tm_tensor {
 } tm_tensor_t;
 
 /* One work item: elements [chunk*chunk_elems, min((chunk+1)*chunk_elems, numel))
- * of tensor `tensor`. A call takes at most 16,777,215 chunks (one 256-thread workgroup
- * each; a launch holds fewer than 2^32 work-items); larger tables return TM_EINVAL. */
+ * of tensor `tensor`. A call takes at most 4,294,967,295 chunks (32-bit indices); larger
+ * tables return TM_EINVAL. The streaming kernels cover a chunk with chunk_elems / 256
+ * one-wave workgroups and split a table over as many launches as the 2^32 work-item
+ * limit of a launch requires. */
 typedef struct tm_chunk {
   uint32_t tensor;
   uint32_t chunk;
@@ -200,6 +202,15 @@ int tm_clip_coef(const float* d_norm, float max_norm, float* d_coef, void* strea
 /* Writes RNE(src) into dst (bf16 working-copy refresh without an update).
  * Rounding rule of torch/headeronly/util/BFloat16.h:100-114 (NaN -> 0x7FC0). */
 int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* stream);
+
+/*
+ * The same cast over a list, one launch: param_bf16 = RNE(master) for every record whose
+ * param_bf16 is non-zero (only master, param_bf16 and numel are read). Replaces the per-weight
+ * cast autocast performs at every forward (torchure/train/trainer.py:374) for the whole list;
+ * used to create and to refresh the bf16 working copies.
+ */
+int tm_cast_bf16_list(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                      int64_t n_chunks, int64_t chunk_elems, void* stream);
 
 /* ---- chunked fused linear + cross-entropy (torchure/loss/fused_linear_ce.py) ---- */
 

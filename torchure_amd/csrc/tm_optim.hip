@@ -676,25 +676,44 @@ __global__ __launch_bounds__(kWave) void accumulate_kernel(float* __restrict__ a
   slice_apply(AccumBf16{acc, micro}, start, end, vec);
 }
 
+// dst (bf16) = RNE(src (fp32)).
+struct CastBf16 {
+  uint16_t* dst;
+  const float* src;
+  __device__ __forceinline__ void group(int64_t e) const {
+    const f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(src + e));
+    u32x2 o;
+    o.x = bf16_rne(a.x) | (bf16_rne(a.y) << 16);
+    o.y = bf16_rne(a.z) | (bf16_rne(a.w) << 16);
+    st<true>(reinterpret_cast<u32x2*>(dst + e), o);
+  }
+  __device__ __forceinline__ void one(int64_t i) const { dst[i] = static_cast<uint16_t>(bf16_rne(src[i])); }
+};
+
 __global__ __launch_bounds__(kWave) void cast_bf16_kernel(uint16_t* __restrict__ dst,
                                                           const float* __restrict__ src, int64_t n,
                                                           int64_t first) {
   const int64_t start = (first + blockIdx.x) * kSlice;
   const int64_t end = min(start + kSlice, n);
   const bool vec = aligned8(reinterpret_cast<uint64_t>(dst)) && aligned16(reinterpret_cast<uint64_t>(src));
-  int64_t vend = start;
-  if (vec) {
-    vend = start + ((end - start) & ~int64_t(3));
-    const int64_t e = start + static_cast<int64_t>(threadIdx.x) * 4;
-    if (e < vend) {
-      const f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(src + e));
-      u32x2 o;
-      o.x = bf16_rne(a.x) | (bf16_rne(a.y) << 16);
-      o.y = bf16_rne(a.z) | (bf16_rne(a.w) << 16);
-      st<true>(reinterpret_cast<u32x2*>(dst + e), o);
-    }
-  }
-  for (int64_t i = vend + threadIdx.x; i < end; i += kWave) dst[i] = static_cast<uint16_t>(bf16_rne(src[i]));
+  slice_apply(CastBf16{dst, src}, start, end, vec);
+}
+
+// The same cast over a list of tensors (param_bf16 = RNE(master) of each record that has a
+// working copy), one slice per wave.
+__global__ __launch_bounds__(kWave) void cast_bf16_list_kernel(
+    const tm_tensor_t* __restrict__ tensors, int64_t n_tensors, const tm_chunk_t* __restrict__ chunks,
+    uint32_t first_chunk, uint32_t slices_per_chunk, int64_t chunk_elems) {
+  tm_chunk_t ck;
+  int64_t start;
+  slice_of(chunks, first_chunk, slices_per_chunk, chunk_elems, ck, start);
+  if (ck.tensor >= n_tensors) return;
+  const tm_tensor_t d = tensors[ck.tensor];
+  if (start >= d.numel || !d.param_bf16) return;
+  const int64_t end = min(start + kSlice, d.numel);
+  const bool vec = aligned8(d.param_bf16) && aligned16(d.master);
+  slice_apply(CastBf16{reinterpret_cast<uint16_t*>(d.param_bf16), reinterpret_cast<const float*>(d.master)},
+              start, end, vec);
 }
 
 // Launches kernel(first, blocks) over `n_slices` one-wave slices in as many launches as the
@@ -894,6 +913,18 @@ int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* strea
   return launch_slices((numel + kSlice - 1) / kSlice, "cast_bf16_kernel", [&](int64_t first, dim3 grid) {
     hipLaunchKernelGGL(cast_bf16_kernel, grid, dim3(kWave), 0, s, d_dst, d_src, numel, first);
   });
+}
+
+int tm_cast_bf16_list(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                      int64_t n_chunks, int64_t chunk_elems, void* stream) {
+  int rc = check_table(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, "tm_cast_bf16_list");
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return launch_chunk_slices(n_chunks, chunk_elems, "cast_bf16_list_kernel",
+                             [&](uint32_t first, uint32_t spc, dim3 grid) {
+                               hipLaunchKernelGGL(cast_bf16_list_kernel, grid, dim3(kWave), 0, s, d_tensors,
+                                                  n_tensors, d_chunks, first, spc, chunk_elems);
+                             });
 }
 
 }  // extern "C"

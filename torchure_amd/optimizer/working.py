@@ -41,17 +41,32 @@ def attach_bf16_working_params(params) -> list[torch.Tensor]:
         offsets.append(total)
         total += (p.numel() + _ALIGN_ELEMS - 1) // _ALIGN_ELEMS * _ALIGN_ELEMS
     flat = torch.empty(max(total, 1), dtype=torch.bfloat16, device=device)
+    views = [flat[off : off + p.numel()].view(p.shape) for p, off in zip(params, offsets)]
+    _cast_list(params, views, device)
     out = []
-    lib = _native.lib()
-    stream = _native.stream_handle(device)
-    for p, off in zip(params, offsets):
-        w = flat[off : off + p.numel()].view(p.shape)
-        _native.check(lib.tm_cast_bf16(w.data_ptr(), p.data_ptr(), p.numel(), stream), "tm_cast_bf16")
+    for p, w in zip(params, views):
         w = w.detach().requires_grad_(p.requires_grad)
         p._tm_working = w
         mark_current(p, w)
         out.append(w)
     return out
+
+
+_CAST_UPLOAD = tables.TableUploader()
+
+
+def _cast_list(masters, copies, device) -> None:
+    """copies[i] = RNE(masters[i]) for the whole list in one launch (tm_cast_bf16_list)."""
+    rows = np.zeros(len(masters), dtype=_native.TENSOR_DTYPE)
+    rows["master"] = _native.host().ptrs(masters)
+    rows["param_bf16"] = _native.host().ptrs(copies)
+    rows["numel"] = np.fromiter((m.numel() for m in masters), dtype=np.int64, count=len(masters))
+    chunk_elems = tables.DEFAULT_CHUNK_ELEMS
+    chunks, n_chunks = tables.CHUNKS.get(rows["numel"], chunk_elems, device)
+    d_rows = _CAST_UPLOAD(rows, device)
+    rc = _native.lib().tm_cast_bf16_list(d_rows.data_ptr(), len(masters), chunks.data_ptr(), n_chunks,
+                                         chunk_elems, _native.stream_handle(device))
+    _native.check(rc, "tm_cast_bf16_list")
 
 
 def mark_current(p: torch.Tensor, w: torch.Tensor) -> None:
@@ -71,16 +86,18 @@ def refresh_bf16_working_params(params) -> None:
     ``model.load_state_dict(...)`` on a resume (torchure/train/trainer.py:340-350), so
     that the next bf16 forward does not run on stale weights. ``AdamW.step()`` raises
     if it finds a master modified since its copy was last written."""
-    lib = _native.lib()
+    per_dev: dict = {}
     for p in params:
         w = getattr(p, "_tm_working", None)
         if w is None:
             continue
         tables.require_device_tensor(p, "refresh_bf16_working_params", "param")
-        _native.check(lib.tm_cast_bf16(w.data_ptr(), p.data_ptr(), p.numel(),
-                                       _native.stream_handle(p.device)), "tm_cast_bf16")
-        torch.autograd.graph.increment_version(w)
-        mark_current(p, w)
+        per_dev.setdefault(p.device, []).append((p, w))
+    for device, pairs in per_dev.items():  # one launch per device
+        _cast_list([p for p, _ in pairs], [w for _, w in pairs], device)
+        for p, w in pairs:
+            torch.autograd.graph.increment_version(w)
+            mark_current(p, w)
 
 
 def accumulate_grad_(acc: torch.Tensor, micro: torch.Tensor) -> None:
