@@ -54,10 +54,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=4.0,
                     help="keep timing CPU steps of a set until this much CPU work has been timed "
                          "(at most 100 steps)")
-    ap.add_argument("--also", default="qwen3-4b-noexpand,qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,"
+    ap.add_argument("--also", default="qwen3-4b-again,qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,"
                                       "qwen3-4b-dropin,qwen3-4b-ddpbuckets,ragged",
                     help="comma list of extra configs reported under 'extra' (empty = none); "
-                         "'<config>-noexpand' runs that config with expandable segments off")
+                         "'<config>-again' runs that config once more, on fresh allocations made "
+                         "after the earlier legs' memory was released")
     ap.add_argument("--mode", choices=("bench", "kernels", "ce"), default="bench",
                     help="kernels: only the norm and update launches (for an -fp32acc config, the "
                          "accumulation launches), --reps times each, plus a 2 GiB device copy for "
@@ -536,19 +537,20 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
         torch.cuda.synchronize()
         return (time.perf_counter() - t0) * 1e3 / reps
 
-    def ours():
+    def ours(chunk="auto"):  # "auto": MI355X sizing, the whole 8192-token call in one chunk
         h = hidden.detach().requires_grad_(True)
         w = weight.detach().requires_grad_(True)
-        fused_linear_cross_entropy(h, w, labels).backward()
+        fused_linear_cross_entropy(h, w, labels, -100, chunk).backward()
 
-    out = {"workload": "qwen3-0.6b lm_head: N 8192, D 1024, V 151936, fwd+bwd",
+    out = {"workload": "qwen3-0.6b lm_head: N 8192, D 1024, V 151936, fwd+bwd, chunk_size='auto'",
            "flops": flops, "ms": round(timed(ours), 4)}
     out["TFLOPs"] = round(flops / (out["ms"] * 1e-3) / 1e12, 1)
     out["frac_of_bf16_mfma_peak"] = round(out["TFLOPs"] / 2500.0, 4)
+    out["default_chunk1024_ms"] = round(timed(lambda: ours(1024)), 4)
 
     def evaluate():  # no input needs a gradient: the logits GEMM and the row losses only
         with torch.no_grad():
-            fused_linear_cross_entropy(hidden, weight, labels)
+            fused_linear_cross_entropy(hidden, weight, labels, -100, "auto")
 
     out["loss_only_ms"] = round(timed(evaluate), 4)
     out["loss_only_TFLOPs"] = round(2.0 * n * d * v / (out["loss_only_ms"] * 1e-3) / 1e12, 1)
@@ -603,6 +605,8 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
         try:
             out["reference_compiled_ms"] = round(timed(ref), 4)
             out["speedup_vs_reference_compiled"] = round(out["reference_compiled_ms"] / out["ms"], 3)
+            out["speedup_vs_reference_compiled_both_chunk1024"] = round(
+                out["reference_compiled_ms"] / out["default_chunk1024_ms"], 3)
             out["reference_compiled_fp32_hidden_autocast_chunk4096_ms"] = round(timed(ref_fp32_hidden), 4)
             out["speedup_fp32_hidden_autocast_chunk4096"] = round(
                 out["reference_compiled_fp32_hidden_autocast_chunk4096_ms"] / out["fp32_hidden_autocast_chunk4096_ms"], 3)
@@ -722,20 +726,6 @@ def run_cpu_baseline(configs: list[str], steps: int, seconds: float):
     )
 
 
-def _set_expandable(on: bool) -> bool:
-    """Switches torch's expandable segments for the allocations that follow (cached blocks
-    are released first, so the next leg maps fresh memory); returns the previous setting."""
-    import torch
-
-    prev = "expandable_segments:true" in os.environ.get("PYTORCH_CUDA_ALLOC_CONF", "").replace(" ", "").lower()
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-    setter = getattr(torch._C, "_accelerator_setAllocatorSettings", None) or torch.cuda.memory._set_allocator_settings
-    setter(f"expandable_segments:{'True' if on else 'False'}")
-    os.environ["PYTORCH_CUDA_ALLOC_CONF"] = f"expandable_segments:{'True' if on else 'False'}"
-    return prev
-
-
 def _host_ram_gib() -> str:
     """Total host memory from /proc/meminfo, or '?' where it cannot be read."""
     try:
@@ -770,6 +760,12 @@ def main():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    import warnings
+
+    with warnings.catch_warnings(record=True) as caught:  # the allocator reads its settings here
+        warnings.simplefilter("always")
+        torch.empty(1, device=dev)
+    ignored = [str(w.message) for w in caught if "not supported" in str(w.message)]
     import torchure_amd
 
     torchure_amd._native.lib()
@@ -785,15 +781,12 @@ def main():
     print(f"[bench] {args.config}: {main_res}", file=sys.stderr, flush=True)
     extra = {}
     for cfg in [c for c in args.also.split(",") if c and c != args.config]:
-        if cfg.endswith("-noexpand"):
-            base_cfg = cfg[: -len("-noexpand")]
-            prev = _set_expandable(False)
-            r = run_gpu(base_cfg, args.steps, args.warmup, args.chunk_elems, dev)
-            _set_expandable(prev)
+        if cfg.endswith("-again"):
+            r = run_gpu(cfg[: -len("-again")], args.steps, args.warmup, args.chunk_elems, dev)
             r["GBps"] = round(r["n_params"] * STEP_BYTES_PER_PARAM / (r["ms_per_step"] * 1e-3) / 1e9, 1)
             r["frac_of_peak"] = round(r["GBps"] / PEAK_HBM_GBS, 4)
             r["update_GBps"] = round(r["n_params"] * UPDATE_BYTES_PER_PARAM / (r["update_ms_mean"] * 1e-3) / 1e9, 1)
-            r["alloc_conf"] = "expandable_segments:False"
+            r["update_frac_of_peak"] = round(r["update_GBps"] / PEAK_HBM_GBS, 4)
             extra[cfg] = r
             print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
             continue
@@ -857,7 +850,8 @@ def main():
         "data": "synthetic (seeded steady-state optimizer inputs; no dataset)",
         "config": {"workload": f"{args.config} optimizer step: clip 1.0 + AdamW + bf16 refresh",
                    "params": n, "tensors": main_res["n_tensors"], "bytes_per_param": STEP_BYTES_PER_PARAM,
-                   "grad_dtype": "bf16", "alloc_conf": args.alloc_conf or os.environ.get("PYTORCH_CUDA_ALLOC_CONF", "")},
+                   "grad_dtype": "bf16", "alloc_conf": args.alloc_conf or os.environ.get("PYTORCH_CUDA_ALLOC_CONF", ""),
+                   "alloc_conf_ignored_by_torch": ignored[0] if ignored else None},
         "frac_of_peak": round(value / PEAK_HBM_GBS, 4),
         "params_per_s": round(n / (ms * 1e-3), 1),
         "roofline": {

@@ -69,8 +69,9 @@ extern "C" {
  * The norm / scale / accumulate entry points read only grad, numel and flags.
  * Preconditions (the records live in device memory, so the library cannot check them
  * without a synchronisation): step is non-null; master, exp_avg, exp_avg_sq and grad are
- * non-null when numel > 0 and hold numel elements; tensors do not overlap. A group index
- * outside [0, n_groups) is read as group 0.
+ * non-null when numel > 0 and hold numel elements; tensors do not overlap. A record whose
+ * group is outside [0, n_groups) is not stepped with another group's hyper-parameters: the
+ * step poisons it instead (its step counter, master, moments and bf16 copy become NaN).
  */
 typedef struct tm_tensor {
   uint64_t master;

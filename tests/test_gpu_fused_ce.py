@@ -260,11 +260,23 @@ def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops(chunk):
     w1 = weight.clone().requires_grad_(True)
     loss = fused_linear_cross_entropy(h1, w1, labels, -100, chunk)
     (loss * 3.0).backward()
+    gh_ref, gw_ref = _chunk_loop_on_the_same_kernels(hidden, weight, labels, chunk, 3.0)
+    torch.cuda.synchronize()
+    assert torch.equal(w1.grad.view(torch.int32), gw_ref.view(torch.int32))
+    assert torch.equal(h1.grad.view(torch.int16), gh_ref.view(torch.int16))
 
+
+def _chunk_loop_on_the_same_kernels(hidden, weight, labels, chunk, grad_out):
+    """The reference's chunk loop (fused_linear_ce.py:67-91,117-126) run on this build's GEMMs
+    and row kernel: a zero fp32 grad_W, `+=` of each chunk's bf16 grad_W, `grad_hidden[s:e] =
+    gh`, then both scaled by grad_out / n_valid (grad_h by its bf16 rounding)."""
+    from torchure_amd import _native
+
+    n, v = hidden.shape[0], weight.shape[0]
     lib = _native.lib()
     stream = _native.stream_handle(DEV)
     w = weight.to(torch.bfloat16)
-    gw_ref = torch.zeros(v, d, dtype=torch.float32, device=DEV)
+    gw_ref = torch.zeros(weight.shape, dtype=torch.float32, device=DEV)
     gh_ref = torch.empty_like(hidden)
     row_loss = torch.empty(n, dtype=torch.float32, device=DEV)
     for s in range(0, n, chunk):
@@ -275,12 +287,44 @@ def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops(chunk):
         gh_ref[s:e] = torch.matmul(logits, w)
         gw_ref += torch.matmul(logits.t(), hidden[s:e])
     n_valid = (labels != -100).sum().clamp_min(1)
-    scale = torch.tensor(3.0, device=DEV) / n_valid
+    scale = torch.tensor(grad_out, device=DEV) / n_valid
     gw_ref.mul_(scale)
     gh_ref.mul_(scale.to(torch.bfloat16))
+    return gh_ref, gw_ref
+
+
+def test_default_chunking_is_the_reference_1024_rows():
+    """Called without chunk_size, the op chunks by 1024 rows, the reference's default
+    (fused_linear_ce.py:131): grad_W and grad_h equal the reference's chunk loop at 1024 rows
+    bit for bit (2600 rows: chunks of 1024, 1024 and 552). chunk_size=None and "auto" take the
+    4 GiB logits budget instead, here one chunk: the bits of chunk_size=2600."""
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(12)
+    n, d, v = 2600, 128, 2048
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::17] = -100
+
+    def run(*chunk_arg):
+        h = hidden.clone().requires_grad_(True)
+        w = weight.clone().requires_grad_(True)
+        fused_linear_cross_entropy(h, w, labels, -100, *chunk_arg).backward()
+        return h.grad, w.grad
+
+    gh, gw = run()
+    gh_ref, gw_ref = _chunk_loop_on_the_same_kernels(hidden, weight, labels, 1024, 1.0)
     torch.cuda.synchronize()
-    assert torch.equal(w1.grad.view(torch.int32), gw_ref.view(torch.int32))
-    assert torch.equal(h1.grad.view(torch.int16), gh_ref.view(torch.int16))
+    assert torch.equal(gw.view(torch.int32), gw_ref.view(torch.int32))
+    assert torch.equal(gh.view(torch.int16), gh_ref.view(torch.int16))
+    gh_one, gw_one = run(n)
+    for auto in (None, "auto"):
+        gh_a, gw_a = run(auto)
+        assert torch.equal(gw_a.view(torch.int32), gw_one.view(torch.int32))
+        assert torch.equal(gh_a.view(torch.int16), gh_one.view(torch.int16))
+    with pytest.raises(ValueError, match="chunk_size"):
+        run("large")
 
 
 def test_out_of_range_label_gives_nan_loss():

@@ -594,6 +594,71 @@ def test_full_size_properties(config):
         assert np.array_equal(opt.state[params[i]]["exp_avg"].cpu().numpy().reshape(-1), t[0]["m"])
 
 
+@pytest.mark.parametrize("config", ["qwen3-0.6b", "qwen3-4b"])
+def test_full_size_steady_state(config):
+    """BASELINE configs 2 and 4 at full size, from the steady state the reference step runs in
+    (torchure/train/trainer.py:391-397): state['step'] 1000 (the kernel uses t = 1001),
+    m ~ N(0, 1e-4), v = |N(0,1)| * 1e-8, masters ~ N(0, 0.02). Config 2 rescales its bf16 grads
+    to global norm 0.5, so clip 1.0 does not trigger (the coefficient is exactly 1.0); config 4
+    keeps N(0, 1e-3) grads, whose norm (~63) does trigger it. The norm is checked against fp64
+    over every grad, the bf16 copy against torch's cast everywhere, and sampled tensors -- the
+    tied embedding (the largest) among them -- bit for bit against the oracle: master, m, v,
+    bf16 copy and step counter."""
+    import torchure_amd as ta
+
+    shapes = shapes_for(config)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV, generator=g) * 0.02) for s in shapes]
+    work = ta.attach_bf16_working_params(params)
+    for w in work:
+        w.grad = (torch.randn(w.shape, device=DEV, generator=g) * 1e-3).to(torch.bfloat16)
+    if config == "qwen3-0.6b":  # config 2: "clip not triggered" -> global norm 0.5
+        sq = sum(float(torch.sum(w.grad.double() ** 2).item()) for w in work)
+        scale = 0.5 / math.sqrt(sq)
+        for w in work:
+            w.grad = (w.grad.float() * scale).to(torch.bfloat16)
+    grads = [w.grad for w in work]
+    opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
+                             {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True})
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=DEV)
+        st["exp_avg"] = torch.randn(p.shape, device=DEV, generator=g) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, device=DEV, generator=g).abs_() * 1e-8
+    sample = [0, 1, 5, 6, 200, len(shapes) - 1]
+
+    def host(t):
+        return t.detach().cpu().numpy().reshape(-1).copy()
+
+    before = {i: (host(params[i]), host(opt.state[params[i]]["exp_avg"]),
+                  host(opt.state[params[i]]["exp_avg_sq"]), H.from_dev_bf16(grads[i]).copy()) for i in sample}
+    exact_sq = sum(float(torch.sum(gr.double() ** 2).item()) for gr in grads)
+    norm = ta.clip_grad_norm(params, None, 1.0)
+    coef = opt._pending[0].clone()
+    opt.step()
+    torch.cuda.synchronize()
+    exact = math.sqrt(exact_sq)
+    assert abs(norm.item() - exact) <= 1e-6 * exact
+    if config == "qwen3-0.6b":
+        assert abs(norm.item() - 0.5) < 1e-3 and coef.item() == 1.0
+    else:
+        assert 50.0 < norm.item() < 80.0 and coef.item() < 0.02
+    for p, w in zip(params, work):
+        assert torch.equal(w, p.detach().to(torch.bfloat16))
+    for i in sample:
+        p0, m0, v0, gb = before[i]
+        out = np.zeros(p0.size, np.uint16)
+        wd = 0.1 if len(shapes[i]) >= 2 else 0.0
+        oracle.adamw_update_bf16(p0, m0, v0, gb, out, float(coef.item()), 1, 1001.0, 3e-4, 0.9, 0.95, wd,
+                                 1e-8, threaded=True)
+        st = opt.state[params[i]]
+        assert np.array_equal(host(params[i]).view(np.int32), p0.view(np.int32)), i
+        assert np.array_equal(host(st["exp_avg"]).view(np.int32), m0.view(np.int32)), i
+        assert np.array_equal(host(st["exp_avg_sq"]).view(np.int32), v0.view(np.int32)), i
+        assert np.array_equal(H.from_dev_bf16(work[i]), out), i
+        assert st["step"].item() == 1001.0
+
+
 def test_accumulate_list_fused_norm_and_reuse():
     """Row (f)1: 4 bf16 micro-steps accumulated into fp32 .grad in one launch each;
     the last also yields the global norm, bit-identical to the standalone norm pass,
@@ -1692,6 +1757,44 @@ def test_launch_planned_on_one_stream_runs_on_another():
             assert torch.equal(oa.state[x][k], ob.state[y][k])
     assert norm_a.norm.view(torch.int32).item() == norm_b.norm.view(torch.int32).item()
     assert norm_a.coef.view(torch.int32).item() == norm_b.coef.view(torch.int32).item()
+
+
+def test_record_with_unknown_group_is_poisoned():
+    """Called through the C ABI with a tensor record whose group index the call does not have,
+    tm_adamw_step poisons that tensor instead of stepping it with another group's
+    hyper-parameters (its step counter, master, moments become NaN, its bf16 copy 0x7FC0),
+    and steps the other records as usual: bit for bit what AdamW.step() gives them."""
+    from torchure_amd import _native
+    from torchure_amd.core import tables
+
+    host = H.make_host_set([(64, 32), (100,)], seed=81, grad_std=0.01)
+    pa, wa, oa = H.device_setup(host, DEV)
+    oa.step()  # the reference bits: no clip, the two torchure groups
+    pb, wb, ob = H.device_setup(host, DEV)
+    rows = np.zeros(2, dtype=_native.TENSOR_DTYPE)
+    for i, (p, w) in enumerate(zip(pb, wb)):
+        st = ob.state[p]
+        rows[i] = (p.data_ptr(), st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(), w.grad.data_ptr(),
+                   w.data_ptr(), st["step"].data_ptr(), p.numel(), 0, _native.TM_GRAD_BF16)
+    rows["group"] = [0, 7]
+    d_rows = tables.upload(rows, DEV)
+    chunk_elems = tables.DEFAULT_CHUNK_ELEMS
+    chunks, n_chunks = tables.CHUNKS.get(rows["numel"], chunk_elems, DEV)
+    ws = torch.empty(_native.workspace_bytes(2), dtype=torch.uint8, device=DEV)
+    hyper = _native.hyper_array([(H.HYPER["lr"], H.HYPER["beta1"], H.HYPER["beta2"], H.WD, H.HYPER["eps"]),
+                                 (H.HYPER["lr"], H.HYPER["beta1"], H.HYPER["beta2"], 0.0, H.HYPER["eps"])])
+    rc = _native.lib().tm_adamw_step(d_rows.data_ptr(), 2, chunks.data_ptr(), n_chunks, chunk_elems, hyper, 2,
+                                     None, ws.data_ptr(), _native.stream_handle(DEV))
+    _native.check(rc, "tm_adamw_step")
+    torch.cuda.synchronize()
+    assert torch.equal(pb[0], pa[0])
+    assert torch.equal(wb[0].view(torch.int16), wa[0].view(torch.int16))
+    for k in ("step", "exp_avg", "exp_avg_sq"):
+        assert torch.equal(ob.state[pb[0]][k], oa.state[pa[0]][k])
+    st = ob.state[pb[1]]
+    for t in (pb[1], st["step"], st["exp_avg"], st["exp_avg_sq"]):
+        assert bool(torch.isnan(t).all())
+    assert bool((wb[1].view(torch.int16) == 0x7FC0).all())
 
 
 def test_chunk_table_built_on_busy_stream_hit_on_another():

@@ -468,10 +468,19 @@ __global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (t >= n_tensors) return;
   const tm_tensor_t d = tensors[t];
-  int32_t gi = d.group;
-  if (gi < 0 || gi >= hyper.n) gi = 0;
-  const tm_hyper_t h = hyper.g[gi];
+  const int32_t gi = d.group;
   float* step_p = reinterpret_cast<float*>(d.step);
+  if (gi < 0 || gi >= hyper.n) {
+    // A record naming a group the call does not have: the records live in device memory, so
+    // the host cannot refuse it without a synchronisation. The tensor is poisoned instead of
+    // stepped with another group's hyper-parameters: its step counter becomes NaN, and NaN
+    // constants make the update write NaN into its master, moments and bf16 copy.
+    const double nan = __builtin_nan("");
+    *step_p = __builtin_nanf("");
+    scal[t] = TensorScal{nan, nan, nan, nan, nan, nan, __builtin_nanf(""), __builtin_nanf(""), 1u, 0u};
+    return;
+  }
+  const tm_hyper_t h = hyper.g[gi];
   const float step = *step_p + 1.0f;
   *step_p = step;
   const double bc1 = 1.0 - pow(h.beta1, static_cast<double>(step));

@@ -38,11 +38,11 @@ hidden is cast to bf16 once (RNE, as autocast does), grad_hidden stays a bf16 GE
 until backward, and tm_ce_widen_scale writes the fp32 gradient float(gh) * grad_out / n_valid
 (the reference's fp32 copy and mul_, :80,120).
 
-MI355X sizing: the chunk is chosen so that the bf16 logits of a chunk take up to
-``logits_bytes`` (4 GiB by default) instead of 1024 rows: with 288 GB of HBM the
-whole Qwen3 vocabulary for 8K-16K tokens fits in one chunk, so the fp32 grad_W
-is written once, by the backward hand-over, instead of being read and written for
-every pair of 1024-row chunks, and the GEMMs get large M.
+Chunking: 1024 rows by default, the reference's default (:131). ``chunk_size=None`` or
+``"auto"`` opts into MI355X sizing: chunks whose bf16 logits take up to 4 GiB, so that
+with 288 GB of HBM the whole Qwen3 vocabulary for 8K-16K tokens fits in one chunk, the
+fp32 grad_W is written once, by the backward hand-over, instead of being read and written
+for every pair of 1024-row chunks, and the GEMMs get large M.
 """
 
 from __future__ import annotations
@@ -96,7 +96,10 @@ def _checked(hidden, weight, labels, chunk_size):
                            f"labels {tuple(labels.shape)} do not match")
     if weight.device != hidden.device or labels.device != hidden.device:
         raise RuntimeError(f"{who}: hidden, weight and labels must be on one device")
-    chunk = auto_chunk_rows(n, v) if chunk_size is None else int(chunk_size)
+    auto = chunk_size is None or (isinstance(chunk_size, str) and chunk_size == "auto")
+    if isinstance(chunk_size, str) and not auto:
+        raise ValueError(f"{who}: chunk_size must be a positive int, None or 'auto', got {chunk_size!r}")
+    chunk = auto_chunk_rows(n, v) if auto else int(chunk_size)
     if chunk < 1:
         raise ValueError(f"{who}: chunk_size must be positive, got {chunk_size}")
     return n, v, chunk, fp32
@@ -246,8 +249,16 @@ def fused_linear_cross_entropy(
     weight: torch.Tensor,  # (V, D) lm_head weight
     labels: torch.Tensor,  # (B, S) or (N,), already shifted, int64
     ignore_index: int = -100,
-    chunk_size: int | None = None,
+    chunk_size: int | str | None = 1024,
 ) -> torch.Tensor:
+    """Mean cross-entropy of ``hidden @ weight.T`` against ``labels`` over the rows whose
+    label is not ``ignore_index``, in chunks of ``chunk_size`` rows, as
+    torchure/loss/fused_linear_ce.py:130-136 (default 1024 rows, as there: each chunk's bf16
+    grad_W is rounded before it is added, so the chunking fixes grad_W's bits).
+    ``chunk_size=None`` or ``"auto"`` sizes chunks by a 4 GiB logits budget instead
+    (``auto_chunk_rows``): the whole Qwen3 vocabulary for 8K-16K tokens in one chunk, one
+    fp32 grad_W pass and large GEMMs, at the cost of other grad_W bits and up to 4 GiB of
+    logits plus one bf16 grad_W (V x D) held from forward to backward."""
     if hidden.dim() == 3:
         hidden = hidden.reshape(-1, hidden.shape[-1])
         labels = labels.reshape(-1)
