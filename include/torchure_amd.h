@@ -176,6 +176,23 @@ int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
                   int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups,
                   int32_t n_groups, const float* d_coef, void* d_ws, void* stream);
 
+/* Largest n_tensors tm_adamw_step_noalloc accepts (the entries of its static scratch). */
+#define TM_NOALLOC_MAX_TENSORS 16384
+
+/*
+ * tm_adamw_step without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has
+ * no counterpart in the reference. Its per-tensor constants live in a static device array of
+ * TM_NOALLOC_MAX_TENSORS entries (1 MiB on every GPU the library runs on, held until the
+ * process ends); a call with more tensors returns TM_EINVAL. It calls no allocating routine.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * or two host threads) race and must be serialised by the caller. Results equal
+ * tm_adamw_step's, bit for bit.
+ */
+int tm_adamw_step_noalloc(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                          int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups,
+                          int32_t n_groups, const float* d_coef, void* stream);
+
 /*
  * Micro-step gradient accumulation: d_acc[i] (fp32) += (float)d_micro[i] (bf16),
  * over `numel` elements. The fp32 accumulation buffer is what torch autograd

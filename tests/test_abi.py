@@ -40,7 +40,8 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_constants():
     h = _header()
     assert int(re.search(r"#define TM_ABI_VERSION (\d+)", h).group(1)) == _native.lib().tm_abi_version()
-    for name in ("TM_GRAD_F32", "TM_FLAG_CLIP", "TM_MAX_GROUPS", "TM_CHUNK_ALIGN", "TM_NORM_PARTIALS"):
+    for name in ("TM_GRAD_F32", "TM_FLAG_CLIP", "TM_MAX_GROUPS", "TM_CHUNK_ALIGN", "TM_NORM_PARTIALS",
+                 "TM_NOALLOC_MAX_TENSORS"):
         val = int(re.search(rf"#define {name} (\d+)u?", h).group(1))
         assert getattr(_native, name) == val, name
 

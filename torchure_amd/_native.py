@@ -30,6 +30,7 @@ TM_FLAG_CLIP = 2
 TM_MAX_GROUPS = 16
 TM_CHUNK_ALIGN = 2048
 TM_NORM_PARTIALS = 2048
+TM_NOALLOC_MAX_TENSORS = 16384
 
 # tm_tensor_t (include/torchure_amd.h), 64 bytes.
 TENSOR_DTYPE = np.dtype(
@@ -83,6 +84,10 @@ _SIGNATURES = {
     "tm_adamw_step": (
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _i64, ctypes.POINTER(TmHyper), ctypes.c_int32, _vp, _vp, _vp],
+    ),
+    "tm_adamw_step_noalloc": (
+        ctypes.c_int,
+        [_vp, _i64, _vp, _i64, _i64, ctypes.POINTER(TmHyper), ctypes.c_int32, _vp, _vp],
     ),
     "tm_grad_accumulate_list": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]),
     "tm_clip_coef": (ctypes.c_int, [_vp, ctypes.c_float, _vp, _vp]),

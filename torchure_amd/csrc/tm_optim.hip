@@ -35,6 +35,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "torchure_amd.h"
 #include "tm_internal.h"
 
@@ -767,6 +769,91 @@ int check_table(const void* d_tensors, int64_t n_tensors, const void* d_chunks, 
   return TM_OK;
 }
 
+int check_step_args(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                    int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups, int32_t n_groups,
+                    const char* who) {
+  int rc = check_table(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, who);
+  if (rc) return rc;
+  if (n_groups < 1 || n_groups > TM_MAX_GROUPS || !h_groups)
+    return fail(TM_EINVAL, "%s: n_groups %d outside 1..%d", who, n_groups, TM_MAX_GROUPS);
+  return TM_OK;
+}
+
+// prep (step += 1, per-tensor constants into scal) then the update, stream-ordered.
+int launch_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks, int64_t n_chunks,
+                int64_t chunk_elems, const tm_hyper_t* h_groups, int32_t n_groups, const float* d_coef,
+                TensorScal* scal, hipStream_t s) {
+  if (n_tensors == 0) return TM_OK;
+  HyperArgs hyper;
+  memset(&hyper, 0, sizeof(hyper));
+  for (int i = 0; i < n_groups; ++i) hyper.g[i] = h_groups[i];
+  hyper.n = n_groups;
+  hipLaunchKernelGGL(adamw_prep_kernel, dim3(static_cast<uint32_t>((n_tensors + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, s, d_tensors, n_tensors, hyper, scal);
+  int rc = check_launch("adamw_prep_kernel");
+  if (rc) return rc;
+  if (n_chunks == 0) return TM_OK;
+  // d_coef == NULL: TM_FLAG_CLIP is ignored (every grad is used unscaled).
+  return launch_chunk_slices(n_chunks, chunk_elems, "adamw_update_kernel",
+                             [&](uint32_t first, uint32_t spc, dim3 grid) {
+                               hipLaunchKernelGGL(adamw_update_kernel, grid, dim3(kWave), 0, s, d_tensors,
+                                                  n_tensors, d_chunks, first, spc, chunk_elems, scal,
+                                                  d_coef);
+                             });
+}
+
+}  // namespace
+
+// ------------------------------------------------- static scratch of the allocation-free step
+//
+// tm_adamw_step_noalloc keeps its per-tensor constants (64 bytes a tensor, written by the prep
+// kernel and read by the update, so nothing in it needs clearing) in this file-scope device
+// array instead of a caller's workspace: TM_NOALLOC_MAX_TENSORS entries, 1 MiB on every GPU the
+// library runs on, held until the process ends. Its name is a host-side stand-in, never a
+// device address: host code uses only the address hipGetSymbolAddress returns, looked up once
+// per device with that device current and kept in g_scratch.
+static __device__ __align__(256) TensorScal scratch[TM_NOALLOC_MAX_TENSORS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+TensorScal* g_scratch[kMaxDevices] = {};
+
+// The device the work of stream s runs on (the current device for the null stream).
+int stream_device(hipStream_t s, int* dev) {
+  hipError_t e = s ? hipStreamGetDevice(s, dev) : hipGetDevice(dev);
+  if (e != hipSuccess) return fail(TM_ELAUNCH, "tm_adamw_step_noalloc: no device for the stream: %s",
+                                   hipGetErrorString(e));
+  if (*dev < 0 || *dev >= kMaxDevices)
+    return fail(TM_EINVAL, "tm_adamw_step_noalloc: device %d beyond the %d supported", *dev, kMaxDevices);
+  return TM_OK;
+}
+
+int static_scratch(hipStream_t s, TensorScal** out) {
+  int dev = -1;
+  int rc = stream_device(s, &dev);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* ptr = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur >= 0 && cur != dev) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess) e = back;
+    }
+    if (e != hipSuccess || !ptr)
+      return fail(TM_ELAUNCH, "tm_adamw_step_noalloc: address of the static scratch on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch[dev] = static_cast<TensorScal*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return TM_OK;
+}
+
 }  // namespace
 
 // ======================================================================= C ABI
@@ -847,30 +934,30 @@ int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
 int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
                   int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups,
                   int32_t n_groups, const float* d_coef, void* d_ws, void* stream) {
-  int rc = check_table(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, "tm_adamw_step");
+  int rc = check_step_args(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, h_groups, n_groups,
+                           "tm_adamw_step");
   if (rc) return rc;
-  if (n_groups < 1 || n_groups > TM_MAX_GROUPS || !h_groups)
-    return fail(TM_EINVAL, "tm_adamw_step: n_groups %d outside 1..%d", n_groups, TM_MAX_GROUPS);
   if (!d_ws) return fail(TM_EINVAL, "tm_adamw_step: null workspace");
-  if (n_tensors == 0) return TM_OK;
-  HyperArgs hyper;
-  memset(&hyper, 0, sizeof(hyper));
-  for (int i = 0; i < n_groups; ++i) hyper.g[i] = h_groups[i];
-  hyper.n = n_groups;
   TensorScal* scal =
       reinterpret_cast<TensorScal*>(static_cast<char*>(d_ws) + align_up(kPartialBytes, 256));
+  return launch_step(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, h_groups, n_groups, d_coef, scal,
+                     static_cast<hipStream_t>(stream));
+}
+
+int tm_adamw_step_noalloc(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
+                          int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups,
+                          int32_t n_groups, const float* d_coef, void* stream) {
+  int rc = check_step_args(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, h_groups, n_groups,
+                           "tm_adamw_step_noalloc");
+  if (rc) return rc;
+  if (n_tensors > TM_NOALLOC_MAX_TENSORS)
+    return fail(TM_EINVAL, "tm_adamw_step_noalloc: %lld tensors, at most %d (its static scratch holds %d)",
+                (long long)n_tensors, TM_NOALLOC_MAX_TENSORS, TM_NOALLOC_MAX_TENSORS);
+  if (n_tensors == 0) return TM_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(adamw_prep_kernel, dim3(static_cast<uint32_t>((n_tensors + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, s, d_tensors, n_tensors, hyper, scal);
-  if ((rc = check_launch("adamw_prep_kernel"))) return rc;
-  if (n_chunks == 0) return TM_OK;
-  // d_coef == NULL: TM_FLAG_CLIP is ignored (every grad is used unscaled).
-  return launch_chunk_slices(n_chunks, chunk_elems, "adamw_update_kernel",
-                             [&](uint32_t first, uint32_t spc, dim3 grid) {
-                               hipLaunchKernelGGL(adamw_update_kernel, grid, dim3(kWave), 0, s, d_tensors,
-                                                  n_tensors, d_chunks, first, spc, chunk_elems, scal,
-                                                  d_coef);
-                             });
+  TensorScal* scal = nullptr;
+  if ((rc = static_scratch(s, &scal))) return rc;
+  return launch_step(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, h_groups, n_groups, d_coef, scal, s);
 }
 
 int tm_grad_accumulate_list(const tm_accum_t* d_list, int64_t n_list, const tm_chunk_t* d_chunks,
