@@ -1165,6 +1165,34 @@ def test_materialize_clip_equals_eager_clip():
         assert torch.equal(a.grad, b.grad)
 
 
+def test_deferred_clip_leaves_grads_unscaled_until_step():
+    """The documented drop-in difference of the deferred clip (the default): between
+    clip_grad_norm and step(), p.grad still reads the unscaled values, where the reference's
+    clip has already scaled them in place (torchure/core/grad_helper.py:32-33). The step
+    applies the scale; materialize_clip() applies it to p.grad on request, giving the
+    in-place clip's values; with defer_clip=False the clip scales p.grad at once."""
+    import torchure_amd as ta
+
+    host = H.make_host_set([(64, 64), (50,)], seed=39, grad_std=0.1, grad_dtype="f32")
+    pd, _, od = H.device_setup(host, DEV, working=False)
+    pe, _, oe = H.device_setup(host, DEV, working=False)
+    oe.defer_clip = False
+    raw = [p.grad.clone() for p in pd]
+    ta.clip_grad_norm(pd, None, 1.0)
+    ta.clip_grad_norm(pe, None, 1.0)
+    torch.cuda.synchronize()
+    coef = od._pending[0].item()
+    assert coef < 1.0
+    for p, g in zip(pd, raw):  # deferred: unscaled until the step
+        assert torch.equal(p.grad, g)
+    for p, g in zip(pe, raw):  # eager (the reference's behaviour): scaled in place
+        assert torch.equal(p.grad, g * torch.tensor(coef, device=DEV))
+    od.materialize_clip()
+    torch.cuda.synchronize()
+    for a, b in zip(pd, pe):
+        assert torch.equal(a.grad, b.grad)
+
+
 @pytest.mark.parametrize("route", ["eager", "materialize"])
 def test_bf16_grads_deferred_and_in_place_clip(route):
     """bf16 working-copy grads take one of two clip routes, each checked against its own

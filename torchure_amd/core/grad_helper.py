@@ -158,6 +158,16 @@ def clip_grad_norm(params, mesh, max_norm, shard_dims=()) -> torch.Tensor:
     (grad_helper.py:20-24), which keeps its bits while the fp32 square neither
     overflows nor underflows, and gives inf above sqrt(FLT_MAX) as the reference does.
     Larger shard dimensions raise NotImplementedError.
+
+    Deferred clip (the default when every grad belongs to one torchure_amd.AdamW whose
+    ``defer_clip`` is set): the reference scales ``p.grad`` in place here
+    (grad_helper.py:32-33); this function instead hands the coefficient, a device scalar, to
+    that optimizer, whose next ``step()`` applies the same fp32 multiply inside the update
+    kernel, saving a read and a write of every grad. Until then ``p.grad`` still reads the
+    unscaled values. Code that inspects the clipped grads before the step calls
+    ``optimizer.materialize_clip()`` (the reference's in-place values) or builds the
+    optimizer with ``defer_clip=False``. A grad modified in place before the step makes the
+    step raise; a grad replaced by a new tensor steps unscaled, as in the reference.
     """
     if shard_dims:
         _check_shard_dims(mesh, shard_dims)
