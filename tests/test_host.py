@@ -305,3 +305,27 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120, cwd=root)
     assert p.returncode == 2
     assert "one GPU only" in p.stderr and not p.stdout.strip()
+
+
+def test_fused_linear_ce_default_chunk_is_the_reference_1024():
+    """fused_linear_cross_entropy keeps the reference's default chunk_size=1024
+    (torchure/loss/fused_linear_ce.py:131); None and "auto" opt into MI355X sizing."""
+    import inspect
+
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    assert inspect.signature(fused_linear_cross_entropy).parameters["chunk_size"].default == 1024
+
+
+def test_bench_cpu_baseline_on_a_small_set():
+    """bench.py's CPU baseline times the reference composition over a whole parameter set
+    with one thread per usable logical CPU, and reports the other sets under configs."""
+    import bench
+
+    out = bench.run_cpu_baseline(["tiny", "tiny"], steps=2, seconds=0.0)
+    logical, physical = bench._cpu_topology()
+    assert out["kind"] == "reference" and out["unit"] == "GB/s" and out["value"] > 0
+    assert out["cores"] == out["logical_cpus"] == logical >= 1
+    assert physical is None or 1 <= physical <= logical
+    assert out["ms_per_step"] > 0 and "whole parameter set (24 tensors, 2622976 params)" in out["sample"]
+    assert out["configs"]["tiny"]["n_params"] == 2622976
