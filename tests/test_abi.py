@@ -97,6 +97,36 @@ def test_argument_validation_without_gpu():
     assert lib.tm_grad_norm(None, 1, fake, 1, 2048, 1.0, 0, fake, fake, None, None) < 0
 
 
+def test_grad_h_gemm_workspace_and_shape_checks_without_gpu():
+    """The split-K grad_h GEMM: K splits a multiple of 8 (one group per XCD) picked by the
+    launch's cost model, fp32 partials of rows x dim per split; shapes it does not tile,
+    misaligned pointers and short workspaces are refused before any HIP call."""
+    lib = _native.lib()
+    ws = lib.tm_ce_grad_h_workspace_bytes
+    v = 151936
+    assert ws(1024, v, 1024) == 16 * 1024 * 1024 * 4  # 16 tiles x 16 splits: one round of 256 CUs
+    assert ws(2048, v, 1024) == 8 * 2048 * 1024 * 4
+    assert ws(1024, v, 2560) == 32 * 1024 * 2560 * 4  # 40 tiles x 32 splits: five full rounds
+    assert ws(3072, v, 1024) == 16 * 3072 * 1024 * 4  # 48 x 16: three full rounds
+    assert ws(8192, v, 4096) == 8 * 8192 * 4096 * 4
+    assert ws(256, 640, 256) == 16 * 256 * 256 * 4  # 10 K slices: more splits only add partials
+    assert ws(1000, v, 1024) == 0 and ws(1024, v, 1000) == 0 and ws(0, v, 256) == 0 and ws(256, 100, 256) == 0
+    fake = ctypes.c_void_p(0x1000)
+    big = 1 << 40
+    for rows, vocab, dim in ((1000, 4096, 1024), (1024, 4000, 1024), (1024, 4096, 1000), (0, 4096, 256)):
+        assert lib.tm_ce_grad_h_bf16(fake, fake, fake, rows, vocab, dim, fake, big, None) < 0
+        assert b"multiples" in lib.tm_last_error()
+    odd = ctypes.c_void_p(0x1008)
+    assert lib.tm_ce_grad_h_bf16(fake, odd, fake, 256, 4096, 256, fake, big, None) < 0
+    assert b"aligned" in lib.tm_last_error()
+    assert lib.tm_ce_grad_h_bf16(fake, fake, fake, 256, 4096, 256, fake, ws(256, 4096, 256) - 1, None) < 0
+    assert b"workspace" in lib.tm_last_error()
+    assert lib.tm_ce_grad_h_bf16(fake, None, fake, 256, 4096, 256, fake, big, None) < 0
+    assert lib.tm_ce_transpose_bf16(fake, fake, 100, 64, None) < 0
+    assert b"multiples of 64" in lib.tm_last_error()
+    assert lib.tm_ce_transpose_bf16(fake, ctypes.c_void_p(0x1002), 64, 64, None) < 0
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "_LIB", None)
     monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "missing.so"))

@@ -271,20 +271,24 @@ def _chunk_loop_on_the_same_kernels(hidden, weight, labels, chunk, grad_out):
     and row kernel: a zero fp32 grad_W, `+=` of each chunk's bf16 grad_W, `grad_hidden[s:e] =
     gh`, then both scaled by grad_out / n_valid (grad_h by its bf16 rounding)."""
     from torchure_amd import _native
+    from torchure_amd.loss.fused_linear_ce import GradHidden
 
     n, v = hidden.shape[0], weight.shape[0]
     lib = _native.lib()
     stream = _native.stream_handle(DEV)
-    w = weight.to(torch.bfloat16)
+    w = weight.to(torch.bfloat16).contiguous()
     gw_ref = torch.zeros(weight.shape, dtype=torch.float32, device=DEV)
     gh_ref = torch.empty_like(hidden)
     row_loss = torch.empty(n, dtype=torch.float32, device=DEV)
+    grad_h = GradHidden(w, [min(chunk, n - s) for s in range(0, n, chunk)], lib, stream)
     for s in range(0, n, chunk):
         e = min(s + chunk, n)
         logits = torch.matmul(hidden[s:e], w.t())
         _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, -100,
                                           row_loss[s:].data_ptr(), stream), "tm_ce_rows_bf16")
-        gh_ref[s:e] = torch.matmul(logits, w)
+        gh = torch.empty((e - s, w.shape[1]), dtype=torch.bfloat16, device=DEV)
+        grad_h(logits, gh)
+        gh_ref[s:e] = gh
         gw_ref += torch.matmul(logits.t(), hidden[s:e])
     n_valid = (labels != -100).sum().clamp_min(1)
     scale = torch.tensor(grad_out, device=DEV) / n_valid

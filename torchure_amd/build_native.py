@@ -18,7 +18,7 @@ import subprocess
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(_HERE)
-SOURCES = [os.path.join(_HERE, "csrc", "tm_optim.hip"), os.path.join(_HERE, "csrc", "tm_ce.hip")]
+SOURCES = [os.path.join(_HERE, "csrc", f) for f in ("tm_optim.hip", "tm_ce.hip", "tm_ce_gemm.hip")]
 INCLUDE = os.path.join(ROOT, "include")
 OUTPUT = os.path.join(_HERE, "libtorchure_amd.so")
 ARCH = "gfx950"

@@ -10,7 +10,9 @@ Per chunk of rows:
   logits = h @ W^T                  bf16 GEMM (hipBLASLt, through torch.matmul)
   tm_ce_rows_bf16                   one fused kernel: logsumexp, per-row loss and
                                     grad_logits = bf16(softmax - onehot), in place
-  grad_h = grad_logits @ W          bf16 GEMM
+  grad_h = grad_logits @ W          bf16 GEMM: tm_ce_grad_h_bf16, a split-K MFMA GEMM with a
+                                    fixed-order reduction, on chunks of 256-4096 rows (multiples
+                                    of 256, D of 256, V of 64); hipBLASLt on other shapes
   grad_W += grad_logits^T @ h       bf16 GEMM, then tm_ce_grad_w(2) into fp32
 then tm_ce_loss sums the per-row losses in a fixed order (deterministic).
 
@@ -121,6 +123,48 @@ def _mean_loss(row_loss, labels, n, ignore_index, lib, stream):
     return out3[2].clone(), out3[1:2]
 
 
+SPLITK_GRAD_H_MAX_ROWS = 4096
+
+
+def splitk_grad_h_fits(rows: int, dim: int, vocab: int) -> bool:
+    """Chunks whose grad_h runs on the split-K MFMA GEMM (tm_ce_grad_h_bf16): the shapes it
+    tiles (rows and dim multiples of 256, vocab of 64) up to SPLITK_GRAD_H_MAX_ROWS rows. With
+    few 256 x 256 output tiles and K = vocab, a library GEMM leaves most of the 256 CUs idle;
+    above that, it fills the chip by itself."""
+    return (256 <= rows <= SPLITK_GRAD_H_MAX_ROWS and rows % 256 == 0 and 0 < dim <= 65536
+            and dim % 256 == 0 and vocab > 0 and vocab % 64 == 0)
+
+
+class GradHidden:
+    """grad_h = grad_logits @ W (fused_linear_ce.py:52, stored at :79) for the chunks of one
+    call: the split-K MFMA GEMM on the chunks ``splitk_grad_h_fits`` accepts, with W^T made
+    once for the call and one fp32 partials workspace shared by the chunks (stream-ordered),
+    and torch.matmul (hipBLASLt) on the others. ``w`` is the contiguous bf16 weight (V x D)."""
+
+    def __init__(self, w: torch.Tensor, chunk_rows, lib, stream):
+        self.w, self.lib, self.stream = w, lib, stream
+        self.vocab, self.dim = w.shape
+        fits = [r for r in set(chunk_rows) if splitk_grad_h_fits(r, self.dim, self.vocab)]
+        self.wt = self.ws = None
+        if fits:
+            self.wt = torch.empty((self.dim, self.vocab), dtype=torch.bfloat16, device=w.device)
+            _native.check(lib.tm_ce_transpose_bf16(self.wt.data_ptr(), w.data_ptr(), self.vocab, self.dim,
+                                                   stream), "tm_ce_transpose_bf16")
+            nbytes = max(lib.tm_ce_grad_h_workspace_bytes(r, self.vocab, self.dim) for r in fits)
+            self.ws = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+
+    def __call__(self, grad_logits: torch.Tensor, out: torch.Tensor) -> None:
+        rows = grad_logits.shape[0]
+        if self.wt is None or not splitk_grad_h_fits(rows, self.dim, self.vocab):
+            torch.matmul(grad_logits, self.w, out=out)
+            return
+        if not (grad_logits.is_contiguous() and out.is_contiguous() and out.dtype == torch.bfloat16):
+            raise RuntimeError("fused_linear_cross_entropy: grad_h GEMM operands must be contiguous bf16")
+        _native.check(self.lib.tm_ce_grad_h_bf16(out.data_ptr(), grad_logits.data_ptr(), self.wt.data_ptr(), rows,
+                                                 self.vocab, self.dim, self.ws.data_ptr(), self.ws.numel(),
+                                                 self.stream), "tm_ce_grad_h_bf16")
+
+
 def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
     """The loss when no input needs a gradient (e.g. evaluation under torch.no_grad): the
     same logits GEMM and the same per-row arithmetic as the training path, so the same
@@ -159,6 +203,7 @@ class _FusedLinearCE(torch.autograd.Function):
         pending = last_gw = None
         accumulated = False
         row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
+        grad_h_of = GradHidden(w, [min(chunk, n - s) for s in range(0, n, chunk)], lib, stream) if want_h else None
         for s in range(0, n, chunk):
             e = min(s + chunk, n)
             h = hb[s:e]
@@ -167,7 +212,7 @@ class _FusedLinearCE(torch.autograd.Function):
                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
                           "tm_ce_rows_bf16")
             if want_h:
-                torch.matmul(logits, w, out=grad_hidden[s:e])
+                grad_h_of(logits, grad_hidden[s:e])
             if want_w:
                 gw = torch.matmul(logits.t(), h)  # (V, D) bf16
                 if e == n:
@@ -184,6 +229,7 @@ class _FusedLinearCE(torch.autograd.Function):
                     pending = None
                     del gw
             del logits
+        del grad_h_of
         loss, ctx.n_valid = _mean_loss(row_loss, labels, n, ignore_index, lib, stream)
         ctx.grad_hidden = grad_hidden
         ctx.fp32_hidden = fp32
