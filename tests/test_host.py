@@ -329,3 +329,18 @@ def test_bench_cpu_baseline_on_a_small_set():
     assert physical is None or 1 <= physical <= logical
     assert out["ms_per_step"] > 0 and "whole parameter set (24 tensors, 2622976 params)" in out["sample"]
     assert out["configs"]["tiny"]["n_params"] == 2622976
+
+
+def test_fused_ce_grad_h_gemm_choice():
+    """Chunks whose grad_h runs on the split-K MFMA GEMM: shapes it tiles (rows and hidden
+    size multiples of 256, vocabulary of 64) with at most 64 output tiles of 256 x 256;
+    everything else stays on torch.matmul."""
+    from torchure_amd.loss.fused_linear_ce import splitk_grad_h_fits
+
+    v = 151936
+    assert splitk_grad_h_fits(1024, 1024, v)  # the reference's chunk on the Qwen3-0.6B head
+    assert splitk_grad_h_fits(4096, 1024, v)  # the trainer's chunk: 64 tiles
+    assert not splitk_grad_h_fits(8192, 1024, v)  # 128 tiles
+    assert splitk_grad_h_fits(1024, 4096, v) and not splitk_grad_h_fits(2048, 4096, v)
+    assert not splitk_grad_h_fits(1000, 1024, v) and not splitk_grad_h_fits(1024, 1000, v)
+    assert not splitk_grad_h_fits(1024, 1024, 151937) and not splitk_grad_h_fits(0, 1024, v)

@@ -14,8 +14,13 @@
 //                        on scheduling.
 // Operands: grad_logits row-major (K contiguous) and W^T (D x V, K contiguous, made by
 // transpose_bf16_kernel), both streamed global -> LDS with direct loads (global_load_lds,
-// 16 bytes a lane) into a two-stage ring of 64-deep K slices; 16-byte chunks are XOR-swizzled
-// by row so the operand reads of 32 consecutive rows spread over the LDS banks. All the
+// 16 bytes a lane) into a two-stage ring of 64-deep K slices. gfx950's LDS has 64 four-byte
+// banks and serves a 16-byte-per-lane read 16 lanes at a time, so the 16 lanes reading 16
+// consecutive 128-byte rows must hit 16 different 16-byte bank groups: a row's chunk c sits at
+// slot c ^ ((row >> 1) & 7), which gives rows 2j and 2j+1 (one even, one odd: the two halves
+// of the banks) the slot pattern c ^ j. (The 32-bank pattern c ^ (row & 7) put rows r and r+8
+// on one bank group and doubled the read time; rocprof counted half the LDS cycles as bank
+// conflicts.) All the
 // workgroups of one split run on one XCD (workgroup w runs on XCD w % 8), so that split's
 // K slices of both operands are read from HBM about once and then served from that XCD's L2.
 
@@ -76,7 +81,8 @@ __global__ __launch_bounds__(kGemmThreads) void grad_h_gemm_kernel(
 
   // One stage: kTile rows of A then kTile rows of Bt, 64 bf16 each; load instruction q of the
   // stage fills rows 8q .. 8q+7 (1 KB, lane i -> row 8q + i/8, chunk slot i%8), loading the
-  // row's 16-byte chunk (i%8) ^ (row & 7) so the chunks end up XOR-swizzled by row.
+  // row's 16-byte chunk (i%8) ^ ((row >> 1) & 7), so that chunk c ends up in slot
+  // c ^ ((row >> 1) & 7).
   auto issue = [&](int it, int stage) {
     const int64_t k0 = static_cast<int64_t>(it) * kSliceK;
     uint8_t* base = smem + stage * kStageBytes;
@@ -84,7 +90,7 @@ __global__ __launch_bounds__(kGemmThreads) void grad_h_gemm_kernel(
     for (int j = 0; j < kLoadsPerWave; ++j) {
       const int q = wave * kLoadsPerWave + j;  // 0 .. 63: A rows for q < 32, Bt rows after
       const int r = (q & 31) * 8 + lrow;
-      const int c = lpos ^ (r & 7);
+      const int c = lpos ^ ((r >> 1) & 7);
       const uint16_t* src = q < 32 ? A + static_cast<int64_t>(m0 + r) * K : Bt + static_cast<int64_t>(n0 + r) * K;
       __builtin_amdgcn_global_load_lds(
           (const void __attribute__((address_space(1)))*)(src + k0 + c * 8),
@@ -115,12 +121,12 @@ __global__ __launch_bounds__(kGemmThreads) void grad_h_gemm_kernel(
 #pragma unroll
       for (int mi = 0; mi < kBlocksM; ++mi) {
         const int r = wm * (kTile / kWavesM) + mi * 32 + (lane & 31);
-        a[mi] = *(const bf16x8*)(base + r * 128 + ((kc ^ (r & 7)) * 16));
+        a[mi] = *(const bf16x8*)(base + r * 128 + ((kc ^ ((r >> 1) & 7)) * 16));
       }
 #pragma unroll
       for (int ni = 0; ni < kBlocksN; ++ni) {
         const int r = wn * (kTile / kWavesN) + ni * 32 + (lane & 31);
-        b[ni] = *(const bf16x8*)(base + kTile * 128 + r * 128 + ((kc ^ (r & 7)) * 16));
+        b[ni] = *(const bf16x8*)(base + kTile * 128 + r * 128 + ((kc ^ ((r >> 1) & 7)) * 16));
       }
 #pragma unroll
       for (int mi = 0; mi < kBlocksM; ++mi)
