@@ -59,10 +59,14 @@ def parse():
                     help="comma list of extra configs reported under 'extra' (empty = none); "
                          "'<config>-again' runs that config once more, on fresh allocations made "
                          "after the earlier legs' memory was released")
-    ap.add_argument("--mode", choices=("bench", "kernels", "ce"), default="bench",
+    ap.add_argument("--mode", choices=("bench", "kernels", "ce", "ce-gemm"), default="bench",
                     help="kernels: only the norm and update launches (for an -fp32acc config, the "
                          "accumulation launches), --reps times each, plus a 2 GiB device copy for "
-                         "calibrating HBM byte counters (for rocprofv3 --pmc)")
+                         "calibrating HBM byte counters (for rocprofv3 --pmc); ce: the fused linear "
+                         "+ CE legs only; ce-gemm: the fused CE's grad_h GEMM, split-K kernel and "
+                         "torch.matmul, at --gemm-shapes")
+    ap.add_argument("--gemm-shapes", default="1024x1024,4096x1024,8192x1024,1024x2560,4096x2560",
+                    help="ce-gemm mode: comma list of ROWSxDIM grad_h shapes (vocabulary 151,936)")
     ap.add_argument("--reps", type=int, default=3)
     ap.add_argument("--states", type=int, default=1,
                     help="kernels mode: build this many copies of the state, each its own set of "
@@ -618,6 +622,55 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
     return out
 
 
+def run_ce_gemm(shapes, reps: int, dev, vocab: int = 151936):
+    """The fused CE's grad_h = grad_logits @ W (torchure/loss/fused_linear_ce.py:52) per chunk
+    shape: this build's split-K MFMA GEMM (tm_ce_grad_h_bf16, its fixed-order reduction
+    included) against torch.matmul (hipBLASLt) on the same bf16 operands, each timed over
+    `reps` launches after one warm-up, plus the once-per-call W^T transpose."""
+    import torch
+
+    from torchure_amd import _native
+
+    lib, stream = _native.lib(), _native.stream_handle(dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    out = {"vocab": vocab, "reps": reps, "shapes": {}}
+    g = torch.Generator(device=dev).manual_seed(0)
+    for dim in sorted({d for _, d in shapes}):
+        w = (torch.randn(vocab, dim, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+        wt = torch.empty((dim, vocab), dtype=torch.bfloat16, device=dev)
+        ms_t = timed(lambda: _native.check(lib.tm_ce_transpose_bf16(wt.data_ptr(), w.data_ptr(), vocab, dim, stream),
+                                           "tm_ce_transpose_bf16"))
+        out["transpose_ms_dim%d" % dim] = round(ms_t, 4)
+        for rows in [r for r, d in shapes if d == dim]:
+            a = torch.randn(rows, vocab, device=dev, generator=g).to(torch.bfloat16)
+            o = torch.empty((rows, dim), dtype=torch.bfloat16, device=dev)
+            nb = lib.tm_ce_grad_h_workspace_bytes(rows, vocab, dim)
+            ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+            ms_s = timed(lambda: _native.check(lib.tm_ce_grad_h_bf16(o.data_ptr(), a.data_ptr(), wt.data_ptr(), rows,
+                                                                     vocab, dim, ws.data_ptr(), nb, stream),
+                                               "tm_ce_grad_h_bf16"))
+            ms_l = timed(lambda: torch.matmul(a, w, out=o))
+            fl = 2.0 * rows * vocab * dim
+            out["shapes"]["%dx%d" % (rows, dim)] = {
+                "splitk_ms": round(ms_s, 4), "splitk_TFLOPs": round(fl / ms_s / 1e9, 1),
+                "hipblaslt_ms": round(ms_l, 4), "hipblaslt_TFLOPs": round(fl / ms_l / 1e9, 1),
+                "splits": nb // (rows * dim * 4)}
+            del a, o, ws
+        del w, wt
+    return out
+
+
 def _cpu_topology():
     """(logical CPUs this process may run on, physical cores among them or None)."""
     try:
@@ -775,6 +828,10 @@ def main():
         return
     if args.mode == "ce":  # fused linear CE only (for rocprofv3)
         print(json.dumps(run_fused_ce(args.reps, dev, with_reference=False)), flush=True)
+        return
+    if args.mode == "ce-gemm":
+        shapes = [tuple(int(x) for x in sh.split("x")) for sh in args.gemm_shapes.split(",") if sh]
+        print(json.dumps(run_ce_gemm(shapes, args.reps, dev)), flush=True)
         return
 
     main_res = run_gpu(args.config, args.steps, args.warmup, args.chunk_elems, dev)
