@@ -253,6 +253,20 @@ int tm_ce_rows_loss_bf16(const uint16_t* d_logits, int64_t ld, const int64_t* d_
                          int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream);
 
 /*
+ * The same chunk math on fp32 logits, for fp32 hidden states outside autocast: there the
+ * reference's products are fp32 GEMMs (fused_linear_ce.py:38,52,57, w = weight.to(fp32) at :65)
+ * and its softmax runs on fp32 logits (:39-51). lse = logsumexp(logits), row_loss = lse -
+ * logits[label] (0 on ignored rows, NaN for a label outside [0, vocab)), and
+ * logits <- exp(logits - lse) - onehot(label) in fp32 (0 on ignored rows): the fp32 difference,
+ * then a full-precision exp, as the reference's exp(logits - lse). tm_ce_rows_loss_f32 gives
+ * the same row losses and only reads the logits.
+ */
+int tm_ce_rows_f32(float* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows, int64_t vocab,
+                   int64_t ignore_index, float* d_row_loss, void* stream);
+int tm_ce_rows_loss_f32(const float* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows,
+                        int64_t vocab, int64_t ignore_index, float* d_row_loss, void* stream);
+
+/*
  * Deterministic loss reduction (fused_linear_ce.py:76-90): d_out3[0] = sum of row
  * losses, d_out3[1] = n_valid = max(1, count(label != ignore_index)),
  * d_out3[2] = d_out3[0] / d_out3[1] (the mean loss).

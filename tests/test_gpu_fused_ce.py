@@ -496,8 +496,8 @@ def test_fp32_hidden_under_autocast(chunk):
     (fused_linear_ce.py:68,80,120). With 512 valid rows the scale is a power of two, so both
     scalings are exact and the fp32 path's results follow bit for bit from the bf16 path's on
     hidden.to(bf16): the same loss, the same grad_W, and grad_h widened exactly. Against the
-    reference composition run under autocast the bars of the composition test hold, and fp32
-    hidden without bf16 autocast is refused."""
+    reference composition run under autocast the bars of the composition test hold, and fp16
+    autocast is refused."""
     from torchure_amd.loss import fused_linear_cross_entropy
 
     g = torch.Generator(device=DEV).manual_seed(11)
@@ -547,8 +547,6 @@ def test_fp32_hidden_under_autocast(chunk):
     assert gh_err <= 1e-2 * ref_gh.abs().max().item()
     assert gw_err <= 1e-2 * ref_gw.abs().max().item()
 
-    with pytest.raises(NotImplementedError, match="autocast"):
-        fused_linear_cross_entropy(hidden.clone().requires_grad_(True), weight, labels)
     with pytest.raises(NotImplementedError, match="autocast"), torch.autocast("cuda", dtype=torch.float16):
         fused_linear_cross_entropy(hidden, weight, labels)
     # bf16 hidden under fp16 autocast: autocast would make the logits fp16, so it is refused too
@@ -626,3 +624,110 @@ def test_non_contiguous_inputs_give_the_contiguous_bits():
     assert torch.equal(hbase.grad.t().contiguous().view(torch.int16), h1.grad.view(torch.int16))
     assert torch.equal(wbase.grad[:, ::2].contiguous().view(torch.int32), w1.grad.view(torch.int32))
     assert torch.count_nonzero(wbase.grad[:, 1::2]).item() == 0
+
+
+@pytest.mark.parametrize("vocab", [4096, 1001, 151936])
+def test_ce_rows_f32_kernel_vs_fp64(vocab):
+    """tm_ce_rows_f32 (fp32 logits, the fp32-hidden path outside autocast) against an fp64
+    restatement of fused_linear_ce.py:39-51 on the same fp32 logits: row losses within 1e-6
+    relative; gradients within 2e-6 relative of exp(x - lse), plus the fp32 rounding of lse and
+    of x - lse (2^-23 of their magnitudes), plus 1e-7 absolute at the label (p - 1 cancels);
+    ignored rows exactly zero; tm_ce_rows_loss_f32 gives the same loss bits
+    and leaves the logits untouched. V = 1001 takes the element-wise path (rows not 16-byte
+    aligned), and rows hold -inf entries and a wide range."""
+    from torchure_amd import _native
+
+    g = torch.Generator(device=DEV).manual_seed(vocab)
+    rows = 64
+    x = torch.randn(rows, vocab, device=DEV, generator=g) * 4.0
+    x[3, ::7] = float("-inf")
+    x[5] *= 20.0
+    labels = torch.randint(0, vocab, (rows,), device=DEV, generator=g)
+    labels[::9] = -100
+    labels[3] = 1  # a finite entry of the masked row
+    lib, stream = _native.lib(), _native.stream_handle(DEV)
+    work = x.clone()
+    loss = torch.empty(rows, dtype=torch.float32, device=DEV)
+    _native.check(lib.tm_ce_rows_f32(work.data_ptr(), vocab, labels.data_ptr(), rows, vocab, -100,
+                                     loss.data_ptr(), stream), "tm_ce_rows_f32")
+    ro = x.clone()
+    loss2 = torch.empty(rows, dtype=torch.float32, device=DEV)
+    _native.check(lib.tm_ce_rows_loss_f32(ro.data_ptr(), vocab, labels.data_ptr(), rows, vocab, -100,
+                                          loss2.data_ptr(), stream), "tm_ce_rows_loss_f32")
+    xd = x.double()
+    lse = torch.logsumexp(xd, dim=1)
+    valid = labels != -100
+    picked = xd.gather(1, labels.clamp(min=0)[:, None])[:, 0]
+    want_loss = torch.where(valid, lse - picked, torch.zeros_like(lse))
+    p = torch.exp(xd - lse[:, None])
+    want = p.clone()
+    idx = valid.nonzero()[:, 0]
+    want[idx, labels[idx]] -= 1.0
+    want[~valid] = 0.0
+    torch.cuda.synchronize()
+    assert torch.equal(ro, x)
+    assert torch.equal(loss.view(torch.int32), loss2.view(torch.int32))
+    torch.testing.assert_close(loss.double(), want_loss, rtol=1e-6, atol=1e-6)
+    err = (work.double() - want).abs()
+    # fp32 rounding of lse (half an ulp of |lse|) and of the difference x - lse move the
+    # exponent by up to (|lse| + |x - lse|) * 2^-24 each
+    dist = (xd - lse[:, None]).abs()
+    dist = torch.where(torch.isfinite(dist), dist, torch.zeros_like(dist))  # -inf entries: p = 0 exactly
+    rel = 2e-6 + (lse.abs()[:, None] + dist) * 2.0 ** -23
+    bound = p * rel + 1e-7 * (want != p).double() + 1e-30
+    bound[~valid] = 0.0
+    assert bool((err <= bound).all()), float((err / bound.clamp_min(1e-300)).max())
+    assert bool((work[~valid] == 0).all())
+
+
+@pytest.mark.parametrize("chunk", [None, 300])
+def test_fp32_hidden_without_autocast(chunk):
+    """fp32 hidden states outside autocast: the reference runs fp32 GEMMs on w =
+    weight.to(fp32) (fused_linear_ce.py:38,52,57,65) and returns fp32 gradients. Against the
+    reference composition (the same torch calls) on the same device: loss within 1e-6
+    relative, both gradients within 1e-5 of their scale; against an fp64 unfused cross
+    entropy: loss within 1e-5 relative and gradients within 1e-4 relative L2. The loss-only
+    call gives the training loss bits; a bf16 weight gets its gradient as autograd hands it
+    over (fp32 cast to the weight's dtype), as in the reference."""
+    import torch.nn.functional as F
+
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(23)
+    n, d, v = 1000, 256, 4096
+    hidden = torch.randn(n, d, device=DEV, generator=g)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::37] = -100
+    h1 = hidden.clone().requires_grad_(True)
+    w1 = weight.clone().requires_grad_(True)
+    loss = fused_linear_cross_entropy(h1, w1, labels, -100, chunk)
+    (loss * 2.0).backward()
+    assert loss.dtype == torch.float32 and h1.grad.dtype == torch.float32 and w1.grad.dtype == torch.float32
+    ref_loss, ref_gh, ref_gw = fused_linear_ce_reference(hidden, weight, labels, -100, chunk_size=chunk or n)
+    torch.cuda.synchronize()
+    assert abs(loss.item() - ref_loss.item()) <= 1e-6 * abs(ref_loss.item())
+    assert (h1.grad - 2.0 * ref_gh).abs().max().item() <= 1e-5 * ref_gh.abs().max().item() * 2.0
+    assert (w1.grad - 2.0 * ref_gw).abs().max().item() <= 1e-5 * ref_gw.abs().max().item() * 2.0
+
+    hd = hidden.double().requires_grad_(True)
+    wd = weight.double().requires_grad_(True)
+    ld = F.cross_entropy(hd @ wd.t(), labels, ignore_index=-100)
+    (ld * 2.0).backward()
+
+    def rel(a, b):
+        return float((a.double() - b).norm() / b.norm())
+
+    assert abs(loss.item() - ld.item()) <= 1e-5 * ld.item()
+    assert rel(h1.grad, hd.grad) < 1e-4 and rel(w1.grad, wd.grad) < 1e-4
+
+    with torch.no_grad():
+        ev = fused_linear_cross_entropy(hidden, weight, labels, -100, chunk)
+    assert ev.view(torch.int32).item() == loss.detach().view(torch.int32).item()
+
+    wb = weight.to(torch.bfloat16).requires_grad_(True)
+    h2 = hidden.clone().requires_grad_(True)
+    fused_linear_cross_entropy(h2, wb, labels, -100, chunk).backward()
+    assert wb.grad.dtype == torch.bfloat16 and h2.grad.dtype == torch.float32
+    with pytest.raises(NotImplementedError, match="float16"):
+        fused_linear_cross_entropy(hidden.half().requires_grad_(True), weight, labels)

@@ -96,6 +96,8 @@ _SIGNATURES = {
     "tm_cast_bf16_list": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp]),
     "tm_ce_rows_bf16": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
     "tm_ce_rows_loss_bf16": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "tm_ce_rows_f32": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "tm_ce_rows_loss_f32": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
     "tm_ce_loss": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "tm_ce_scale_grads": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp]),
     "tm_ce_grad_w": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_int, _vp, _vp, _vp]),

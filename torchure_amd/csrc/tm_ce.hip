@@ -54,6 +54,7 @@ constexpr int kRegCols = 20;  // 8-element vectors per thread kept in registers 
 constexpr int kMaxWaves = (kRowThreadsRegs > TM_CE_STREAM_THREADS ? kRowThreadsRegs : TM_CE_STREAM_THREADS) / 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <typename... A>
 int ce_fail(int code, const char* fmt, A... args) {
@@ -396,6 +397,102 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
     row[i] = static_cast<uint16_t>(rne16(g_of(__uint_as_float(static_cast<uint32_t>(row[i]) << 16), i)));
 }
 
+// (max, sum of exp(x - max)) with the full-precision expf, for fp32 outputs.
+__device__ __forceinline__ void ms_merge_f(float& m, float& s, float m2, float s2) {
+  if (m2 == -INFINITY) return;
+  if (m2 > m) {
+    s = s * expf(m - m2) + s2;
+    m = m2;
+  } else if (m2 == m) {
+    s = s + s2;
+  } else {
+    s = s + s2 * expf(m2 - m);
+  }
+}
+
+__device__ __forceinline__ void ms_add_f(float& m, float& s, float x) {
+  if (x == -INFINITY) return;
+  if (x > m) {
+    s = s * expf(m - x) + 1.0f;
+    m = x;
+  } else {
+    s = s + expf(x - m);
+  }
+}
+
+// Block-wide (max, sumexp) of 256-thread workgroups, fixed order, full-precision exp.
+__device__ __forceinline__ void block_ms_f(float& m, float& s) {
+  __shared__ float lm[4], ls[4];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, 64);
+    const float s2 = __shfl_xor(s, off, 64);
+    ms_merge_f(m, s, m2, s2);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    lm[threadIdx.x >> 6] = m;
+    ls[threadIdx.x >> 6] = s;
+  }
+  __syncthreads();
+  m = lm[0];
+  s = ls[0];
+  for (int w = 1; w < 4; ++w) ms_merge_f(m, s, lm[w], ls[w]);
+  __syncthreads();
+}
+
+// fp32 logits: hidden states and weight in fp32 outside autocast, where the reference's
+// products are fp32 GEMMs (fused_linear_ce.py:38,52,57 with w = weight.to(hidden.dtype) at
+// :65) and its chunk math runs on fp32 logits (:39-51). One 256-thread workgroup per row and
+// two reads of it: an online (max, sum of exp) pass, lse = max + log(sum); then (kGrad) the
+// gradient in place, exp(x - lse) on valid rows (0 on ignored rows) minus 1 at the label,
+// with the reference's rounding steps: the fp32 difference x - lse, then a full-precision exp.
+template <bool kGrad>
+__global__ __launch_bounds__(256) void ce_rows_f32_kernel(float* __restrict__ logits, int64_t ld,
+                                                          const int64_t* __restrict__ labels, int64_t vocab,
+                                                          int64_t ignore_index, float* __restrict__ row_loss) {
+  const int64_t r = blockIdx.x;
+  float* row = logits + r * ld;
+  const int64_t label = labels[r];
+  const bool valid = label != ignore_index;
+  const int64_t nvec = vocab >> 2;  // full 4-element vectors (16 B)
+  const bool vec = ((reinterpret_cast<uint64_t>(row) & 15u) == 0);
+  const int64_t vend = vec ? nvec * 4 : 0;
+  float m = -INFINITY, s = 0.0f;
+  if (vec) {
+    float mm[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY}, ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t v = threadIdx.x; v < nvec; v += 256) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(row + v * 4);
+      ms_add_f(mm[0], ss[0], x.x);
+      ms_add_f(mm[1], ss[1], x.y);
+      ms_add_f(mm[2], ss[2], x.z);
+      ms_add_f(mm[3], ss[3], x.w);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ms_merge_f(m, s, mm[j], ss[j]);
+  }
+  for (int64_t i = vend + threadIdx.x; i < vocab; i += 256) ms_add_f(m, s, row[i]);
+  block_ms_f(m, s);
+  const float lse = m + logf(s);
+  const bool in_range = label >= 0 && label < vocab;
+  const float target = (valid && in_range) ? row[label] : 0.0f;
+  __syncthreads();  // the target is read before any write
+  if (threadIdx.x == 0) row_loss[r] = !valid ? 0.0f : (in_range ? lse - target : __builtin_nanf(""));
+  if constexpr (!kGrad) return;
+  auto g_of = [&](float x, int64_t idx) -> float {
+    if (!valid) return 0.0f;
+    const float p = expf(x - lse);
+    return idx == label ? p - 1.0f : p;
+  };
+  if (vec) {
+    for (int64_t v = threadIdx.x; v < nvec; v += 256) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(row + v * 4);
+      const int64_t b = v * 4;
+      *reinterpret_cast<f32x4*>(row + b) = f32x4{g_of(x.x, b), g_of(x.y, b + 1), g_of(x.z, b + 2), g_of(x.w, b + 3)};
+    }
+  }
+  for (int64_t i = vend + threadIdx.x; i < vocab; i += 256) row[i] = g_of(row[i], i);
+}
+
 // Fixed-order sums over rows: loss_sum, n_valid (count of label != ignore), mean.
 __global__ __launch_bounds__(256) void ce_loss_kernel(const float* __restrict__ row_loss,
                                                       const int64_t* __restrict__ labels,
@@ -453,7 +550,6 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(uint16_t* __restrict__ gh
 // cost one pass over the accumulator. Then, with kScale (the backward of the last chunk),
 // acc *= g / n_valid. Each element sees the same fp32 operations in the same order as the
 // reference's `+=` per chunk, then `mul_`.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <bool kAccumulate, bool kScale, bool kTwo>
 __global__ __launch_bounds__(256) void ce_grad_w_kernel(float* __restrict__ acc,
@@ -560,6 +656,25 @@ int ce_rows_launch(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int6
   return TM_OK;
 }
 
+template <bool kGrad>
+int ce_rows_f32_launch(float* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows, int64_t vocab,
+                       int64_t ignore_index, float* d_row_loss, void* stream, const char* who) {
+  if (rows < 0 || vocab <= 0 || ld < vocab)
+    return ce_fail(TM_EINVAL, "%s: bad sizes rows=%lld vocab=%lld ld=%lld", who, (long long)rows,
+                   (long long)vocab, (long long)ld);
+  if (rows == 0) return TM_OK;
+  if (!d_logits || !d_labels || !d_row_loss) return ce_fail(TM_EINVAL, "%s: null pointer", who);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t max_rows = 0xFFFFFFFFll / 256;  // a launch holds fewer than 2^32 work-items
+  for (int64_t r0 = 0; r0 < rows; r0 += max_rows) {
+    const uint32_t nr = static_cast<uint32_t>(rows - r0 < max_rows ? rows - r0 : max_rows);
+    hipLaunchKernelGGL((ce_rows_f32_kernel<kGrad>), dim3(nr), dim3(256), 0, s, d_logits + r0 * ld, ld,
+                       d_labels + r0, vocab, ignore_index, d_row_loss + r0);
+    if (int rc = ce_check_launch(who)) return rc;
+  }
+  return TM_OK;
+}
+
 template <bool kTwo>
 int ce_grad_w_launch(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d_chunk2, int64_t nw,
                      int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream,
@@ -603,6 +718,18 @@ int tm_ce_rows_loss_bf16(const uint16_t* d_logits, int64_t ld, const int64_t* d_
   // the kGrad=false kernels only read the logits
   return ce_rows_launch<false>(const_cast<uint16_t*>(d_logits), ld, d_labels, rows, vocab, ignore_index,
                                d_row_loss, stream, "tm_ce_rows_loss_bf16");
+}
+
+int tm_ce_rows_f32(float* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows, int64_t vocab,
+                   int64_t ignore_index, float* d_row_loss, void* stream) {
+  return ce_rows_f32_launch<true>(d_logits, ld, d_labels, rows, vocab, ignore_index, d_row_loss, stream,
+                                  "tm_ce_rows_f32");
+}
+
+int tm_ce_rows_loss_f32(const float* d_logits, int64_t ld, const int64_t* d_labels, int64_t rows, int64_t vocab,
+                        int64_t ignore_index, float* d_row_loss, void* stream) {
+  return ce_rows_f32_launch<false>(const_cast<float*>(d_logits), ld, d_labels, rows, vocab, ignore_index,
+                                   d_row_loss, stream, "tm_ce_rows_loss_f32");
 }
 
 int tm_ce_loss(const float* d_row_loss, const int64_t* d_labels, int64_t rows, int64_t ignore_index,

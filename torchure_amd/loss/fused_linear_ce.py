@@ -34,12 +34,14 @@ write, so the loss bits are those of the training path. When only one input requ
 gradient, the other's GEMM is skipped. The reference computes both gradients whenever
 the weight requires one (fused_linear_ce.py:63-93) and lets autograd drop them.
 
-Hidden states are bf16, or fp32 inside bf16 CUDA autocast: the trainer's call
-(objectives/autoregressive.py:38-44) passes the final norm's fp32 output, for which the
+Hidden states are bf16 or fp32. fp32 inside bf16 CUDA autocast is the trainer's call
+(objectives/autoregressive.py:38-44): it passes the final norm's fp32 output, for which the
 reference's buffers take fp32 (:65,68) and autocast runs the products on bf16 casts. Here
 hidden is cast to bf16 once (RNE, as autocast does), grad_hidden stays a bf16 GEMM output
 until backward, and tm_ce_widen_scale writes the fp32 gradient float(gh) * grad_out / n_valid
-(the reference's fp32 copy and mul_, :80,120).
+(the reference's fp32 copy and mul_, :80,120). fp32 hidden states outside autocast take the
+reference's fp32 path: fp32 GEMMs on weight.to(fp32), tm_ce_rows_f32 on fp32 logits, and the
+reference's fp32 `+=` and `mul_` for grad_W.
 
 Chunking: 1024 rows by default, the reference's default (:131). ``chunk_size=None`` or
 ``"auto"`` opts into MI355X sizing: chunks whose bf16 logits take up to 4 GiB, so that
@@ -72,7 +74,9 @@ def _fp32_hidden_under_autocast(hidden) -> bool:
 
 
 def _checked(hidden, weight, labels, chunk_size):
-    """Argument checks shared by both paths; returns (n, v, chunk rows, fp32 hidden)."""
+    """Argument checks shared by all paths; returns (n, v, chunk rows, mode): "bf16" (bf16
+    hidden), "autocast" (fp32 hidden inside bf16 autocast: bf16 products) or "fp32" (fp32 hidden
+    outside autocast: fp32 products, as the reference's with w = weight.to(fp32))."""
     who = "fused_linear_cross_entropy"
     for t, what in ((hidden, "hidden"), (labels, "labels")):  # made contiguous by the caller
         tables.require_device_tensor(t, who, what)
@@ -85,11 +89,16 @@ def _checked(hidden, weight, labels, chunk_size):
         raise NotImplementedError(
             f"{who}: CUDA autocast with {torch.get_autocast_dtype('cuda')} is not supported; the "
             "products run as bf16 GEMMs (bf16 autocast, or none)")
-    fp32 = _fp32_hidden_under_autocast(hidden)
-    if hidden.dtype != torch.bfloat16 and not fp32:
+    if _fp32_hidden_under_autocast(hidden):
+        mode = "autocast"
+    elif hidden.dtype == torch.float32 and not torch.is_autocast_enabled("cuda"):
+        mode = "fp32"
+    elif hidden.dtype == torch.bfloat16:
+        mode = "bf16"
+    else:
         raise NotImplementedError(
-            f"{who}: hidden must be bfloat16, or float32 inside bf16 CUDA autocast (got {hidden.dtype}, "
-            "autocast " + ("on" if torch.is_autocast_enabled("cuda") else "off") + "); the products run as bf16 GEMMs")
+            f"{who}: hidden must be bfloat16, or float32 (inside bf16 CUDA autocast or outside autocast), "
+            f"got {hidden.dtype} with autocast " + ("on" if torch.is_autocast_enabled("cuda") else "off"))
     if labels.dtype != torch.int64:
         raise RuntimeError(f"{who}: labels must be int64")
     n, d = hidden.shape
@@ -105,14 +114,14 @@ def _checked(hidden, weight, labels, chunk_size):
     chunk = auto_chunk_rows(n, v) if auto else int(chunk_size)
     if chunk < 1:
         raise ValueError(f"{who}: chunk_size must be positive, got {chunk_size}")
-    return n, v, chunk, fp32
+    return n, v, chunk, mode
 
 
-def _bf16(logits: torch.Tensor) -> torch.Tensor:
-    """The row kernels read bf16 bits: refuse anything else loudly."""
-    if logits.dtype != torch.bfloat16 or not logits.is_contiguous():
+def _bf16(logits: torch.Tensor, dtype=torch.bfloat16) -> torch.Tensor:
+    """The row kernels read bf16 bits (fp32 on the fp32 path): refuse anything else loudly."""
+    if logits.dtype != dtype or not logits.is_contiguous():
         raise RuntimeError(f"fused_linear_cross_entropy: the logits GEMM returned {logits.dtype} "
-                           f"(contiguous: {logits.is_contiguous()}), the row kernels need contiguous bf16")
+                           f"(contiguous: {logits.is_contiguous()}), the row kernels need contiguous {dtype}")
     return logits
 
 
@@ -173,26 +182,62 @@ def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
     same logits GEMM and the same per-row arithmetic as the training path, so the same
     bits, without the two gradient GEMMs or the gradient write. The reference's forward
     computes and drops the gradients in this case (fused_linear_ce.py:63-93)."""
-    n, v, chunk, fp32 = _checked(hidden, weight, labels, chunk_size)
+    n, v, chunk, mode = _checked(hidden, weight, labels, chunk_size)
     lib = _native.lib()
     stream = _native.stream_handle(hidden.device)
-    hb = hidden.to(torch.bfloat16) if fp32 else hidden  # autocast's cast (RNE)
-    w = weight.to(torch.bfloat16).contiguous()
+    dt = torch.float32 if mode == "fp32" else torch.bfloat16
+    hb = hidden.to(torch.bfloat16) if mode == "autocast" else hidden  # autocast's cast (RNE)
+    w = weight.to(dt).contiguous()
+    rows_loss = lib.tm_ce_rows_loss_f32 if mode == "fp32" else lib.tm_ce_rows_loss_bf16
     row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
     for s in range(0, n, chunk):
         e = min(s + chunk, n)
-        logits = _bf16(torch.matmul(hb[s:e], w.t()))
-        _native.check(lib.tm_ce_rows_loss_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
-                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
-                      "tm_ce_rows_loss_bf16")
+        logits = _bf16(torch.matmul(hb[s:e], w.t()), dt)
+        _native.check(rows_loss(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, int(ignore_index),
+                                row_loss[s:].data_ptr(), stream), "tm_ce_rows_loss")
         del logits
     return _mean_loss(row_loss, labels, n, ignore_index, lib, stream)[0]
+
+
+def _fp32_forward(ctx, hidden, weight, labels, ignore_index, n, v, chunk):
+    """fp32 hidden states outside autocast. The reference then casts the weight to fp32 once
+    (fused_linear_ce.py:65), its three products are fp32 GEMMs and its buffers are fp32
+    (:66-72). This path does the same: per chunk, fp32 logits from torch.matmul, tm_ce_rows_f32
+    in place (the chunk math of :39-51 on fp32 logits), grad_h = grad_logits @ w into the fp32
+    grad_hidden (:52,79), and grad_weight += grad_logits^T @ h into a zero-filled fp32 buffer
+    (:57,80-81), the reference's own fp32 `+=`. Backward scales both in place."""
+    lib = _native.lib()
+    stream = _native.stream_handle(hidden.device)
+    w = weight.to(torch.float32).contiguous()
+    want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    grad_hidden = torch.empty(hidden.shape, dtype=torch.float32, device=hidden.device) if want_h else None
+    grad_weight = torch.zeros(weight.shape, dtype=torch.float32, device=weight.device) if want_w else None
+    row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
+    for s in range(0, n, chunk):
+        e = min(s + chunk, n)
+        h = hidden[s:e]
+        logits = _bf16(torch.matmul(h, w.t()), torch.float32)  # (C, V) fp32
+        _native.check(lib.tm_ce_rows_f32(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
+                                         int(ignore_index), row_loss[s:].data_ptr(), stream), "tm_ce_rows_f32")
+        if want_h:
+            torch.matmul(logits, w, out=grad_hidden[s:e])
+        if want_w:
+            grad_weight += torch.matmul(logits.t(), h)
+        del logits
+    loss, ctx.n_valid = _mean_loss(row_loss, labels, n, ignore_index, lib, stream)
+    ctx.grad_hidden = grad_hidden
+    ctx.grad_weight = grad_weight
+    ctx.fp32_path = True
+    return loss
 
 
 class _FusedLinearCE(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, labels, ignore_index, chunk_size):
-        n, v, chunk, fp32 = _checked(hidden, weight, labels, chunk_size)
+        n, v, chunk, mode = _checked(hidden, weight, labels, chunk_size)
+        if mode == "fp32":
+            return _fp32_forward(ctx, hidden, weight, labels, ignore_index, n, v, chunk)
+        fp32 = mode == "autocast"
         lib = _native.lib()
         stream = _native.stream_handle(hidden.device)
         hb = hidden.to(torch.bfloat16) if fp32 else hidden  # autocast's cast (RNE)
@@ -236,6 +281,7 @@ class _FusedLinearCE(torch.autograd.Function):
         loss, ctx.n_valid = _mean_loss(row_loss, labels, n, ignore_index, lib, stream)
         ctx.grad_hidden = grad_hidden
         ctx.fp32_hidden = fp32
+        ctx.fp32_path = False
         ctx.want_w = want_w
         ctx.grad_weight = grad_weight
         ctx.pending_gw = pending
@@ -251,6 +297,15 @@ class _FusedLinearCE(torch.autograd.Function):
                 "fused_linear_cross_entropy: backward called twice. the stashed grads are "
                 "consumed in place on the first call, so retain_graph does not work through this op")
         grad_hidden, grad_weight, n_valid = ctx.grad_hidden, ctx.grad_weight, ctx.n_valid
+        if ctx.fp32_path:
+            ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = None
+            # fused_linear_ce.py:107-126: scale = grad_out / n_valid, both buffers scaled in place
+            scale = grad_out.detach().to(torch.float32) / n_valid[0]
+            if grad_hidden is not None:
+                grad_hidden.mul_(scale)
+            if grad_weight is not None:
+                grad_weight.mul_(scale)
+            return grad_hidden, grad_weight, None, None, None
         last_gw, pending = ctx.last_gw, ctx.pending_gw
         ctx.grad_hidden = ctx.grad_weight = ctx.n_valid = ctx.last_gw = ctx.pending_gw = None
         lib = _native.lib()
@@ -294,7 +349,7 @@ class _FusedLinearCE(torch.autograd.Function):
 
 
 def fused_linear_cross_entropy(
-    hidden: torch.Tensor,  # (B, S, D) or (N, D), bf16 (fp32 inside bf16 autocast)
+    hidden: torch.Tensor,  # (B, S, D) or (N, D), bf16 or fp32
     weight: torch.Tensor,  # (V, D) lm_head weight
     labels: torch.Tensor,  # (B, S) or (N,), already shifted, int64
     ignore_index: int = -100,
