@@ -227,8 +227,32 @@ int64_t splits_for(int64_t rows, int64_t vocab, int64_t dim) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-std::once_flag g_lds_once;
-hipError_t g_lds_status = hipSuccess;
+// The kernel's 128 KB of dynamic LDS exceeds the 64 KB default: the attribute is set once per
+// device, with that device current, before the first launch there.
+constexpr int kMaxDevices = 64;
+std::mutex g_lds_mu;
+bool g_lds_set[kMaxDevices] = {};
+
+hipError_t allow_lds(hipStream_t stream) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_lds_mu);
+  if (g_lds_set[dev]) return hipSuccess;
+  int cur = -1;
+  e = hipGetDevice(&cur);
+  if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(grad_h_gemm_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+  if (cur >= 0 && cur != dev) {
+    const hipError_t back = hipSetDevice(cur);
+    if (e == hipSuccess) e = back;
+  }
+  if (e == hipSuccess) g_lds_set[dev] = true;
+  return e;
+}
 
 }  // namespace
 
@@ -255,17 +279,14 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
   if (ws_bytes < tm_ce_grad_h_workspace_bytes(rows, vocab, dim))
     return gemm_fail(TM_EINVAL, "tm_ce_grad_h_bf16: workspace of %zu bytes, %zu needed", ws_bytes,
                      tm_ce_grad_h_workspace_bytes(rows, vocab, dim));
-  std::call_once(g_lds_once, [] {
-    g_lds_status = hipFuncSetAttribute(reinterpret_cast<const void*>(grad_h_gemm_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
-  });
-  if (g_lds_status != hipSuccess)
-    return gemm_fail(TM_ELAUNCH, "tm_ce_grad_h_bf16: LDS attribute: %s", hipGetErrorString(g_lds_status));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t lds = allow_lds(s);
+  if (lds != hipSuccess)
+    return gemm_fail(TM_ELAUNCH, "tm_ce_grad_h_bf16: LDS attribute: %s", hipGetErrorString(lds));
   const int64_t splits = splits_for(rows, vocab, dim);
   const int64_t tiles = (rows / kTile) * (dim / kTile);
   const int64_t total_iters = vocab / kSliceK;
   const int64_t per = (total_iters + splits - 1) / splits;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   float* partials = static_cast<float*>(d_ws);
   hipLaunchKernelGGL(grad_h_gemm_kernel, dim3(static_cast<uint32_t>(tiles * splits)), dim3(kGemmThreads),
                      kGemmLds, s, d_grad_logits, d_wt, partials, static_cast<int>(rows), static_cast<int>(dim),
