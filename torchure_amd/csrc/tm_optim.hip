@@ -169,15 +169,18 @@ __device__ __forceinline__ bool aligned8(uint64_t a) { return (a & 7u) == 0; }
 // ran at 6.6-7.2 TB/s instead of 5.2-5.7, and a copy at 6.5 TB/s instead of 5.1.
 constexpr int kWave = 64;
 constexpr int kSlice = kWave * 4;
-// Dynamic LDS requested by every one-wave streaming launch, and used by none of them: it caps
-// a CU at 12 resident workgroups of these kernels (12 x 13,312 B of gfx950's 160 KB; 13 would
-// need 173,056 B, also with 512- or 1024-byte allocation granules), i.e. 3 waves per SIMD
-// instead of as many as the wave slots hold (their 47 VGPRs do not limit them). Fewer waves
-// in flight means fewer concurrent requests queued at the memory side. The 4B update (28 B/param) then runs 6.39-6.46 TB/s
-// on the process's first allocation and on a second one, against 5.65 and 6.07 TB/s uncapped
-// (0.6B: 6.41-6.43 against 5.96-5.99). Measured caps: 11-14 workgroups per CU within 3%, 10 and
-// fewer slower (8: 5.8 TB/s, 5: 3.4).
-constexpr int kSliceLds = 13312;
+// Dynamic LDS that the update launch requests and never uses. It caps a CU at 12
+// resident update workgroups (12 x 13,312 B of gfx950's 160 KB; 13 would need 173,056 B, also
+// with 512- or 1024-byte allocation granules), i.e. 3 waves per SIMD instead of as many as
+// the wave slots hold (its 47 VGPRs do not limit them). Each update wave keeps eight 1 KB or
+// 512 B streams in flight (28 B per element); with fewer such waves, fewer requests queue at
+// the memory side. The 4B update then runs 6.39-6.46 TB/s on the process's first allocation
+// and on a second one, against 5.65 and 6.07 TB/s uncapped (0.6B: 6.41-6.43 against
+// 5.96-5.99). Caps of 11-14 workgroups per CU were within 3%; 10 and fewer were slower (8: 5.8
+// TB/s, 5: 3.4). The lighter streams run uncapped. They move 4-10 B per element per wave (the
+// eager scale, the cast, the accumulation), and the same cap halved their rates: the 4B cast
+// 6.5 -> 3.3 TB/s, the accumulation 6.7 -> 4.3, the scale 4.7 -> 2.2.
+constexpr int kUpdateLds = 13312;
 // A launch holds fewer than 2^32 work-items: at most this many one-wave workgroups.
 constexpr int64_t kMaxSliceBlocks = 0xFFFFFFFFll / kWave;
 
@@ -805,7 +808,7 @@ int launch_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_
   // d_coef == NULL: TM_FLAG_CLIP is ignored (every grad is used unscaled).
   return launch_chunk_slices(n_chunks, chunk_elems, "adamw_update_kernel",
                              [&](uint32_t first, uint32_t spc, dim3 grid) {
-                               hipLaunchKernelGGL(adamw_update_kernel, grid, dim3(kWave), kSliceLds, s, d_tensors,
+                               hipLaunchKernelGGL(adamw_update_kernel, grid, dim3(kWave), kUpdateLds, s, d_tensors,
                                                   n_tensors, d_chunks, first, spc, chunk_elems, scal,
                                                   d_coef);
                              });
@@ -935,7 +938,7 @@ int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
   hipStream_t s = static_cast<hipStream_t>(stream);
   return launch_chunk_slices(n_chunks, chunk_elems, "grad_scale_kernel",
                              [&](uint32_t first, uint32_t spc, dim3 grid) {
-                               hipLaunchKernelGGL(grad_scale_kernel, grid, dim3(kWave), kSliceLds, s, d_tensors,
+                               hipLaunchKernelGGL(grad_scale_kernel, grid, dim3(kWave), 0, s, d_tensors,
                                                   n_tensors, d_chunks, first, spc, chunk_elems, d_coef);
                              });
 }
@@ -988,7 +991,7 @@ int tm_grad_accumulate_list(const tm_accum_t* d_list, int64_t n_list, const tm_c
   }
   return launch_chunk_slices(n_chunks, chunk_elems, "accumulate_list_kernel",
                              [&](uint32_t first, uint32_t spc, dim3 grid) {
-                               hipLaunchKernelGGL(accumulate_list_kernel, grid, dim3(kWave), kSliceLds, s, d_list,
+                               hipLaunchKernelGGL(accumulate_list_kernel, grid, dim3(kWave), 0, s, d_list,
                                                   n_list, d_chunks, first, spc, chunk_elems);
                              });
 }
@@ -1006,7 +1009,7 @@ int tm_grad_accumulate_bf16(float* d_acc, const uint16_t* d_micro, int64_t numel
   if (!d_acc || !d_micro) return fail(TM_EINVAL, "tm_grad_accumulate_bf16: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   return launch_slices((numel + kSlice - 1) / kSlice, "accumulate_kernel", [&](int64_t first, dim3 grid) {
-    hipLaunchKernelGGL(accumulate_kernel, grid, dim3(kWave), kSliceLds, s, d_acc, d_micro, numel, first);
+    hipLaunchKernelGGL(accumulate_kernel, grid, dim3(kWave), 0, s, d_acc, d_micro, numel, first);
   });
 }
 
@@ -1016,7 +1019,7 @@ int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* strea
   if (!d_dst || !d_src) return fail(TM_EINVAL, "tm_cast_bf16: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
   return launch_slices((numel + kSlice - 1) / kSlice, "cast_bf16_kernel", [&](int64_t first, dim3 grid) {
-    hipLaunchKernelGGL(cast_bf16_kernel, grid, dim3(kWave), kSliceLds, s, d_dst, d_src, numel, first);
+    hipLaunchKernelGGL(cast_bf16_kernel, grid, dim3(kWave), 0, s, d_dst, d_src, numel, first);
   });
 }
 
@@ -1027,7 +1030,7 @@ int tm_cast_bf16_list(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_
   hipStream_t s = static_cast<hipStream_t>(stream);
   return launch_chunk_slices(n_chunks, chunk_elems, "cast_bf16_list_kernel",
                              [&](uint32_t first, uint32_t spc, dim3 grid) {
-                               hipLaunchKernelGGL(cast_bf16_list_kernel, grid, dim3(kWave), kSliceLds, s, d_tensors,
+                               hipLaunchKernelGGL(cast_bf16_list_kernel, grid, dim3(kWave), 0, s, d_tensors,
                                                   n_tensors, d_chunks, first, spc, chunk_elems);
                              });
 }
