@@ -169,3 +169,39 @@ def test_op_grad_h_uses_the_gemm_on_eligible_chunks(chunk):
     assert abs(loss.item() - ref_loss.item()) <= 1e-5 * abs(ref_loss.item())
     assert (h1.grad.float() - ref_gh.float()).abs().max().item() <= 1e-2 * ref_gh.float().abs().max().item()
     assert (w1.grad - ref_gw).abs().max().item() <= 1e-2 * ref_gw.abs().max().item()
+
+
+def test_op_mixes_the_gemm_and_the_library_on_ragged_chunks():
+    """2600 rows in 1024-row chunks (D 256, V 4096): the two full chunks take the split-K
+    GEMM and the 552-row tail torch.matmul, each bit for bit, within one call."""
+    from torchure_amd import _native
+    from torchure_amd.loss import fused_linear_cross_entropy
+    from torchure_amd.loss.fused_linear_ce import splitk_grad_h_fits
+
+    g = torch.Generator(device=DEV).manual_seed(41)
+    n, d, v, chunk = 2600, 256, 4096, 1024
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::23] = -100
+    h1 = hidden.clone().requires_grad_(True)
+    fused_linear_cross_entropy(h1, weight, labels, -100, chunk).backward()
+
+    lib, stream = _native.lib(), _native.stream_handle(DEV)
+    w = weight.to(torch.bfloat16)
+    want = torch.empty_like(hidden)
+    row_loss = torch.empty(n, dtype=torch.float32, device=DEV)
+    kinds = []
+    for s in range(0, n, chunk):
+        e = min(s + chunk, n)
+        logits = torch.matmul(hidden[s:e], w.t())
+        _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, -100,
+                                          row_loss[s:].data_ptr(), stream), "tm_ce_rows_bf16")
+        fits = splitk_grad_h_fits(e - s, d, v)
+        kinds.append(fits)
+        want[s:e] = _grad_h(logits, w) if fits else torch.matmul(logits, w)
+    assert kinds == [True, True, False]
+    n_valid = (labels != -100).sum().clamp_min(1)
+    want.mul_((torch.tensor(1.0, device=DEV) / n_valid).to(torch.bfloat16))
+    torch.cuda.synchronize()
+    assert torch.equal(h1.grad.view(torch.int16), want.view(torch.int16))
