@@ -304,6 +304,17 @@ int tm_ce_grad_w2(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d_ch
                   int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream);
 
 /*
+ * The same hand-over for n_chunks (1 to 8) consecutive chunks in one pass
+ * (fused_linear_ce.py:80-81 run for each of them in order, and :126 when d_grad_out is given):
+ *   d_grad_w[i] = (((accumulate ? d_grad_w[i] : +0.0f) + float(c0[i])) + float(c1[i]) + ...) [* scale]
+ * h_chunks is a host array of n_chunks device pointers (bf16, nw elements each), read at the
+ * call. The reference's fp32 additions in its order: the bits of one `+=` per chunk, for one
+ * read and one write of the fp32 accumulator per n_chunks chunks.
+ */
+int tm_ce_grad_w_fold(float* d_grad_w, const uint16_t* const* h_chunks, int n_chunks, int64_t nw, int accumulate,
+                      const float* d_grad_out, const float* d_n_valid, void* stream);
+
+/*
  * grad_hidden of fp32 hidden states (fused_linear_ce.py:68,80,120 under autocast: the
  * buffer has the hidden states' dtype, holds the widened bf16 GEMM result and is scaled
  * in place in fp32): d_dst[i] = float(d_src[i]) * (*d_grad_out / *d_n_valid), -0 kept.

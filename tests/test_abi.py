@@ -127,6 +127,22 @@ def test_grad_h_gemm_workspace_and_shape_checks_without_gpu():
     assert lib.tm_ce_transpose_bf16(fake, ctypes.c_void_p(0x1002), 64, 64, None) < 0
 
 
+def test_grad_w_fold_argument_checks_without_gpu():
+    """tm_ce_grad_w_fold takes 1 to 8 chunks, all non-null, and grad_out / n_valid both or
+    neither; the checks run before any HIP call."""
+    lib = _native.lib()
+    fake = ctypes.c_void_p(0x1000)
+    ptrs = (ctypes.c_void_p * 9)(*([0x1000] * 9))
+    for k in (0, 9):
+        assert lib.tm_ce_grad_w_fold(fake, ptrs, k, 100, 0, None, None, None) < 0
+        assert b"chunks" in lib.tm_last_error()
+    assert lib.tm_ce_grad_w_fold(fake, None, 2, 100, 0, None, None, None) < 0
+    holes = (ctypes.c_void_p * 2)(0x1000, None)
+    assert lib.tm_ce_grad_w_fold(fake, holes, 2, 100, 0, None, None, None) < 0
+    assert b"null chunk 1" in lib.tm_last_error()
+    assert lib.tm_ce_grad_w_fold(fake, ptrs, 2, 100, 0, fake, None, None) < 0
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_native, "_LIB", None)
     monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "missing.so"))

@@ -240,10 +240,55 @@ def test_ce_grad_w2_handover_bit_exact(accumulate, scaled, n, offset):
     assert np.array_equal(a, b), np.argwhere(a != b)[:5]
 
 
-@pytest.mark.parametrize("chunk", [700, 350, 256, 175, 100])
+@pytest.mark.parametrize("k,accumulate,scaled,n,offset", [
+    (1, 0, 1, 4096, 0), (3, 1, 0, 4096, 0), (5, 0, 0, 1003, 0), (8, 1, 1, 4096, 0),
+    (8, 0, 1, 2050, 1), (7, 1, 1, 777, 3)])
+def test_ce_grad_w_fold_bit_exact(k, accumulate, scaled, n, offset):
+    """tm_ce_grad_w_fold (k chunks in one pass) vs the reference's torch ops on the same data:
+    `grad_weight += gw` once per chunk in order, on a zero-filled (or given) fp32 buffer, then
+    `mul_(grad_out / n_valid)` (fused_linear_ce.py:80-81,126), bit for bit, with -0, +-inf, NaN
+    and subnormal bf16 inputs, odd sizes and buffers that are not 16-byte aligned."""
+    import ctypes
+
+    from torchure_amd import _native
+
+    r = H.rng(5 * n + 13 * offset + 17 * k + accumulate)
+    bits = []
+    for j in range(k):
+        b = oracle.bf16_rne((r.standard_normal(n + offset) * 0.3).astype(np.float32))
+        b[offset + 2 * j:offset + 2 * j + 6] = [0x8000, 0x0000, 0x7F80, 0xFF80, 0x7FC0, 0x0001]
+        bits.append(torch.from_numpy(b.view(np.int16).copy()).to(DEV)[offset:])
+    acc0 = torch.from_numpy((r.standard_normal(n + offset) * 0.1).astype(np.float32)).to(DEV)[offset:]
+    acc0[0] = acc0[20] = -0.0
+    grad_out = torch.tensor([0.37], dtype=torch.float32, device=DEV)
+    n_valid = torch.tensor([977.0], dtype=torch.float32, device=DEV)
+
+    want = acc0.clone() if accumulate else torch.zeros(n, dtype=torch.float32, device=DEV)
+    for b in bits:
+        want += b.view(torch.bfloat16).float()
+    if scaled:
+        want.mul_(grad_out[0] / n_valid[0])
+
+    got_base = torch.full((n + offset,), 123.0, dtype=torch.float32, device=DEV)
+    got = got_base[offset:]
+    if accumulate:
+        got.copy_(acc0)
+    ptrs = (ctypes.c_void_p * k)(*[b.data_ptr() for b in bits])
+    rc = _native.lib().tm_ce_grad_w_fold(got.data_ptr(), ptrs, k, n, accumulate,
+                                         grad_out.data_ptr() if scaled else None,
+                                         n_valid.data_ptr() if scaled else None, _native.stream_handle(DEV))
+    _native.check(rc, "tm_ce_grad_w_fold")
+    torch.cuda.synchronize()
+    a = got.cpu().numpy().view(np.uint32)
+    w = want.cpu().numpy().view(np.uint32)
+    assert np.array_equal(a, w), np.argwhere(a != w)[:5]
+
+
+@pytest.mark.parametrize("chunk", [700, 350, 256, 175, 100, 80, 40])
 def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops(chunk):
-    """Pairing the chunks' hand-overs and deferring the last chunk change nothing: grad_W of
-    the op with 1, 2, 3, 4 and 7 chunks equals, bit for bit, the reference's chunk loop run
+    """Folding the chunks' hand-overs and deferring the last chunk change nothing: grad_W of
+    the op with 1, 2, 3, 4, 7, 9 and 18 chunks (folds of 8 in forward, the rest with the last
+    in backward) equals, bit for bit, the reference's chunk loop run
     on the same kernels -- zero buffer, `+=` of each chunk's bf16 grad_W, then
     `mul_(grad_out / n_valid)` (fused_linear_ce.py:67-91,117-126) -- and grad_h likewise
     (`grad_hidden[s:e] = gh`, then `mul_(scale.to(bf16))`)."""

@@ -102,6 +102,7 @@ _SIGNATURES = {
     "tm_ce_scale_grads": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp]),
     "tm_ce_grad_w": (ctypes.c_int, [_vp, _vp, _i64, ctypes.c_int, _vp, _vp, _vp]),
     "tm_ce_grad_w2": (ctypes.c_int, [_vp, _vp, _vp, _i64, ctypes.c_int, _vp, _vp, _vp]),
+    "tm_ce_grad_w_fold": (ctypes.c_int, [_vp, _vp, ctypes.c_int, _i64, ctypes.c_int, _vp, _vp, _vp]),
     "tm_ce_widen_scale": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp]),
     "tm_ce_grad_h_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "tm_ce_grad_h_bf16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp]),

@@ -595,6 +595,61 @@ __global__ __launch_bounds__(256) void ce_grad_w_kernel(float* __restrict__ acc,
   }
 }
 
+// grad_W hand-over of up to kMaxFold chunks in one pass (fused_linear_ce.py:80-81 for each of
+// them in order, and :126 with kScale): acc = ((((kAccumulate ? acc : +0) + float(c[0])) +
+// float(c[1])) + ...) [* g / n_valid]. The reference's fp32 additions in its order, so the bits
+// of one `+=` per chunk, for one read and one write of the fp32 accumulator per n chunks.
+constexpr int kMaxFold = 8;
+struct FoldChunks {
+  const uint16_t* p[kMaxFold];
+};
+
+template <bool kAccumulate, bool kScale>
+__global__ __launch_bounds__(256) void ce_grad_w_fold_kernel(float* __restrict__ acc, FoldChunks ch, int n,
+                                                             int64_t nw, const float* __restrict__ grad_out,
+                                                             const float* __restrict__ n_valid) {
+  const float scale = kScale ? *grad_out / *n_valid : 1.0f;
+  uint64_t addr_bits = reinterpret_cast<uint64_t>(acc);
+#pragma unroll
+  for (int c = 0; c < kMaxFold; ++c)
+    if (c < n) addr_bits |= reinterpret_cast<uint64_t>(ch.p[c]);
+  const bool vec = (addr_bits & 15u) == 0;
+  const int64_t vend = vec ? (nw & ~int64_t(7)) : 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * 8;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8; i < vend; i += stride) {
+    u32x4 w[kMaxFold];
+#pragma unroll
+    for (int c = 0; c < kMaxFold; ++c)
+      if (c < n) w[c] = *reinterpret_cast<const u32x4*>(ch.p[c] + i);
+    f32x4 a = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 b = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i + 4) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < kMaxFold; ++c) {
+      if (c < n) {
+        a.x = a.x + lo16(w[c].x); a.y = a.y + hi16(w[c].x);
+        a.z = a.z + lo16(w[c].y); a.w = a.w + hi16(w[c].y);
+        b.x = b.x + lo16(w[c].z); b.y = b.y + hi16(w[c].z);
+        b.z = b.z + lo16(w[c].w); b.w = b.w + hi16(w[c].w);
+      }
+    }
+    if (kScale) {
+      a.x = a.x * scale; a.y = a.y * scale; a.z = a.z * scale; a.w = a.w * scale;
+      b.x = b.x * scale; b.y = b.y * scale; b.z = b.z * scale; b.w = b.w * scale;
+    }
+    *reinterpret_cast<f32x4*>(acc + i) = a;
+    *reinterpret_cast<f32x4*>(acc + i + 4) = b;
+  }
+  for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < nw;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    float x = kAccumulate ? acc[i] : 0.0f;
+#pragma unroll
+    for (int c = 0; c < kMaxFold; ++c)
+      if (c < n) x = x + __uint_as_float(static_cast<uint32_t>(ch.p[c][i]) << 16);
+    if (kScale) x = x * scale;
+    acc[i] = x;
+  }
+}
+
 // Backward of fp32 hidden states, fused_linear_ce.py:68,80,120: the reference keeps grad_hidden
 // in the hidden states' dtype, so under autocast its fp32 buffer holds the widened bf16 GEMM
 // result (`grad_hidden[s:e] = gh`, -0 kept) and is scaled in fp32 (`mul_(scale)`):
@@ -703,6 +758,39 @@ int ce_grad_w_launch(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d
   return ce_check_launch("ce_grad_w_kernel");
 }
 
+int ce_grad_w_fold_launch(float* d_grad_w, const uint16_t* const* h_chunks, int n_chunks, int64_t nw,
+                          int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream) {
+  const char* who = "tm_ce_grad_w_fold";
+  if (nw < 0 || n_chunks < 1 || n_chunks > kMaxFold)
+    return ce_fail(TM_EINVAL, "%s: %d chunks (1 to %d) of %lld elements", who, n_chunks, kMaxFold, (long long)nw);
+  if (!h_chunks || !d_grad_w || (d_grad_out != nullptr) != (d_n_valid != nullptr))
+    return ce_fail(TM_EINVAL, "%s: null pointer", who);
+  FoldChunks ch = {};
+  for (int c = 0; c < n_chunks; ++c) {
+    if (!h_chunks[c]) return ce_fail(TM_EINVAL, "%s: null chunk %d", who, c);
+    ch.p[c] = h_chunks[c];
+  }
+  if (nw == 0) return TM_OK;
+  int64_t blocks = (nw + 256 * 8 - 1) / (256 * 8);
+  if (blocks > 65536) blocks = 65536;
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool scale = d_grad_out != nullptr;
+  if (accumulate && scale)
+    hipLaunchKernelGGL((ce_grad_w_fold_kernel<true, true>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                       d_grad_out, d_n_valid);
+  else if (accumulate)
+    hipLaunchKernelGGL((ce_grad_w_fold_kernel<true, false>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                       d_grad_out, d_n_valid);
+  else if (scale)
+    hipLaunchKernelGGL((ce_grad_w_fold_kernel<false, true>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                       d_grad_out, d_n_valid);
+  else
+    hipLaunchKernelGGL((ce_grad_w_fold_kernel<false, false>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                       d_grad_out, d_n_valid);
+  return ce_check_launch("ce_grad_w_fold_kernel");
+}
+
 }  // namespace
 
 extern "C" {
@@ -767,6 +855,11 @@ int tm_ce_grad_w2(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d_ch
                   int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream) {
   return ce_grad_w_launch<true>(d_grad_w, d_chunk, d_chunk2, nw, accumulate, d_grad_out, d_n_valid, stream,
                                 "tm_ce_grad_w2");
+}
+
+int tm_ce_grad_w_fold(float* d_grad_w, const uint16_t* const* h_chunks, int n_chunks, int64_t nw, int accumulate,
+                      const float* d_grad_out, const float* d_n_valid, void* stream) {
+  return ce_grad_w_fold_launch(d_grad_w, h_chunks, n_chunks, nw, accumulate, d_grad_out, d_n_valid, stream);
 }
 
 int tm_ce_widen_scale(float* d_dst, const uint16_t* d_src, int64_t n, const float* d_grad_out,

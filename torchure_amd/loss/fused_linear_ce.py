@@ -52,6 +52,8 @@ for every pair of 1024-row chunks, and the GEMMs get large M.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from torchure_amd import _native
@@ -145,6 +147,21 @@ def splitk_grad_h_fits(rows: int, dim: int, vocab: int) -> bool:
     at 1.3 PFLOP/s where this one reaches 1.05."""
     return (rows > 0 and dim > 0 and rows % 256 == 0 and dim % 256 == 0 and dim <= 65536
             and (rows // 256) * (dim // 256) <= SPLITK_GRAD_H_MAX_TILES and vocab > 0 and vocab % 64 == 0)
+
+
+FOLD_CHUNKS = 8  # chunks per grad_W fold (tm_ce_grad_w_fold takes at most 8)
+FOLD_BYTES = 4 << 30  # bf16 chunk grad_W held before a fold, at most
+
+
+def _fold(lib, grad_weight, chunks, accumulated, g, n_valid, stream) -> None:
+    """grad_weight = ((grad_weight or +0) + float(c0) + float(c1) + ...) [* g / n_valid], the
+    reference's `grad_weight += gw` per chunk in order (fused_linear_ce.py:80-81) and, with g,
+    its backward `mul_` (:126), in one pass over the fp32 buffer."""
+    ptrs = (ctypes.c_void_p * len(chunks))(*[c.data_ptr() for c in chunks])
+    _native.check(lib.tm_ce_grad_w_fold(grad_weight.data_ptr(), ptrs, len(chunks), chunks[0].numel(),
+                                        int(accumulated), g.data_ptr() if g is not None else None,
+                                        n_valid.data_ptr() if n_valid is not None else None, stream),
+                  "tm_ce_grad_w_fold")
 
 
 class GradHidden:
@@ -245,10 +262,10 @@ class _FusedLinearCE(torch.autograd.Function):
         want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         # bf16 GEMM output either way; for fp32 hidden it is widened and scaled in backward
         grad_hidden = torch.empty(hidden.shape, dtype=torch.bfloat16, device=hidden.device) if want_h else None
-        # Chunks' bf16 grad_W are added to the fp32 grad_W two at a time (one pass for each
-        # pair); the last chunk, and an unpaired one before it, wait for backward.
+        # Chunks' bf16 grad_W wait in `pending` and are folded into the fp32 grad_W several at a
+        # time (one pass per fold); the last chunk, and those still pending, wait for backward.
         grad_weight = None
-        pending = last_gw = None
+        pending, last_gw = [], None
         accumulated = False
         row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
         grad_h_of = GradHidden(w, [min(chunk, n - s) for s in range(0, n, chunk)], lib, stream) if want_h else None
@@ -265,17 +282,15 @@ class _FusedLinearCE(torch.autograd.Function):
                 gw = torch.matmul(logits.t(), h)  # (V, D) bf16
                 if e == n:
                     last_gw = gw
-                elif pending is None:
-                    pending = gw
                 else:
-                    if grad_weight is None:
-                        grad_weight = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
-                    _native.check(lib.tm_ce_grad_w2(grad_weight.data_ptr(), pending.data_ptr(), gw.data_ptr(),
-                                                    gw.numel(), int(accumulated), None, None, stream),
-                                  "tm_ce_grad_w2")
-                    accumulated = True
-                    pending = None
+                    pending.append(gw)
                     del gw
+                    if len(pending) == FOLD_CHUNKS or len(pending) * pending[0].numel() * 2 >= FOLD_BYTES:
+                        if grad_weight is None:
+                            grad_weight = torch.empty(weight.shape, dtype=torch.float32, device=weight.device)
+                        _fold(lib, grad_weight, pending, accumulated, None, None, stream)
+                        accumulated = True
+                        pending = []
             del logits
         del grad_h_of
         loss, ctx.n_valid = _mean_loss(row_loss, labels, n, ignore_index, lib, stream)
@@ -317,14 +332,8 @@ class _FusedLinearCE(torch.autograd.Function):
             if last_gw is not None:
                 if grad_weight is None:
                     grad_weight = torch.empty(shape, dtype=torch.float32, device=device)
-                if pending is not None:  # the unpaired chunk before the last, then the last
-                    _native.check(lib.tm_ce_grad_w2(grad_weight.data_ptr(), pending.data_ptr(),
-                                                    last_gw.data_ptr(), last_gw.numel(), int(ctx.accumulated),
-                                                    g.data_ptr(), n_valid.data_ptr(), stream), "tm_ce_grad_w2")
-                else:
-                    _native.check(lib.tm_ce_grad_w(grad_weight.data_ptr(), last_gw.data_ptr(), last_gw.numel(),
-                                                   int(ctx.accumulated), g.data_ptr(), n_valid.data_ptr(),
-                                                   stream), "tm_ce_grad_w")
+                # the chunks still pending, then the last, with the scaling (at most FOLD_CHUNKS)
+                _fold(lib, grad_weight, pending + [last_gw], ctx.accumulated, g, n_valid, stream)
                 del last_gw, pending
             else:  # no rows at all: the reference scales its zero-filled buffer
                 grad_weight = scale_w = torch.zeros(shape, dtype=torch.float32, device=device)
