@@ -14,7 +14,7 @@ Per chunk of rows:
                                     fixed-order reduction, on chunks with at most 64 output tiles
                                     of 256 x 256 (rows and D multiples of 256, V of 64: up to 4096
                                     rows for D = 1024); hipBLASLt on other shapes
-  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_ce_grad_w(2) into fp32
+  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_ce_grad_w_fold into fp32
 then tm_ce_loss sums the per-row losses in a fixed order (deterministic).
 
 The last chunk's bf16 grad_W is not added in forward: it waits for backward, where
@@ -22,10 +22,10 @@ tm_ce_grad_w adds it and applies grad_out / n_valid in the same pass. With a sin
 chunk (the usual case at 4 GiB of logits) the fp32 grad_W is then written once,
 straight from the bf16 GEMM output (6 B per element), instead of a zero fill, an
 accumulate and a scaling pass (22 B per element). With several chunks, the chunks'
-bf16 grad_W are added two at a time (tm_ce_grad_w2: one read and one write of the fp32
-grad_W per pair), and an unpaired chunk before the last is added together with the last
-in backward. The fp32 additions and the scaling are the reference's, in the reference's
-order, so the bits are unchanged.
+bf16 grad_W wait and are added up to 8 at a time (tm_ce_grad_w_fold: one read and one
+write of the fp32 grad_W per fold; a fold also starts once 4 GiB of chunks wait), and the
+chunks still waiting are added together with the last in backward. The fp32 additions and
+the scaling are the reference's, in the reference's order, so the bits are unchanged.
 
 Only the gradients autograd needs are computed. With grad mode off, or no input that
 requires a gradient (evaluation), the call returns the loss from the logits GEMM and
@@ -47,7 +47,7 @@ Chunking: 1024 rows by default, the reference's default (:131). ``chunk_size=Non
 ``"auto"`` opts into MI355X sizing: chunks whose bf16 logits take up to 4 GiB, so that
 with 288 GB of HBM the whole Qwen3 vocabulary for 8K-16K tokens fits in one chunk, the
 fp32 grad_W is written once, by the backward hand-over, instead of being read and written
-for every pair of 1024-row chunks, and the GEMMs get large M.
+for every fold of 1024-row chunks, and the GEMMs get large M.
 """
 
 from __future__ import annotations
