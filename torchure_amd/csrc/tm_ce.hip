@@ -226,11 +226,15 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
       // `keep` stays in VGPRs): a load under a per-thread branch next to its use made each
       // of them wait for the one before. A thread past the row's last vector loads that
       // last vector again, a real element of the row, which leaves the max and min as they
-      // are; the sum and the stores below skip those slots.
+      // are; the sum and the stores below skip those slots. The loss-only pass reads the
+      // row non-temporally: 3-22% faster than temporal loads from 1024 to 8192 rows of the
+      // Qwen3 vocabulary (same bits); the gradient pass, which rewrites the row, measured
+      // no better with them at 2048 rows and beyond.
 #pragma unroll
       for (int k = 0; k < kRegCols; ++k) {
         const int64_t v = threadIdx.x + static_cast<int64_t>(k) * kCeThreads;
-        keep[k] = *reinterpret_cast<const u32x4*>(row + (v < nvec ? v : nvec - 1) * 8);
+        const u32x4* src = reinterpret_cast<const u32x4*>(row + (v < nvec ? v : nvec - 1) * 8);
+        keep[k] = kGrad ? *src : __builtin_nontemporal_load(src);
       }
       __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from starting the max before the last load
 #pragma unroll
@@ -367,7 +371,9 @@ __global__ __launch_bounds__(kCeThreads) void ce_rows_kernel(uint16_t* __restric
       o.z = pack_bf16x2(p[4], p[5]);
       o.w = pack_bf16x2(p[6], p[7]);
     }
-    *reinterpret_cast<u32x4*>(row + b) = o;
+    // non-temporal: the GEMMs that read grad_logits next find none of it in cache anyway
+    // (0.3-2.5 GB); 0-7% faster than temporal stores from 8192 down to 1024 rows
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(row + b));
   };
   auto write_row = [&](auto fold_tag) {
     if constexpr (kInRegs) {
