@@ -55,10 +55,11 @@ def parse():
                     help="keep timing CPU steps of a set until this much CPU work has been timed "
                          "(at most 100 steps)")
     ap.add_argument("--also", default="qwen3-4b-again,qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,"
-                                      "qwen3-4b-dropin,qwen3-4b-ddpbuckets,ragged",
+                                      "qwen3-4b-dropin,qwen3-4b-ddpbuckets,qwen3-4b-eager,ragged",
                     help="comma list of extra configs reported under 'extra' (empty = none); "
                          "'<config>-again' runs that config once more, on fresh allocations made "
-                         "after the earlier legs' memory was released")
+                         "after the earlier legs' memory was released; '<config>-eager' steps with "
+                         "the clip scaling the grads in place first (defer_clip=False)")
     ap.add_argument("--mode", choices=("bench", "kernels", "ce", "ce-gemm"), default="bench",
                     help="kernels: only the norm and update launches (for an -fp32acc config, the "
                          "accumulation launches), --reps times each, plus a 2 GiB device copy for "
@@ -299,6 +300,53 @@ def run_gpu(config: str, steps: int, warmup: int, chunk_elems, dev):
     del params, work, opt
     torch.cuda.empty_cache()
     return out
+
+
+def run_gpu_eager(config: str, steps: int, warmup: int, chunk_elems, dev):
+    """The reference's own clip order with the optimizer built with ``defer_clip=False``:
+    clip_grad_norm scales the bf16 grads in place (torchure/core/grad_helper.py:33, the
+    eager scale kernel: read 2 + write 2 B/param), then AdamW.step() reads the scaled grads.
+    34 B/param a step (norm 2 + scale 4 + update 28), against 30 with the clip deferred into
+    the update. Also times the scale launch alone, back to back, with events."""
+    import torch
+
+    import torchure_amd as ta
+    from torchure_amd.core.grad_helper import scale_grads_
+
+    params, work, opt, n_params = build_state(config, chunk_elems, dev)
+    opt.defer_clip = False
+    stream = torch.cuda.current_stream(dev)
+
+    def one():
+        ta.clip_grad_norm(params, None, 1.0)
+        opt.step()
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    grads = [w.grad for w in work]
+    coef = torch.tensor(1.0, dtype=torch.float32, device=dev)  # a multiply by 1.0 keeps the grads
+    scale_grads_(grads, coef)
+    reps = max(5, min(steps, 50))
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(reps):
+        scale_grads_(grads, coef)
+    b.record(stream)
+    torch.cuda.synchronize()
+    scale_ms = a.elapsed_time(b) / reps
+    del params, work, opt, grads
+    torch.cuda.empty_cache()
+    gbs = 34 * n_params / (ms * 1e-3) / 1e9
+    return dict(config=config + "-eager-clip", n_params=n_params, ms_per_step=round(ms, 4), bytes_per_param=34,
+                GBps=round(gbs, 1), frac_of_peak=round(gbs / PEAK_HBM_GBS, 4), scale_ms_mean=round(scale_ms, 4),
+                scale_GBps=round(4 * n_params / (scale_ms * 1e-3) / 1e9, 1))
 
 
 def ddp_bucket_grads(params, bucket_mb: int = 25) -> int:
@@ -851,6 +899,11 @@ def main():
             bucketed = cfg.endswith("-ddpbuckets")
             base_cfg = cfg.rsplit("-", 1)[0]
             r = run_gpu_dropin(base_cfg, args.steps, args.warmup, args.chunk_elems, dev, buckets=bucketed)
+            extra[cfg] = r
+            print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
+            continue
+        if cfg.endswith("-eager"):
+            r = run_gpu_eager(cfg[: -len("-eager")], args.steps, args.warmup, args.chunk_elems, dev)
             extra[cfg] = r
             print(f"[bench] {cfg}: {r}", file=sys.stderr, flush=True)
             continue

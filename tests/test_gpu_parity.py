@@ -1127,8 +1127,10 @@ def test_sparse_grads_are_refused():
 def test_eager_scale_matches_foreach_mul():
     """The eager clip's in-place scale against torch._foreach_mul_ with the same 0-d device
     coefficient (torchure/core/grad_helper.py:33), bit for bit, for fp32 and bf16 grads:
-    lengths of 1, 7, 1000, one chunk + 5 and 40,000 elements, and views at offsets that
-    are not 16-byte aligned, so the vector, tail and element-wise paths all run."""
+    lengths of 1, 7, 1000, one chunk + 5 and 40,000 elements, lengths around the kernel's
+    512-element slice and its two 256-element halves (255, 257, 300, 511, 513, 770), and views
+    at offsets that are not 16-byte aligned, so the vector, tail and element-wise paths all
+    run."""
     from torchure_amd.core.grad_helper import scale_grads_
 
     gen = torch.Generator(device=DEV).manual_seed(77)
@@ -1139,6 +1141,8 @@ def test_eager_scale_matches_foreach_mul():
         base[7] = -0.0
         grads = [base[0:1], base[16:23], base[32:1032], base[2048:2048 + 16384 + 5],
                  base[50_000:90_000], base[100_001:100_001 + 5000], base[110_003:110_003 + 33]]
+        grads += [base[o:o + n] for o, n in ((120_000, 255), (121_000, 257), (122_000, 300),
+                                             (123_000, 511), (124_000, 513), (125_008, 770))]
         ref = [g.clone() for g in grads]
         coef = torch.tensor(0.3712, device=DEV)
         scale_grads_(grads, coef)

@@ -185,14 +185,15 @@ constexpr int kUpdateLds = 13312;
 constexpr int64_t kMaxSliceBlocks = 0xFFFFFFFFll / kWave;
 
 // Chunk and first element of this workgroup's slice, in a launch that starts at chunk
-// first_chunk with slices_per_chunk = chunk_elems / kSlice workgroups per chunk.
+// first_chunk with slices_per_chunk = chunk_elems / kS workgroups per chunk.
+template <int kS = kSlice>
 __device__ __forceinline__ void slice_of(const tm_chunk_t* __restrict__ chunks, uint32_t first_chunk,
                                          uint32_t slices_per_chunk, int64_t chunk_elems,
                                          tm_chunk_t& ck, int64_t& start) {
   const uint32_t local = blockIdx.x / slices_per_chunk;
   const uint32_t sub = blockIdx.x - local * slices_per_chunk;
   ck = chunks[first_chunk + local];
-  start = static_cast<int64_t>(ck.chunk) * chunk_elems + static_cast<int64_t>(sub) * kSlice;
+  start = static_cast<int64_t>(ck.chunk) * chunk_elems + static_cast<int64_t>(sub) * kS;
 }
 
 // Policy::group(e) / Policy::one(i) over the slice [start, end): lane t takes the group
@@ -412,11 +413,20 @@ __global__ void clip_coef_kernel(const float* __restrict__ norm, float max_norm,
 
 // ------------------------------------------------------------------- grad scale
 
+// The eager scale covers 512 elements per wave: lane t takes the groups [start + 4t, +4) and
+// [start + 256 + 4t, +4), whose loads are both issued before either store. Each wave
+// instruction is still one contiguous span (1 KiB of fp32, 512 B of bf16). With 256 elements
+// per wave a bf16 scale moved 1 KiB per workgroup and ran at 4.8 TB/s on MI355X; with 512,
+// 6.75 TB/s (2^31 bf16 elements, read and written in place).
+constexpr int kScaleSlice = 2 * kSlice;
+static_assert(TM_CHUNK_ALIGN % kScaleSlice == 0, "a chunk must hold whole scale slices");
+
 struct ScaleF32 {
   float* g;
   float coef;
-  __device__ __forceinline__ void group(int64_t e) const {
-    f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(g + e));
+  typedef f32x4 Raw;
+  __device__ __forceinline__ Raw load(int64_t e) const { return ld<true>(reinterpret_cast<const f32x4*>(g + e)); }
+  __device__ __forceinline__ void finish(Raw a, int64_t e) const {
     a.x = a.x * coef;
     a.y = a.y * coef;
     a.z = a.z * coef;
@@ -432,11 +442,12 @@ struct ScaleF32 {
 struct ScaleBf16 {
   uint16_t* g;
   float coef_b;
+  typedef u32x2 Raw;
   __device__ __forceinline__ uint32_t scale2(uint32_t w) const {
     return bf16_rne(bf16_lo(w) * coef_b) | (bf16_rne(bf16_hi(w) * coef_b) << 16);
   }
-  __device__ __forceinline__ void group(int64_t e) const {
-    u32x2 w = ld<true>(reinterpret_cast<const u32x2*>(g + e));
+  __device__ __forceinline__ Raw load(int64_t e) const { return ld<true>(reinterpret_cast<const u32x2*>(g + e)); }
+  __device__ __forceinline__ void finish(Raw w, int64_t e) const {
     w.x = scale2(w.x);
     w.y = scale2(w.y);
     st<true>(reinterpret_cast<u32x2*>(g + e), w);
@@ -446,7 +457,26 @@ struct ScaleBf16 {
   }
 };
 
-// One slice per wave; the same single multiply per element on the vector and the
+// Policy::load / finish over the two groups of a kScaleSlice slice [start, end) when vec is
+// set; the rest of the slice goes element by element.
+template <class Policy>
+__device__ __forceinline__ void slice_apply2(const Policy& pol, int64_t start, int64_t end, bool vec) {
+  int64_t vend = start;
+  if (vec) {
+    vend = start + ((end - start) & ~int64_t(3));
+    const int64_t e0 = start + static_cast<int64_t>(threadIdx.x) * 4;
+    const int64_t e1 = e0 + kSlice;
+    const bool has0 = e0 < vend, has1 = e1 < vend;
+    typename Policy::Raw r0{}, r1{};
+    if (has0) r0 = pol.load(e0);
+    if (has1) r1 = pol.load(e1);
+    if (has0) pol.finish(r0, e0);
+    if (has1) pol.finish(r1, e1);
+  }
+  for (int64_t i = vend + threadIdx.x; i < end; i += kWave) pol.one(i);
+}
+
+// One kScaleSlice slice per wave; the same single multiply per element on the vector and the
 // element-wise path (16-byte fp32 / 8-byte bf16 vectors where the grad is so aligned).
 __global__ __launch_bounds__(kWave) void grad_scale_kernel(
     const tm_tensor_t* __restrict__ tensors, int64_t n_tensors,
@@ -454,17 +484,17 @@ __global__ __launch_bounds__(kWave) void grad_scale_kernel(
     int64_t chunk_elems, const float* __restrict__ coef_p) {
   tm_chunk_t ck;
   int64_t start;
-  slice_of(chunks, first_chunk, slices_per_chunk, chunk_elems, ck, start);
+  slice_of<kScaleSlice>(chunks, first_chunk, slices_per_chunk, chunk_elems, ck, start);
   if (ck.tensor >= n_tensors) return;
   const tm_tensor_t d = tensors[ck.tensor];
   if (start >= d.numel) return;
-  const int64_t end = min(start + kSlice, d.numel);
+  const int64_t end = min(start + kScaleSlice, d.numel);
   const float coef = *coef_p;
   if (d.flags & TM_GRAD_F32) {
-    slice_apply(ScaleF32{reinterpret_cast<float*>(d.grad), coef}, start, end, aligned16(d.grad));
+    slice_apply2(ScaleF32{reinterpret_cast<float*>(d.grad), coef}, start, end, aligned16(d.grad));
   } else {
     const float coef_b = __uint_as_float(bf16_rne(coef) << 16);
-    slice_apply(ScaleBf16{reinterpret_cast<uint16_t*>(d.grad), coef_b}, start, end, aligned8(d.grad));
+    slice_apply2(ScaleBf16{reinterpret_cast<uint16_t*>(d.grad), coef_b}, start, end, aligned8(d.grad));
   }
 }
 
@@ -752,10 +782,11 @@ int launch_slices(int64_t n_slices, const char* what, F&& launch) {
 }
 
 // The same over a chunk table: kernel(first_chunk, slices_per_chunk, blocks), each launch
-// covering whole chunks.
+// covering whole chunks with slices of slice_elems (a divisor of TM_CHUNK_ALIGN).
 template <class F>
-int launch_chunk_slices(int64_t n_chunks, int64_t chunk_elems, const char* what, F&& launch) {
-  const uint32_t spc = static_cast<uint32_t>(chunk_elems / kSlice);
+int launch_chunk_slices(int64_t n_chunks, int64_t chunk_elems, const char* what, F&& launch,
+                        int64_t slice_elems = kSlice) {
+  const uint32_t spc = static_cast<uint32_t>(chunk_elems / slice_elems);
   const int64_t per = kMaxSliceBlocks / spc;
   for (int64_t first = 0; first < n_chunks; first += per) {
     const int64_t cnt = min(per, n_chunks - first);
@@ -936,11 +967,13 @@ int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
   if (rc) return rc;
   if (!d_coef) return fail(TM_EINVAL, "tm_grad_scale: null coef");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return launch_chunk_slices(n_chunks, chunk_elems, "grad_scale_kernel",
-                             [&](uint32_t first, uint32_t spc, dim3 grid) {
-                               hipLaunchKernelGGL(grad_scale_kernel, grid, dim3(kWave), 0, s, d_tensors,
-                                                  n_tensors, d_chunks, first, spc, chunk_elems, d_coef);
-                             });
+  return launch_chunk_slices(
+      n_chunks, chunk_elems, "grad_scale_kernel",
+      [&](uint32_t first, uint32_t spc, dim3 grid) {
+        hipLaunchKernelGGL(grad_scale_kernel, grid, dim3(kWave), 0, s, d_tensors, n_tensors, d_chunks, first,
+                           spc, chunk_elems, d_coef);
+      },
+      kScaleSlice);
 }
 
 int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
