@@ -230,6 +230,14 @@ int tm_cast_bf16(uint16_t* d_dst, const float* d_src, int64_t numel, void* strea
 int tm_cast_bf16_list(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
                       int64_t n_chunks, int64_t chunk_elems, void* stream);
 
+/*
+ * dst = src over nbytes (a multiple of 16; both pointers 16-byte aligned; the ranges must not
+ * overlap), one wave per KiB with non-temporal 16-byte accesses. No counterpart in the
+ * reference: it is the best 1:1 read/write stream this library's launch shapes reach on
+ * MI355X, which bench.py times beside the update as the device's measured streaming ceiling.
+ */
+int tm_stream_copy(void* d_dst, const void* d_src, int64_t nbytes, void* stream);
+
 /* ---- chunked fused linear + cross-entropy (torchure/loss/fused_linear_ce.py) ---- */
 
 /*

@@ -95,6 +95,14 @@ def test_argument_validation_without_gpu():
     assert lib.tm_grad_accumulate_bf16(None, None, 10, None) < 0
     assert lib.tm_cast_bf16(None, None, -1, None) < 0
     assert lib.tm_grad_norm(None, 1, fake, 1, 2048, 1.0, 0, fake, fake, None, None) < 0
+    # tm_stream_copy: size, alignment and overlap are checked before any launch
+    assert lib.tm_stream_copy(ctypes.c_void_p(0x2000), fake, 24, None) < 0
+    assert b"multiple of 16" in lib.tm_last_error()
+    assert lib.tm_stream_copy(ctypes.c_void_p(0x2008), fake, 32, None) < 0
+    assert b"aligned" in lib.tm_last_error()
+    assert lib.tm_stream_copy(ctypes.c_void_p(0x1010), fake, 32, None) < 0
+    assert b"overlap" in lib.tm_last_error()
+    assert lib.tm_stream_copy(fake, fake, 0, None) == _native.TM_OK
 
 
 def test_grad_h_gemm_workspace_and_shape_checks_without_gpu():

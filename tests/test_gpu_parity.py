@@ -1910,3 +1910,22 @@ def test_two_optimizers_stepped_from_two_threads():
             for k in ("step", "exp_avg", "exp_avg_sq"):
                 assert torch.equal(oa.state[x][k], ob.state[y][k])
         assert [n.view(torch.int32).item() for n in na] == [n.view(torch.int32).item() for n in nb]
+
+
+def test_stream_copy_copies_every_byte():
+    """tm_stream_copy (the bench's streaming-copy ceiling) copies exactly nbytes: sizes that fill
+    whole waves and ones that end inside a wave, at buffer offsets of 16 bytes, leaving the bytes
+    around the destination range untouched."""
+    from torchure_amd import _native
+
+    lib = _native.lib()
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    src = torch.randint(0, 256, (3 << 20,), dtype=torch.uint8, device=DEV, generator=gen)
+    for nbytes, off in ((16, 0), (1024, 16), (1040, 32), (65536 * 16 + 48, 0), ((3 << 20) - 64, 16)):
+        dst = torch.full((nbytes + 2 * 64,), 0xA5, dtype=torch.uint8, device=DEV)
+        rc = lib.tm_stream_copy(dst.data_ptr() + 64, src.data_ptr() + off, nbytes, _native.stream_handle(DEV))
+        _native.check(rc, "tm_stream_copy")
+        torch.cuda.synchronize()
+        assert torch.equal(dst[64:64 + nbytes], src[off:off + nbytes]), nbytes
+        assert bool((dst[:64] == 0xA5).all()) and bool((dst[64 + nbytes:] == 0xA5).all()), nbytes
+

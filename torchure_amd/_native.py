@@ -92,6 +92,7 @@ _SIGNATURES = {
     "tm_grad_accumulate_list": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]),
     "tm_clip_coef": (ctypes.c_int, [_vp, ctypes.c_float, _vp, _vp]),
     "tm_grad_accumulate_bf16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
+    "tm_stream_copy": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "tm_cast_bf16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "tm_cast_bf16_list": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _vp]),
     "tm_ce_rows_bf16": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _vp]),
