@@ -90,7 +90,8 @@ def run_kernels_only(config: str, reps: int, chunk_elems, dev, states: int = 1, 
     """Launch sequence profiled by rocprofv3 --pmc: `reps` x (norm, update), then a
     plain copy of 2 GiB (512 Mi fp32) whose FETCH_SIZE/WRITE_SIZE calibrate the counters.
     For an ``-fp32acc`` config: `reps` x a middle micro-step's accumulation
-    (accumulate_list_kernel), then `reps` x the last micro-step's (accumulate_list_norm_kernel).
+    (accumulate_list_kernel), then `reps` x the last micro-step's (accumulate_list_sumsq_kernel,
+    slice_reduce_kernel, norm_finalize_kernel).
     The state is built from a few pooled buffers (every tensor a view), so setting it up
     takes a handful of device dispatches however many tensors the config has."""
     import torch

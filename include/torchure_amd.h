@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TM_ABI_VERSION 1
+#define TM_ABI_VERSION 2
 
 /* status codes */
 #define TM_OK 0
@@ -206,11 +206,16 @@ int tm_grad_accumulate_bf16(float* d_acc, const uint16_t* d_micro, int64_t numel
  * With with_norm != 0 (the last micro-step) the same pass also produces the global
  * L2 norm of the accumulated grads into d_norm, bit-identical to tm_grad_norm on the
  * resulting fp32 buffers with the same chunk table -- the separate norm read pass of
- * torch._foreach_norm (torchure/core/grad_helper.py:17-18) disappears.
- *   d_ws  at least tm_workspace_bytes(0) bytes when with_norm != 0
+ * torch._foreach_norm (torchure/core/grad_helper.py:17-18) disappears. The pass writes
+ * one fp64 partial per 256-element slice into the workspace, which two small launches
+ * then reduce in a fixed order.
+ *   d_ws, ws_bytes  with_norm != 0: at least tm_accum_norm_workspace_bytes(n_chunks,
+ *                   chunk_elems) bytes (else unused; may be NULL)
+ * (ABI version 2 added ws_bytes; version 1 took a 16 KB workspace.)
  */
+size_t tm_accum_norm_workspace_bytes(int64_t n_chunks, int64_t chunk_elems);
 int tm_grad_accumulate_list(const tm_accum_t* d_list, int64_t n_list, const tm_chunk_t* d_chunks,
-                            int64_t n_chunks, int64_t chunk_elems, int with_norm, void* d_ws,
+                            int64_t n_chunks, int64_t chunk_elems, int with_norm, void* d_ws, size_t ws_bytes,
                             float* d_norm, void* stream);
 
 /* Clip coefficient from a norm already on the device:

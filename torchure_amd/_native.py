@@ -21,7 +21,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libtorchure_amd.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "torchure_amd.h")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TM_OK = 0
 TM_GRAD_BF16 = 0
@@ -89,7 +89,8 @@ _SIGNATURES = {
         ctypes.c_int,
         [_vp, _i64, _vp, _i64, _i64, ctypes.POINTER(TmHyper), ctypes.c_int32, _vp, _vp],
     ),
-    "tm_grad_accumulate_list": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, _vp, _vp]),
+    "tm_accum_norm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),
+    "tm_grad_accumulate_list": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, ctypes.c_int, _vp, ctypes.c_size_t, _vp, _vp]),
     "tm_clip_coef": (ctypes.c_int, [_vp, ctypes.c_float, _vp, _vp]),
     "tm_grad_accumulate_bf16": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "tm_stream_copy": (ctypes.c_int, [_vp, _vp, _i64, _vp]),

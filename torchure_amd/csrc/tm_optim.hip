@@ -233,18 +233,60 @@ __device__ __forceinline__ double block_sum(double x) {
   return s;
 }
 
-// ------------------------------------------------- fp32 sum-of-squares skeleton
+// ------------------------------------------------------- fp32 sum of squares: slice order
 //
-// Every fp32 sum of squares (the norm of fp32 grads, and the norm fused into the
-// last micro-step of grad accumulation) visits a chunk's elements in this one
-// fixed order, so the fused and the standalone norm give identical bits:
-//   vector part: per 2048-element block iteration, thread t takes the groups
-//     [base + 4t, +4) and [base + 1024 + 4t, +4) (each wave instruction is one
-//     contiguous 1 KiB span) and adds their 8 squares, fma-chained in fp64, to its
-//     accumulator; a last partial iteration takes single groups of 4;
-//   tail (and unaligned tensors): element by element, stride kThreads.
+// Every fp32 sum of squares (the norm of fp32 grads, and the norm fused into the last
+// micro-step of grad accumulation) is formed in this one fixed order, so the fused and the
+// standalone norm give identical bits:
+//   slice partial: a chunk is cut into slices of kSlice = 256 elements. Over a slice
+//     [start, end), lane t of a wave takes the group [start + 4t, +4) when the fp32 buffer is
+//     16-byte aligned (sumsq4: its 4 squares fma-chained in fp64 from 0.0), then the elements
+//     vend + t, vend + t + 64, ... of the slice's tail (all of the slice when the buffer is not
+//     aligned), each fma'd onto the same lane sum; wave_sum then reduces the 64 lane sums in
+//     its fixed tree (slice_wave_sum);
+//   chunk total: lane t adds the chunk's slice partials t, t + 64, t + 128, ... in order,
+//     starting from 0.0 (slices past the tensor's end count as 0.0), then slice_wave_sum;
+//   block total: block b of the fixed grid of TM_NORM_PARTIALS adds the totals of its chunks
+//     b, b + G, ... in order, starting from 0.0.
+// norm_partials_kernel computes the slice partials itself (4 waves per block, through LDS);
+// the fused accumulation runs one wave per slice, writes each slice partial to a workspace
+// and slice_reduce_kernel forms the chunk and block totals from them.
 // Policy::group(e) produces the 4 fp32 values at e (and may store them);
 // Policy::one(i) produces one value.
+
+constexpr int kSliceGroup = 64;  // slice partials a chunk total adds per lane round
+
+// The fixed reduction tree of the slice order over the 64 lanes of a wave, on DPP moves
+// within rows of 16 lanes and four lane reads (an xor-shuffle tree of doubles went through
+// LDS permutes, and formed once per KiB of fp32 grads it slowed the standalone norm by a
+// fifth): lanes i and i^1, then i and i^2 (each quad's sum in its 4 lanes), then the
+// half-row mirror (two quads), the row mirror (the row's 16 lanes; each pair adds the same two
+// values, so every lane of a row holds the same bits), then ((row0 + row1) + row2) + row3.
+// Every lane of the wave must be active; every lane returns the same value.
+template <int kCtrl>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(x));
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u)), kCtrl, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(u >> 32)), kCtrl, 0xF, 0xF,
+                                             false);
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                                     static_cast<uint32_t>(lo)));
+}
+
+__device__ __forceinline__ double lane_f64(double x, int lane) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(x));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u)), lane));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(u >> 32)), lane));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+__device__ __forceinline__ double slice_wave_sum(double x) {
+  x = x + dpp_f64<0xB1>(x);   // quad_perm [1,0,3,2]: lane i^1
+  x = x + dpp_f64<0x4E>(x);   // quad_perm [2,3,0,1]: lane i^2
+  x = x + dpp_f64<0x141>(x);  // row_half_mirror: lane 7 - i within 8
+  x = x + dpp_f64<0x140>(x);  // row_mirror: lane 15 - i within 16
+  return ((lane_f64(x, 0) + lane_f64(x, 16)) + lane_f64(x, 32)) + lane_f64(x, 48);
+}
 
 __device__ __forceinline__ double sumsq4(const f32x4 a, double s) {
   s = fma((double)a.x, (double)a.x, s);
@@ -254,27 +296,22 @@ __device__ __forceinline__ double sumsq4(const f32x4 a, double s) {
   return s;
 }
 
+// The slice partial of [start, end) (end - start <= kSlice), the same value in every lane.
 template <class Policy>
-__device__ __forceinline__ double sumsq_range_f32(const Policy& pol, int64_t start, int64_t end,
-                                                  bool vec) {
-  double acc = 0.0;
+__device__ __forceinline__ double slice_sumsq(const Policy& pol, int64_t start, int64_t end, bool vec) {
+  const int lane = threadIdx.x & 63;
+  double s = 0.0;
   int64_t vend = start;
   if (vec) {
     vend = start + ((end - start) & ~int64_t(3));
-    const int64_t lane4 = static_cast<int64_t>(threadIdx.x) * 4;
-    int64_t base = start;
-    for (; base + 2 * kGroupSpan0 <= vend; base += 2 * kGroupSpan0) {
-      const f32x4 a = pol.group(base + lane4);
-      const f32x4 b = pol.group(base + kGroupSpan0 + lane4);
-      acc += sumsq4(b, sumsq4(a, 0.0));
-    }
-    for (int64_t e = base + lane4; e < vend; e += kGroupSpan0) acc += sumsq4(pol.group(e), 0.0);
+    const int64_t e = start + static_cast<int64_t>(lane) * 4;
+    if (e < vend) s = sumsq4(pol.group(e), s);
   }
-  for (int64_t i = vend + threadIdx.x; i < end; i += kThreads) {
+  for (int64_t i = vend + lane; i < end; i += kWave) {
     const double x = pol.one(i);
-    acc = fma(x, x, acc);
+    s = fma(x, x, s);
   }
-  return acc;
+  return slice_wave_sum(s);
 }
 
 struct ReadF32 {
@@ -285,17 +322,28 @@ struct ReadF32 {
   __device__ __forceinline__ float one(int64_t i) const { return g[i]; }
 };
 
+// The 4 bf16 values at micro + e widened: one 8-byte load when micro is 8-byte aligned,
+// else four 2-byte loads (the lane still owns the same 4 elements).
+__device__ __forceinline__ f32x4 micro4(const uint16_t* micro, int64_t e, bool mvec) {
+  if (mvec) {
+    const u32x2 w = ld<true>(reinterpret_cast<const u32x2*>(micro + e));
+    return f32x4{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+  }
+  return f32x4{bf16_at(micro, e), bf16_at(micro, e + 1), bf16_at(micro, e + 2), bf16_at(micro, e + 3)};
+}
+
 // acc (fp32) += micro (bf16), stored back; yields the new accumulator values.
 struct AccumBf16 {
   float* acc;
   const uint16_t* micro;
+  bool mvec;
   __device__ __forceinline__ f32x4 group(int64_t e) const {
     f32x4 a = ld<true>(reinterpret_cast<const f32x4*>(acc + e));
-    const u32x2 w = ld<true>(reinterpret_cast<const u32x2*>(micro + e));
-    a.x = a.x + bf16_lo(w.x);
-    a.y = a.y + bf16_hi(w.x);
-    a.z = a.z + bf16_lo(w.y);
-    a.w = a.w + bf16_hi(w.y);
+    const f32x4 m = micro4(micro, e, mvec);
+    a.x = a.x + m.x;
+    a.y = a.y + m.y;
+    a.z = a.z + m.z;
+    a.w = a.w + m.w;
     st<true>(reinterpret_cast<f32x4*>(acc + e), a);
     return a;
   }
@@ -311,9 +359,9 @@ struct AccumBf16 {
 struct AssignBf16 {
   float* acc;
   const uint16_t* micro;
+  bool mvec;
   __device__ __forceinline__ f32x4 group(int64_t e) const {
-    const u32x2 w = ld<true>(reinterpret_cast<const u32x2*>(micro + e));
-    const f32x4 a = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+    const f32x4 a = micro4(micro, e, mvec);
     st<true>(reinterpret_cast<f32x4*>(acc + e), a);
     return a;
   }
@@ -326,11 +374,61 @@ struct AssignBf16 {
 
 // ------------------------------------------------------------------- norm pass 1
 
+// The chunk total of an fp32 buffer in the slice order, formed by a kThreads-thread block:
+// in each round of kSliceGroup slices, wave w forms the slice partials w, w + 4, ..., four at
+// a time with their loads issued together, and parks them in sp (LDS); wave 0's lane t then
+// adds partial t of the round. Valid in every lane of wave 0. Called by whole blocks only.
+__device__ __forceinline__ double chunk_total_f32(const float* g, int64_t start, int64_t end, int64_t spc,
+                                                  bool vec, double* sp) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const ReadF32 pol{g};
+  double lane_acc = 0.0;
+  for (int64_t g0 = 0; g0 < spc; g0 += kSliceGroup) {
+#pragma unroll 1
+    for (int b = 0; b < kSliceGroup / (4 * kWaves); ++b) {
+      const int k0 = wave + kWaves * 4 * b;  // this batch's slices: k0, k0 + kWaves, ...
+      f32x4 v[4];
+      unsigned full = 0;  // whole aligned slices, read together
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t j = g0 + k0 + kWaves * u;
+        const int64_t s0 = start + j * kSlice;
+        if (vec && j < spc && s0 + kSlice <= end) {
+          full |= 1u << u;
+          v[u] = pol.group(s0 + static_cast<int64_t>(lane) * 4);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (full & (1u << u)) {
+          const double p = slice_wave_sum(sumsq4(v[u], 0.0));
+          if (lane == 0) sp[k0 + kWaves * u] = p;
+        }
+      }
+#pragma unroll 1
+      for (int u = 0; u < 4; ++u) {  // a tensor's last slice, unaligned buffers, past the end
+        if (full & (1u << u)) continue;
+        const int64_t j = g0 + k0 + kWaves * u;
+        const int64_t s0 = start + j * kSlice;
+        const double p = (j < spc && s0 < end) ? slice_sumsq(pol, s0, min(s0 + kSlice, end), vec) : 0.0;
+        if (lane == 0) sp[k0 + kWaves * u] = p;
+      }
+    }
+    __syncthreads();
+    if (wave == 0) lane_acc += sp[lane];
+    __syncthreads();
+  }
+  return slice_wave_sum(lane_acc);
+}
+
 __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
     const tm_tensor_t* __restrict__ tensors, int64_t n_tensors,
     const tm_chunk_t* __restrict__ chunks, int64_t n_chunks, int64_t chunk_elems,
     double* __restrict__ partials) {
-  double acc = 0.0;
+  __shared__ double sp[kSliceGroup];
+  double acc = 0.0;        // bf16 grads: this thread's share
+  double f32_total = 0.0;  // fp32 grads: the block total of their chunk totals (wave 0)
+  const int64_t spc = chunk_elems / kSlice;
   for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
     const tm_chunk_t ck = chunks[c];
     if (ck.tensor >= n_tensors) continue;
@@ -338,9 +436,10 @@ __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
     const int64_t start = static_cast<int64_t>(ck.chunk) * chunk_elems;
     if (start >= d.numel) continue;
     const int64_t end = min(start + chunk_elems, d.numel);
-    if (d.flags & TM_GRAD_F32) {
-      acc += sumsq_range_f32(ReadF32{reinterpret_cast<const float*>(d.grad)}, start, end,
-                             aligned16(d.grad));
+    if (d.flags & TM_GRAD_F32) {  // block-uniform: the whole block takes this chunk
+      const double t = chunk_total_f32(reinterpret_cast<const float*>(d.grad), start, end, spc,
+                                       aligned16(d.grad), sp);
+      if (threadIdx.x < kWave) f32_total += t;
     } else {
       const uint16_t* __restrict__ g = reinterpret_cast<const uint16_t*>(d.grad);
       if (aligned16(d.grad)) {
@@ -374,7 +473,7 @@ __global__ __launch_bounds__(kThreads) void norm_partials_kernel(
     }
   }
   const double s = block_sum(acc);
-  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+  if (threadIdx.x == 0) partials[blockIdx.x] = s + f32_total;
 }
 
 // ------------------------------------------------------------------- norm pass 2
@@ -682,37 +781,68 @@ __global__ __launch_bounds__(kWave) void accumulate_list_kernel(
   const bool vec = aligned16(d.acc) && aligned8(d.micro);
   float* a = reinterpret_cast<float*>(d.acc);
   const uint16_t* m = reinterpret_cast<const uint16_t*>(d.micro);
-  if (d.flags & TM_ACCUM_ASSIGN) slice_apply(AssignBf16{a, m}, start, end, vec);
-  else slice_apply(AccumBf16{a, m}, start, end, vec);
+  if (d.flags & TM_ACCUM_ASSIGN) slice_apply(AssignBf16{a, m, true}, start, end, vec);
+  else slice_apply(AccumBf16{a, m, true}, start, end, vec);
 }
 
-// The last micro-step: the same accumulation over the fixed grid of TM_NORM_PARTIALS
-// blocks (block b owns chunks b, b+G, ..., the partition of norm_partials_kernel), each
-// writing the fp64 partial sum of squares of the new accumulator values.
-__global__ __launch_bounds__(kThreads) void accumulate_list_norm_kernel(
+// Where slice j of chunk c keeps its partial: chunks are padded to whole groups of
+// kSliceGroup slots, and within a group the slot of slice j is (j % 8) * 8 + j / 8. Workgroup
+// w of a launch runs on XCD w % 8 and covers slice w % slices_per_chunk (a multiple of 8), so
+// the 8 partials one XCD writes for a group are contiguous (64 bytes, whole L2 sectors);
+// in slice order they would be interleaved with the other XCDs' and every XCD's L2 would
+// write back partly written lines (measured 1.023x the algorithmic write bytes).
+static_assert((TM_CHUNK_ALIGN / kSlice) % 8 == 0, "slices per chunk must be a multiple of the 8 XCDs");
+__device__ __forceinline__ int64_t slice_slot(int64_t c, int64_t j, int64_t slices_per_chunk) {
+  const int64_t stride = (slices_per_chunk + kSliceGroup - 1) / kSliceGroup * kSliceGroup;
+  const int64_t k = j % kSliceGroup;
+  return c * stride + (j - k) + (k % 8) * 8 + k / 8;
+}
+
+// The last micro-step, one wave per slice: the accumulation of accumulate_list_kernel, and
+// the slice partial of the new accumulator values (the slice order above, whose lane mapping
+// follows the accumulator's alignment alone) written to its slice_slot; a slice past its
+// tensor's end writes 0.
+__global__ __launch_bounds__(kWave) void accumulate_list_sumsq_kernel(
     const tm_accum_t* __restrict__ list, int64_t n_list, const tm_chunk_t* __restrict__ chunks,
-    int64_t n_chunks, int64_t chunk_elems, double* __restrict__ partials) {
-  double acc = 0.0;
-  for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
-    const tm_chunk_t ck = chunks[c];
-    if (ck.tensor >= n_list) continue;
+    uint32_t first_chunk, uint32_t slices_per_chunk, int64_t chunk_elems, double* __restrict__ slice_partials) {
+  const uint32_t local = blockIdx.x / slices_per_chunk;
+  const uint32_t sub = blockIdx.x - local * slices_per_chunk;
+  const int64_t c = static_cast<int64_t>(first_chunk) + local;
+  const tm_chunk_t ck = chunks[c];
+  double p = 0.0;
+  if (ck.tensor < n_list) {
     const tm_accum_t d = list[ck.tensor];
-    const int64_t start = static_cast<int64_t>(ck.chunk) * chunk_elems;
-    if (start >= d.numel) continue;
-    const int64_t end = min(start + chunk_elems, d.numel);
-    if (d.micro) {
-      const bool vec = aligned16(d.acc) && aligned8(d.micro);
+    const int64_t start = static_cast<int64_t>(ck.chunk) * chunk_elems + static_cast<int64_t>(sub) * kSlice;
+    if (start < d.numel) {
+      const int64_t end = min(start + kSlice, d.numel);
       float* a = reinterpret_cast<float*>(d.acc);
-      const uint16_t* m = reinterpret_cast<const uint16_t*>(d.micro);
-      acc += (d.flags & TM_ACCUM_ASSIGN) ? sumsq_range_f32(AssignBf16{a, m}, start, end, vec)
-                                         : sumsq_range_f32(AccumBf16{a, m}, start, end, vec);
-    } else {  // no micro-grad this step: the accumulator only enters the norm
-      acc += sumsq_range_f32(ReadF32{reinterpret_cast<const float*>(d.acc)}, start, end,
-                             aligned16(d.acc));
+      const bool vec = aligned16(d.acc);
+      if (d.micro) {
+        const uint16_t* m = reinterpret_cast<const uint16_t*>(d.micro);
+        const bool mvec = aligned8(d.micro);
+        p = (d.flags & TM_ACCUM_ASSIGN) ? slice_sumsq(AssignBf16{a, m, mvec}, start, end, vec)
+                                        : slice_sumsq(AccumBf16{a, m, mvec}, start, end, vec);
+      } else {  // no micro-grad this step: the accumulator only enters the norm
+        p = slice_sumsq(ReadF32{a}, start, end, vec);
+      }
     }
   }
-  const double s = block_sum(acc);
-  if (threadIdx.x == 0) partials[blockIdx.x] = s;
+  if (threadIdx.x == 0) slice_partials[slice_slot(c, sub, slices_per_chunk)] = p;
+}
+
+// Block b of the fixed grid of TM_NORM_PARTIALS: the chunk totals of its chunks b, b + G, ...
+// from their slice partials, added in chunk order (the slice order above), into partials[b].
+__global__ __launch_bounds__(kWave) void slice_reduce_kernel(const double* __restrict__ slice_partials,
+                                                             int64_t n_chunks, int64_t slices_per_chunk,
+                                                             double* __restrict__ partials) {
+  double total = 0.0;
+  for (int64_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+    double lane_acc = 0.0;
+    for (int64_t j = threadIdx.x; j < slices_per_chunk; j += kWave)
+      lane_acc += slice_partials[slice_slot(c, j, slices_per_chunk)];
+    total += slice_wave_sum(lane_acc);
+  }
+  if (threadIdx.x == 0) partials[blockIdx.x] = total;
 }
 
 // ------------------------------------------------------------------- elementwise
@@ -726,7 +856,7 @@ __global__ __launch_bounds__(kWave) void accumulate_kernel(float* __restrict__ a
   const int64_t end = min(start + kSlice, n);
   const bool vec = aligned16(reinterpret_cast<uint64_t>(acc)) &&
                    aligned8(reinterpret_cast<uint64_t>(micro));
-  slice_apply(AccumBf16{acc, micro}, start, end, vec);
+  slice_apply(AccumBf16{acc, micro, true}, start, end, vec);
 }
 
 // dst (bf16) = RNE(src (fp32)).
@@ -1015,19 +1145,38 @@ int tm_adamw_step_noalloc(const tm_tensor_t* d_tensors, int64_t n_tensors, const
   return launch_step(d_tensors, n_tensors, d_chunks, n_chunks, chunk_elems, h_groups, n_groups, d_coef, scal, s);
 }
 
+size_t tm_accum_norm_workspace_bytes(int64_t n_chunks, int64_t chunk_elems) {
+  if (n_chunks < 0 || chunk_elems <= 0) return 0;
+  const int64_t spc = chunk_elems / kSlice;
+  const int64_t stride = (spc + kSliceGroup - 1) / kSliceGroup * kSliceGroup;  // slice_slot's padding
+  return align_up(kPartialBytes, 256) +
+         align_up(sizeof(double) * static_cast<size_t>(n_chunks) * static_cast<size_t>(stride), 256);
+}
+
 int tm_grad_accumulate_list(const tm_accum_t* d_list, int64_t n_list, const tm_chunk_t* d_chunks,
-                            int64_t n_chunks, int64_t chunk_elems, int with_norm, void* d_ws,
+                            int64_t n_chunks, int64_t chunk_elems, int with_norm, void* d_ws, size_t ws_bytes,
                             float* d_norm, void* stream) {
   int rc = check_table(d_list, n_list, d_chunks, n_chunks, chunk_elems, "tm_grad_accumulate_list");
   if (rc) return rc;
-  if (with_norm && (!d_ws || !d_norm))
-    return fail(TM_EINVAL, "tm_grad_accumulate_list: norm requested with null workspace or output");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (with_norm) {
+    if (!d_ws || !d_norm)
+      return fail(TM_EINVAL, "tm_grad_accumulate_list: norm requested with null workspace or output");
+    const size_t need = tm_accum_norm_workspace_bytes(n_chunks, chunk_elems);
+    if (ws_bytes < need)
+      return fail(TM_EINVAL, "tm_grad_accumulate_list: workspace of %zu bytes, %zu needed for the norm", ws_bytes,
+                  need);
     double* partials = static_cast<double*>(d_ws);
-    hipLaunchKernelGGL(accumulate_list_norm_kernel, dim3(TM_NORM_PARTIALS), dim3(kThreads), 0, s,
-                       d_list, n_list, d_chunks, n_chunks, chunk_elems, partials);
-    if ((rc = check_launch("accumulate_list_norm_kernel"))) return rc;
+    double* slice_partials = reinterpret_cast<double*>(static_cast<char*>(d_ws) + align_up(kPartialBytes, 256));
+    rc = launch_chunk_slices(n_chunks, chunk_elems, "accumulate_list_sumsq_kernel",
+                             [&](uint32_t first, uint32_t spc, dim3 grid) {
+                               hipLaunchKernelGGL(accumulate_list_sumsq_kernel, grid, dim3(kWave), 0, s, d_list,
+                                                  n_list, d_chunks, first, spc, chunk_elems, slice_partials);
+                             });
+    if (rc) return rc;
+    hipLaunchKernelGGL(slice_reduce_kernel, dim3(TM_NORM_PARTIALS), dim3(kWave), 0, s, slice_partials, n_chunks,
+                       chunk_elems / kSlice, partials);
+    if ((rc = check_launch("slice_reduce_kernel"))) return rc;
     hipLaunchKernelGGL(norm_finalize_kernel, dim3(1), dim3(kThreads), 0, s, partials, 0.0f, 0,
                        d_norm, static_cast<float*>(nullptr));
     return check_launch("norm_finalize_kernel");

@@ -215,10 +215,13 @@ def accumulate_grads_(params, *, last: bool = False,
     chunks, n_chunks = tables.CHUNKS.get(rows["numel"], chunk_elems, device)
     d_rows = _ACC_UPLOAD(rows, device)
     norm = torch.empty((), dtype=torch.float32, device=device) if last else None
-    ws = torch.empty(_native.workspace_bytes(0), dtype=torch.uint8, device=device) if last else None
+    ws = None
+    if last:  # one fp64 partial per 256-element slice, reduced in a fixed order
+        ws = torch.empty(int(_native.lib().tm_accum_norm_workspace_bytes(n_chunks, chunk_elems)),
+                         dtype=torch.uint8, device=device)
     rc = _native.lib().tm_grad_accumulate_list(
         d_rows.data_ptr(), len(accs), chunks.data_ptr(), n_chunks, chunk_elems, int(last),
-        ws.data_ptr() if last else None, norm.data_ptr() if last else None,
+        ws.data_ptr() if last else None, ws.numel() if last else 0, norm.data_ptr() if last else None,
         _native.stream_handle(device))
     _native.check(rc, "tm_grad_accumulate_list")
     for a, m in zip(accs, micros):
