@@ -103,6 +103,15 @@ def test_argument_validation_without_gpu():
     assert lib.tm_stream_copy(ctypes.c_void_p(0x1010), fake, 32, None) < 0
     assert b"overlap" in lib.tm_last_error()
     assert lib.tm_stream_copy(fake, fake, 0, None) == _native.TM_OK
+    # the fused norm of the last micro-step needs one fp64 slot per 256-element slice (chunks
+    # padded to 64 slots) beyond the 16 KB of block partials, and refuses less
+    ws = lib.tm_accum_norm_workspace_bytes
+    assert ws(10, 16384) == 16384 + 10 * 64 * 8
+    assert ws(10, 2048) == 16384 + 10 * 64 * 8 and ws(3, 18432) == 16384 + 3 * 128 * 8
+    assert ws(0, 16384) == 16384
+    assert lib.tm_grad_accumulate_list(fake, 1, fake, 10, 16384, 1, fake, ws(10, 16384) - 8, fake, None) < 0
+    assert b"needed" in lib.tm_last_error()
+    assert lib.tm_grad_accumulate_list(fake, 1, fake, 1, 16384, 1, None, 1 << 20, fake, None) < 0
 
 
 def test_grad_h_gemm_workspace_and_shape_checks_without_gpu():

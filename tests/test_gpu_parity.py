@@ -1929,3 +1929,66 @@ def test_stream_copy_copies_every_byte():
         assert torch.equal(dst[64:64 + nbytes], src[off:off + nbytes]), nbytes
         assert bool((dst[:64] == 0xA5).all()) and bool((dst[64 + nbytes:] == 0xA5).all()), nbytes
 
+
+
+@pytest.mark.parametrize("chunk_elems", [2048, 10240, 16384, 18432])
+def test_fused_and_standalone_norm_partials_bit_equal(chunk_elems):
+    """The last micro-step's fused norm and tm_grad_norm over the resulting fp32 buffers form
+    the same 2048 fp64 block partials, bit for bit (not only the same fp32 norm): chunks of 8,
+    40, 64 and 72 slices (one round of slice partials, a partial round, two rounds), lengths
+    around the 256-element slice and the chunk, accumulators that are not 16-byte aligned
+    (element-wise lane mapping) and micro-grads that are not 8-byte aligned (the accumulator's
+    mapping with 2-byte loads); the sums match fp64 within 1e-12 relative."""
+    from torchure_amd import _native
+
+    lib = _native.lib()
+    lens = [1, 255, 256, 257, 5000, 16384, 16385, 40000, 100003, 18431]
+    acc_off = [0, 64, 1, 128, 3, 0, 2, 64, 0, 5]      # fp32 elements: odd ones break 16 B alignment
+    mic_off = [0, 8, 3, 0, 8, 1, 0, 5, 8, 0]          # bf16 elements: odd ones break 8 B alignment
+    gen = torch.Generator(device=DEV).manual_seed(99)
+    room = sum(lens) + 256 * len(lens)
+    acc_pool = torch.randn(room, device=DEV, generator=gen) * 1e-2
+    mic_pool = (torch.randn(room, device=DEV, generator=gen) * 2e-3).to(torch.bfloat16)
+    accs, mics, pa, pm = [], [], 0, 0
+    for n, oa, om in zip(lens, acc_off, mic_off):
+        accs.append(acc_pool[pa + oa: pa + oa + n])
+        mics.append(mic_pool[pm + om: pm + om + n])
+        pa += oa + n + 64 - (oa + n) % 64
+        pm += om + n + 64 - (om + n) % 64
+    assert [a.numel() for a in accs] == lens and [m.numel() for m in mics] == lens
+    numels = np.asarray(lens, dtype=np.int64)
+    chunks = torch.from_numpy(_native.fill_chunks(numels, chunk_elems).view(np.uint8).copy()).to(DEV)
+    n_chunks = chunks.numel() // 8
+    stream = _native.stream_handle(DEV)
+
+    rows = np.zeros(len(lens), dtype=_native.ACCUM_DTYPE)
+    rows["acc"] = [a.data_ptr() for a in accs]
+    rows["micro"] = [m.data_ptr() for m in mics]
+    rows["numel"] = numels
+    d_rows = torch.from_numpy(rows.view(np.uint8).copy()).to(DEV)
+    ws_a = torch.zeros(int(lib.tm_accum_norm_workspace_bytes(n_chunks, chunk_elems)), dtype=torch.uint8, device=DEV)
+    norm_a = torch.empty((), dtype=torch.float32, device=DEV)
+    want = [(a.double() + m.double()).float() for a, m in zip(accs, mics)]
+    _native.check(lib.tm_grad_accumulate_list(d_rows.data_ptr(), len(lens), chunks.data_ptr(), n_chunks, chunk_elems,
+                                              1, ws_a.data_ptr(), ws_a.numel(), norm_a.data_ptr(), stream),
+                  "tm_grad_accumulate_list")
+    torch.cuda.synchronize()
+    for a, w in zip(accs, want):
+        assert torch.equal(a.view(torch.int32), w.view(torch.int32))
+
+    trows = np.zeros(len(lens), dtype=_native.TENSOR_DTYPE)
+    trows["grad"] = [a.data_ptr() for a in accs]
+    trows["numel"] = numels
+    trows["flags"] = _native.TM_GRAD_F32
+    d_trows = torch.from_numpy(trows.view(np.uint8).copy()).to(DEV)
+    ws_b = torch.zeros(_native.workspace_bytes(len(lens)), dtype=torch.uint8, device=DEV)
+    norm_b = torch.empty((), dtype=torch.float32, device=DEV)
+    _native.check(lib.tm_grad_norm(d_trows.data_ptr(), len(lens), chunks.data_ptr(), n_chunks, chunk_elems, 0.0, 0,
+                                   ws_b.data_ptr(), norm_b.data_ptr(), None, stream), "tm_grad_norm")
+    torch.cuda.synchronize()
+    part_a = ws_a[: 8 * _native.TM_NORM_PARTIALS].view(torch.float64)
+    part_b = ws_b[: 8 * _native.TM_NORM_PARTIALS].view(torch.float64)
+    assert torch.equal(part_a.view(torch.int64), part_b.view(torch.int64))
+    assert norm_a.view(torch.int32).item() == norm_b.view(torch.int32).item()
+    exact = math.fsum(float((a.double() ** 2).sum()) for a in accs)
+    assert abs(float(part_a.sum()) - exact) <= 1e-12 * exact
