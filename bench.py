@@ -628,7 +628,27 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
         loss.backward()
 
     out["fp32_hidden_autocast_chunk4096_ms"] = round(timed(ours_fp32_hidden), 4)
-    del hidden32
+
+    # The same two calls on a head that carries a bf16 working copy kept by the optimizer
+    # (attach_bf16_working_params): the op reads the copy instead of casting the fp32 master.
+    import torchure_amd as ta
+
+    head = torch.nn.Parameter(weight.detach().clone())
+    ta.attach_bf16_working_params([head])
+
+    def ours_fp32_hidden_copy():
+        h = hidden32.detach().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            loss = fused_linear_cross_entropy(h, head, labels, -100, 4096)
+        torch.autograd.grad(loss, (h, head))  # no accumulation into head.grad, as in the leg above
+
+    def evaluate_copy():
+        with torch.no_grad():
+            fused_linear_cross_entropy(hidden, head, labels, -100, "auto")
+
+    out["working_copy_fp32_hidden_autocast_chunk4096_ms"] = round(timed(ours_fp32_hidden_copy), 4)
+    out["working_copy_loss_only_ms"] = round(timed(evaluate_copy), 4)
+    del head, hidden32
     if with_reference:
         comp = torch.compile(_ce_chunk_reference, dynamic=False)
 

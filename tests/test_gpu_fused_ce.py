@@ -776,3 +776,57 @@ def test_fp32_hidden_without_autocast(chunk):
     assert wb.grad.dtype == torch.bfloat16 and h2.grad.dtype == torch.float32
     with pytest.raises(NotImplementedError, match="float16"):
         fused_linear_cross_entropy(hidden.half().requires_grad_(True), weight, labels)
+
+
+def test_fp32_weight_with_current_working_copy():
+    """An fp32 head weight with an attached bf16 working copy: while the copy is current the op
+    reads it instead of casting the master, with the cast's bits (loss, grad_h and grad_W equal a
+    weight without a copy, bit for bit, training and loss-only); the copy really is what the op
+    reads (bytes overwritten behind autograd's back change the loss, and a refresh restores it);
+    a master modified in place makes the copy stale and the op casts again."""
+    import torchure_amd as ta
+    from torchure_amd import _native
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(31)
+    n, d, v = 1500, 256, 6000
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::9] = -100
+    master = torch.nn.Parameter(torch.randn(v, d, device=DEV, generator=g) * 0.05)
+    (copy,) = ta.attach_bf16_working_params([master])
+
+    def run(weight):
+        h = hidden.clone().requires_grad_(True)
+        loss = fused_linear_cross_entropy(h, weight, labels, -100, 512)
+        gh, gw = torch.autograd.grad(loss, (h, weight))
+        with torch.no_grad():
+            eval_loss = fused_linear_cross_entropy(hidden, weight, labels, -100, 512)
+        return loss.detach(), gh, gw, eval_loss
+
+    def same(a, b):
+        return all(torch.equal(x.view(torch.int32) if x.dtype == torch.float32 else x.view(torch.int16),
+                               y.view(torch.int32) if y.dtype == torch.float32 else y.view(torch.int16))
+                   for x, y in zip(a, b))
+
+    plain = torch.nn.Parameter(master.detach().clone())
+    assert same(run(master), run(plain))
+    assert torch.equal(run(master)[0], run(plain)[3])  # loss-only gives the training bits
+
+    # overwrite the copy's bytes without an autograd version bump: the op reads the copy
+    junk = (torch.randn(v, d, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    _native.check(_native.lib().tm_stream_copy(copy.data_ptr(), junk.data_ptr(), junk.numel() * 2,
+                                               _native.stream_handle(DEV)), "tm_stream_copy")
+    torch.cuda.synchronize()
+    assert not torch.equal(run(master)[0], run(plain)[0])
+    ta.refresh_bf16_working_params([master])
+    assert same(run(master), run(plain))
+
+    # a master changed in place: the copy is stale, the op casts the master again
+    with torch.no_grad():
+        master.mul_(1.5)
+        plain.mul_(1.5)
+    _native.check(_native.lib().tm_stream_copy(copy.data_ptr(), junk.data_ptr(), junk.numel() * 2,
+                                               _native.stream_handle(DEV)), "tm_stream_copy")
+    torch.cuda.synchronize()
+    assert same(run(master), run(plain))

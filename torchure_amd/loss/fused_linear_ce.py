@@ -58,6 +58,7 @@ import torch
 
 from torchure_amd import _native
 from torchure_amd.core import tables
+from torchure_amd.optimizer.working import current_copy
 
 DEFAULT_LOGITS_BYTES = 4 << 30
 
@@ -194,6 +195,18 @@ class GradHidden:
                                                  self.stream), "tm_ce_grad_h_bf16")
 
 
+def _bf16_weight(weight: torch.Tensor) -> torch.Tensor:
+    """The contiguous bf16 weight the products run on: ``weight.to(bf16)`` (RNE, as autocast
+    casts), or, for an fp32 master whose bf16 working copy is current (attached with
+    torchure_amd.attach_bf16_working_params and rewritten by each AdamW step), that copy, which
+    holds the same bits, so the cast's read of 4 and write of 2 bytes per element is skipped."""
+    if weight.dtype == torch.float32:
+        w = current_copy(weight)
+        if w is not None:
+            return w.detach()
+    return weight.to(torch.bfloat16).contiguous()
+
+
 def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
     """The loss when no input needs a gradient (e.g. evaluation under torch.no_grad): the
     same logits GEMM and the same per-row arithmetic as the training path, so the same
@@ -204,7 +217,7 @@ def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
     stream = _native.stream_handle(hidden.device)
     dt = torch.float32 if mode == "fp32" else torch.bfloat16
     hb = hidden.to(torch.bfloat16) if mode == "autocast" else hidden  # autocast's cast (RNE)
-    w = weight.to(dt).contiguous()
+    w = weight.to(dt).contiguous() if mode == "fp32" else _bf16_weight(weight)
     rows_loss = lib.tm_ce_rows_loss_f32 if mode == "fp32" else lib.tm_ce_rows_loss_bf16
     row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
     for s in range(0, n, chunk):
@@ -258,7 +271,7 @@ class _FusedLinearCE(torch.autograd.Function):
         lib = _native.lib()
         stream = _native.stream_handle(hidden.device)
         hb = hidden.to(torch.bfloat16) if fp32 else hidden  # autocast's cast (RNE)
-        w = weight.to(torch.bfloat16).contiguous()  # cast once, not per chunk
+        w = _bf16_weight(weight)  # cast once, not per chunk (or the current working copy)
         want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         # bf16 GEMM output either way; for fp32 hidden it is widened and scaled in backward
         grad_hidden = torch.empty(hidden.shape, dtype=torch.bfloat16, device=hidden.device) if want_h else None

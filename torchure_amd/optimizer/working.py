@@ -79,6 +79,18 @@ def is_current(p: torch.Tensor, w: torch.Tensor) -> bool:
     return getattr(w, "_tm_master_version", None) == p._version
 
 
+def current_copy(p: torch.Tensor) -> torch.Tensor | None:
+    """``p``'s attached bf16 working copy if it holds RNE(``p``) now, else None: the copy has
+    ``p``'s shape and device and ``p`` has not been modified in place since the copy was last
+    written (by attach, refresh or ``AdamW.step()``), the test the step itself applies. Its bits
+    are then those of ``p.to(torch.bfloat16)``, so a reader may take it instead of casting."""
+    w = getattr(p, "_tm_working", None)
+    if (w is None or p.dtype != torch.float32 or w.dtype != torch.bfloat16 or w.shape != p.shape
+            or w.device != p.device or not w.is_contiguous() or not is_current(p, w)):
+        return None
+    return w
+
+
 def refresh_bf16_working_params(params) -> None:
     """Rewrite the attached bf16 working copies as RNE(master), in place.
 
