@@ -82,3 +82,50 @@ def test_noalloc_step_argument_checks():
     assert lib.tm_adamw_step_noalloc(fake, 1, fake, 1, 2048, hyper, 0, None, None) < 0
     assert b"n_groups" in lib.tm_last_error()
     assert lib.tm_adamw_step_noalloc(None, 0, None, 0, 2048, hyper, 1, None, None) == _native.TM_OK
+
+
+def test_noalloc_step_captured_in_a_hip_graph():
+    """The allocation-free step is what a caller under HIP graph capture can launch: captured in
+    a torch.cuda.CUDAGraph and replayed three times, with eager work and synchronisations
+    between the replays, it leaves after every replay the state of as many eager
+    tm_adamw_step_noalloc calls on an identical copy, bit for bit (each replay advances the
+    device-side step counters, so the bias corrections change from replay to replay)."""
+    from torchure_amd import _native
+
+    lib = _native.lib()
+    shapes = [(512, 300), (1031,), (77, 45), (4096,), (33,)]
+    host = H.make_host_set(shapes, seed=95, grad_std=0.02)
+    graph_set = H.device_setup(host, DEV)
+    eager_set = H.device_setup(host, DEV)
+    warm_set = H.device_setup(host, DEV)
+
+    def launch(sl):
+        rc = lib.tm_adamw_step_noalloc(sl.d_rows.data_ptr(), sl.n, sl.chunks.data_ptr(), sl.n_chunks,
+                                       sl.chunk_elems, sl.groups_c, sl.n_groups, None,
+                                       _native.stream_handle(DEV))
+        _native.check(rc, "tm_adamw_step_noalloc")
+
+    plans = [opt.plan_step(None, set()) for _, _, opt in (graph_set, eager_set, warm_set)]
+    assert all(len(p) == 1 for p in plans)
+    graph_launch, eager_launch, warm_launch = (p[0] for p in plans)
+    launch(warm_launch)  # the first call on the device looks up the static scratch, outside capture
+    torch.cuda.synchronize()
+
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            launch(graph_launch)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    _assert_same(graph_set, H.device_setup(host, DEV))  # capturing ran nothing
+
+    for k in range(3):
+        print(f"replay {k}", flush=True)
+        g.replay()
+        launch(eager_launch)
+        torch.cuda.synchronize()
+        assert torch.randn(4096, device=DEV).abs().sum().item() > 0  # eager work between replays
+        _assert_same(graph_set, eager_set)
+        assert float(graph_set[2].state[graph_set[0][0]]["step"].item()) == 1000.0 + k + 1
