@@ -35,23 +35,11 @@
 
 namespace {
 
-constexpr int kRowThreadsRegs = 1024;  // 16 wave64 per row when the row stays in registers
-#ifndef TM_CE_STREAM_THREADS
-#define TM_CE_STREAM_THREADS 256
-#endif
-#ifndef TM_CE_STREAM_LDS
-#define TM_CE_STREAM_LDS 0
-#endif
-// Streaming path: threads per row, and dynamic LDS per workgroup used only to cap how
-// many rows are in flight per CU (so the second read of a row can hit the MALL).
-constexpr int kRowThreadsStream = TM_CE_STREAM_THREADS;
-constexpr int kStreamLds = TM_CE_STREAM_LDS;
-#ifndef TM_CE_REG_ROWS
-#define TM_CE_REG_ROWS 1
-#endif
+constexpr int kRowThreadsRegs = 1024;   // 16 wave64 per row when the row stays in registers
+constexpr int kRowThreadsStream = 256;  // threads per row on the streaming path (longer rows)
 constexpr int kStreamUnroll = 4;  // vectors per thread loaded together on the streaming path
 constexpr int kRegCols = 20;  // 8-element vectors per thread kept in registers (V <= 163,840)
-constexpr int kMaxWaves = (kRowThreadsRegs > TM_CE_STREAM_THREADS ? kRowThreadsRegs : TM_CE_STREAM_THREADS) / 64;
+constexpr int kMaxWaves = (kRowThreadsRegs > kRowThreadsStream ? kRowThreadsRegs : kRowThreadsStream) / 64;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -699,7 +687,7 @@ int ce_rows_launch(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int6
   if (rows == 0) return TM_OK;
   if (!d_logits || !d_labels || !d_row_loss) return ce_fail(TM_EINVAL, "%s: null pointer", who);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool regs = TM_CE_REG_ROWS && (vocab >> 3) <= static_cast<int64_t>(kRowThreadsRegs) * kRegCols;
+  const bool regs = (vocab >> 3) <= static_cast<int64_t>(kRowThreadsRegs) * kRegCols;
   // a launch holds fewer than 2^32 work-items: longer row lists (small vocabularies in one
   // chunk) go in several launches
   const int64_t max_rows = 0xFFFFFFFFll / (regs ? kRowThreadsRegs : kRowThreadsStream);
@@ -711,7 +699,7 @@ int ce_rows_launch(uint16_t* d_logits, int64_t ld, const int64_t* d_labels, int6
                          lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
     else
       hipLaunchKernelGGL((ce_rows_kernel<false, kRowThreadsStream, kGrad>), dim3(nr), dim3(kRowThreadsStream),
-                         kStreamLds, s, lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
+                         0, s, lg, ld, d_labels + r0, vocab, ignore_index, d_row_loss + r0);
     if (int rc = ce_check_launch(who)) return rc;
   }
   return TM_OK;
