@@ -47,7 +47,7 @@ def _run_step(host, *, max_norm=1.0, grad_on_master=False):
 
 
 def test_tiny_config_step_matches_oracle():
-    """Config 1 (tiny Qwen3 set, fresh state, clip triggers at norm ~1.62)."""
+    """The tiny Qwen3-style set (fresh state, clip triggers at norm ~1.62)."""
     host = H.make_host_set(shapes_for("tiny"), seed=1, steady=False)
     params, work, opt, norm, coef = _run_step(host)
     tens = H.oracle_tensors(host)
@@ -119,8 +119,8 @@ def test_norm_vs_fp64_and_deterministic():
 
 
 def test_steady_state_no_clip_config2():
-    """Config 2 shape family (steady state, step 1000 -> 1001), grads rescaled so
-    the global norm is 0.5 and the clip does not trigger (coef exactly 1)."""
+    """The steady state (step 1000 -> 1001, m ~ N(0,1e-4), v = |N|*1e-8) with grads rescaled
+    so the global norm is 0.5 and the clip does not trigger (coef exactly 1)."""
     shapes = shapes_for("tiny")
     host = H.make_host_set(shapes, seed=4)
     total = np.sqrt(sum(oracle.sumsq(h["g"]) for h in host))
@@ -135,7 +135,7 @@ def test_steady_state_no_clip_config2():
 
 
 def test_ragged_three_chained_steps():
-    """Config 5 in miniature: odd lengths (scalar tail), 1-D no-decay tensors,
+    """The ragged list in miniature: odd lengths (scalar tail), 1-D no-decay tensors,
     all-zero grads, three chained steps with drift checked every step."""
     shapes = ragged_shapes(n_tensors=300, max_log2=16, seed=9)
     host = H.make_host_set(shapes, seed=5, zero_grad_every=100)
@@ -164,7 +164,7 @@ def test_ragged_three_chained_steps():
 
 
 def test_fp32_accumulated_grads_config3():
-    """Config 3 in miniature: 4 bf16 micro-grads summed into fp32 buffers by the
+    """Grad accumulation in miniature: 4 bf16 micro-grads summed into fp32 buffers by the
     accumulate kernel, scaled to global norm 5 (clip coef ~0.2), WSD lr at the
     decay-phase step 9800 of T=10000 (lr = 3e-4 * 0.1)."""
     import torchure_amd as ta
@@ -596,11 +596,11 @@ def test_full_size_properties(config):
 
 @pytest.mark.parametrize("config", ["qwen3-0.6b", "qwen3-4b"])
 def test_full_size_steady_state(config):
-    """BASELINE configs 2 and 4 at full size, from the steady state the reference step runs in
-    (torchure/train/trainer.py:391-397): state['step'] 1000 (the kernel uses t = 1001),
-    m ~ N(0, 1e-4), v = |N(0,1)| * 1e-8, masters ~ N(0, 0.02). Config 2 rescales its bf16 grads
-    to global norm 0.5, so clip 1.0 does not trigger (the coefficient is exactly 1.0); config 4
-    keeps N(0, 1e-3) grads, whose norm (~63) does trigger it. The norm is checked against fp64
+    """The Qwen3-0.6B and Qwen3-4B parameter sets at full size, from the steady state the
+    reference step runs in (torchure/train/trainer.py:391-397): state['step'] 1000 (the kernel
+    uses t = 1001), m ~ N(0, 1e-4), v = |N(0,1)| * 1e-8, masters ~ N(0, 0.02). The 0.6B set
+    rescales its bf16 grads to global norm 0.5, so clip 1.0 does not trigger (the coefficient is
+    exactly 1.0); the 4B set keeps N(0, 1e-3) grads, whose norm (~63) does trigger it. The norm is checked against fp64
     over every grad, the bf16 copy against torch's cast everywhere, and sampled tensors -- the
     tied embedding (the largest) among them -- bit for bit against the oracle: master, m, v,
     bf16 copy and step counter."""
@@ -612,7 +612,7 @@ def test_full_size_steady_state(config):
     work = ta.attach_bf16_working_params(params)
     for w in work:
         w.grad = (torch.randn(w.shape, device=DEV, generator=g) * 1e-3).to(torch.bfloat16)
-    if config == "qwen3-0.6b":  # config 2: "clip not triggered" -> global norm 0.5
+    if config == "qwen3-0.6b":  # the 0.6B steady state has the clip not triggered: norm 0.5
         sq = sum(float(torch.sum(w.grad.double() ** 2).item()) for w in work)
         scale = 0.5 / math.sqrt(sq)
         for w in work:
@@ -660,7 +660,7 @@ def test_full_size_steady_state(config):
 
 
 def test_accumulate_list_fused_norm_and_reuse():
-    """Row (f)1: 4 bf16 micro-steps accumulated into fp32 .grad in one launch each;
+    """Micro-step accumulation: 4 bf16 micro-steps accumulated into fp32 .grad in one launch each;
     the last also yields the global norm, bit-identical to the standalone norm pass,
     and clip_grad_norm reuses it; the step then matches the oracle bit for bit."""
     import torchure_amd as ta
@@ -745,7 +745,7 @@ def test_accumulate_rejects_before_touching_any_grad():
 
 
 def test_ragged_full_size_three_chained_steps():
-    """Config 5 at full size: 10,000 tensors, ~1.02e10 elements (~163 GB resident),
+    """The ragged list at full size: 10,000 tensors, ~1.02e10 elements (~163 GB resident),
     ~30% odd lengths, 40% 1-D (no decay), 1% all-zero grads; three chained steps.
     Size-independent checks on every tensor (norm vs fp64, bf16 copy = torch's cast
     of the master, step counters) and bit-exact oracle checks on a sample that covers
@@ -1519,7 +1519,7 @@ def test_tensor_beyond_2_31_elements():
 
 
 def test_full_size_config3_fp32_accumulation():
-    """Config 3 at full size (Qwen3-0.6B shapes, 596M params): four bf16 micro-steps
+    """Grad accumulation at full size (Qwen3-0.6B shapes, 596M params): four bf16 micro-steps
     accumulated into fp32 .grad (the last one also measuring the norm), grads scaled
     so the global norm is ~5 and the clip triggers, WSD lr at decay step 9800. The
     fused norm equals the standalone norm pass bit for bit and fp64 within 1e-6;
