@@ -659,6 +659,56 @@ def test_full_size_steady_state(config):
         assert st["step"].item() == 1001.0
 
 
+
+@pytest.mark.parametrize("config", ["qwen3-0.6b", "qwen3-4b"])
+def test_full_size_every_element_matches_torch_rocm_fused_adamw(config):
+    """Every element of a full-size step (596M / 4.02B params, steady state, bf16 grads, clip 1.0
+    triggered) against torch.optim.AdamW(fused=True) on the same GPU -- the reference's own
+    optimizer -- fed the same inputs the reference trainer would give it: fp32 grads equal to the
+    widened bf16 grads, scaled in place by the same clip coefficient (torch._foreach_mul_, the
+    reference's clip). Masters, m, v and step counters bit for bit on every element, and the bf16
+    working copies equal to torch's cast of torch's masters."""
+    import torchure_amd as ta
+
+    shapes = shapes_for(config)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    params = [torch.nn.Parameter(torch.randn(s, device=DEV, generator=g) * 0.02) for s in shapes]
+    work = ta.attach_bf16_working_params(params)
+    for w in work:
+        w.grad = (torch.randn(w.shape, device=DEV, generator=g) * 1e-3).to(torch.bfloat16)
+    opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
+                             {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True})
+    for p in params:
+        st = opt.state[p]
+        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=DEV)
+        st["exp_avg"] = torch.randn(p.shape, device=DEV, generator=g) * 1e-4
+        st["exp_avg_sq"] = torch.randn(p.shape, device=DEV, generator=g).abs_() * 1e-8
+    ref = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    topt = torch.optim.AdamW([{"params": [q for q in ref if q.dim() >= 2], "weight_decay": 0.1},
+                              {"params": [q for q in ref if q.dim() < 2], "weight_decay": 0.0}],
+                             lr=3e-4, betas=(0.9, 0.95), eps=1e-8, fused=True)
+    for p, q, w in zip(params, ref, work):
+        q.grad = w.grad.float()
+        st, tst = opt.state[p], topt.state[q]
+        tst["step"] = st["step"].clone()
+        tst["exp_avg"] = st["exp_avg"].clone()
+        tst["exp_avg_sq"] = st["exp_avg_sq"].clone()
+    norm = ta.clip_grad_norm(params, None, 1.0)
+    coef = opt._pending[0].clone()
+    opt.step()
+    torch._foreach_mul_([q.grad for q in ref], coef)
+    topt.step()
+    torch.cuda.synchronize()
+    assert norm.item() > 1.0 and coef.item() < 1.0  # the clip triggered
+    i32 = torch.int32
+    for i, (p, q, w) in enumerate(zip(params, ref, work)):
+        st, tst = opt.state[p], topt.state[q]
+        assert torch.equal(p.detach().view(i32), q.detach().view(i32)), i
+        assert torch.equal(st["exp_avg"].view(i32), tst["exp_avg"].view(i32)), i
+        assert torch.equal(st["exp_avg_sq"].view(i32), tst["exp_avg_sq"].view(i32)), i
+        assert st["step"].item() == tst["step"].item() == 1001.0
+        assert torch.equal(w.detach().view(torch.int16), q.detach().to(torch.bfloat16).view(torch.int16)), i
+
 def test_accumulate_list_fused_norm_and_reuse():
     """Micro-step accumulation: 4 bf16 micro-steps accumulated into fp32 .grad in one launch each;
     the last also yields the global norm, bit-identical to the standalone norm pass,
