@@ -783,10 +783,12 @@ def test_fp32_weight_with_current_working_copy():
     reads it instead of casting the master, with the cast's bits (loss, grad_h and grad_W equal a
     weight without a copy, bit for bit, training and loss-only); the copy really is what the op
     reads (bytes overwritten behind autograd's back change the loss, and a refresh restores it);
-    a master modified in place makes the copy stale and the op casts again."""
+    a master modified in place makes the copy stale and the op casts again; after AdamW.step()
+    the copy is current again, and a copy modified in place through torch is not taken."""
     import torchure_amd as ta
     from torchure_amd import _native
     from torchure_amd.loss import fused_linear_cross_entropy
+    from torchure_amd.optimizer.working import current_copy
 
     g = torch.Generator(device=DEV).manual_seed(31)
     n, d, v = 1500, 256, 6000
@@ -829,4 +831,18 @@ def test_fp32_weight_with_current_working_copy():
     _native.check(_native.lib().tm_stream_copy(copy.data_ptr(), junk.data_ptr(), junk.numel() * 2,
                                                _native.stream_handle(DEV)), "tm_stream_copy")
     torch.cuda.synchronize()
+    assert same(run(master), run(plain))
+    # AdamW.step() writes the copy with the master, so the op reads it again afterwards
+    ta.refresh_bf16_working_params([master])
+    opt = ta.AdamW([master], lr=1e-3, fused=True)
+    master.grad = torch.randn(v, d, device=DEV, generator=g) * 1e-3
+    opt.step()
+    with torch.no_grad():
+        plain.copy_(master)
+    assert current_copy(master) is copy
+    assert same(run(master), run(plain))
+    # a copy changed in place through torch is no longer taken for the cast
+    with torch.no_grad():
+        copy.add_(1.0)
+    assert current_copy(master) is None
     assert same(run(master), run(plain))

@@ -344,3 +344,33 @@ def test_fused_ce_grad_h_gemm_choice():
     assert splitk_grad_h_fits(1024, 4096, v) and not splitk_grad_h_fits(2048, 4096, v)
     assert not splitk_grad_h_fits(1000, 1024, v) and not splitk_grad_h_fits(1024, 1000, v)
     assert not splitk_grad_h_fits(1024, 1024, 151937) and not splitk_grad_h_fits(0, 1024, v)
+
+
+def test_working_copy_freshness_rule():
+    """``current_copy`` hands out an attached bf16 copy only while it still holds RNE(master):
+    an in-place change of the master or of the copy itself (seen through their autograd
+    version counters) makes readers cast the master again."""
+    from torchure_amd.optimizer.working import current_copy, mark_current
+
+    p = torch.randn(8, 4)
+    w = p.to(torch.bfloat16)
+    assert current_copy(p) is None  # nothing attached
+    p._tm_working = w
+    assert current_copy(p) is None  # attached but never marked
+    mark_current(p, w)
+    assert current_copy(p) is w
+    w.add_(1)  # the copy written outside attach / refresh / step
+    assert current_copy(p) is None
+    w.copy_(p)
+    mark_current(p, w)
+    assert current_copy(p) is w
+    p.mul_(2)  # the master changed: the copy is stale
+    assert current_copy(p) is None
+    mark_current(p, w)
+    p2 = p.detach().clone()
+    p2._tm_working = w.view(4, 8)  # wrong shape
+    mark_current(p2, p2._tm_working)
+    assert current_copy(p2) is None
+    p3 = p.double()
+    p3._tm_working = w
+    assert current_copy(p3) is None  # not an fp32 master

@@ -624,6 +624,7 @@ class StepLaunch:
         for e in self.pairs:  # the bump above made each master's version one higher
             e.expect += 1
             e.work._tm_master_version = e.expect
+            e.work._tm_copy_version = e.work._version
 
 
 def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out: bool = True) -> int:

@@ -70,8 +70,9 @@ def _cast_list(masters, copies, device) -> None:
 
 
 def mark_current(p: torch.Tensor, w: torch.Tensor) -> None:
-    """Record that ``w`` holds RNE(``p``) as of ``p``'s current autograd version."""
+    """Record that ``w`` holds RNE(``p``) as of ``p``'s and ``w``'s current autograd versions."""
     w._tm_master_version = p._version
+    w._tm_copy_version = w._version
 
 
 def is_current(p: torch.Tensor, w: torch.Tensor) -> bool:
@@ -81,12 +82,13 @@ def is_current(p: torch.Tensor, w: torch.Tensor) -> bool:
 
 def current_copy(p: torch.Tensor) -> torch.Tensor | None:
     """``p``'s attached bf16 working copy if it holds RNE(``p``) now, else None: the copy has
-    ``p``'s shape and device and ``p`` has not been modified in place since the copy was last
-    written (by attach, refresh or ``AdamW.step()``), the test the step itself applies. Its bits
-    are then those of ``p.to(torch.bfloat16)``, so a reader may take it instead of casting."""
+    ``p``'s shape and device, and neither ``p`` nor the copy has been modified in place since
+    the copy was last written (by attach, refresh or ``AdamW.step()``). Its bits are then those
+    of ``p.to(torch.bfloat16)``, so a reader may take it instead of casting."""
     w = getattr(p, "_tm_working", None)
     if (w is None or p.dtype != torch.float32 or w.dtype != torch.bfloat16 or w.shape != p.shape
-            or w.device != p.device or not w.is_contiguous() or not is_current(p, w)):
+            or w.device != p.device or not w.is_contiguous() or not is_current(p, w)
+            or getattr(w, "_tm_copy_version", None) != w._version):
         return None
     return w
 
