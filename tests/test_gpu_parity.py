@@ -2042,3 +2042,131 @@ def test_fused_and_standalone_norm_partials_bit_equal(chunk_elems):
     assert norm_a.view(torch.int32).item() == norm_b.view(torch.int32).item()
     exact = math.fsum(float((a.double() ** 2).sum()) for a in accs)
     assert abs(float(part_a.sum()) - exact) <= 1e-12 * exact
+
+
+def _views_at_phases(specs, seed, chunk_elems=None):
+    """Tensors as views of one pool per role (master, m, v fp32; grad and working copy bf16, or
+    an fp32 grad on the master), each placed so that its fp32 views start the given number of
+    elements past a 1 KiB boundary. ``specs``: (numel, {role: elements past 1 KiB}, fp32 grad).
+    Every view is surrounded by guard elements holding a sentinel. Returns the pools, the views
+    and the host state."""
+    import torchure_amd as ta
+    from torchure_amd.optimizer.working import mark_current
+
+    host = H.make_host_set([(n,) for n, _, _ in specs], seed=seed)
+    for h, (_, _, f32) in zip(host, specs):
+        h["wd"] = H.WD  # every view is stepped in the decay group (one-element tensors included)
+        if f32:
+            h["g"] = oracle.bf16_to_f32(h["g"]).copy()
+    gap = 1024  # guard elements between views (a multiple of 256)
+    offs, total = [], gap
+    for n, _, _ in specs:
+        offs.append(total)
+        total += (n + 256 + gap + 255) // 256 * 256
+    pools = {r: torch.full((total,), float("nan"), device=DEV) for r in ("p", "m", "v", "gf")}
+    pools["g"] = torch.full((total,), 7.0, device=DEV).to(torch.bfloat16)
+    pools["w"] = torch.full((total,), 7.0, device=DEV).to(torch.bfloat16)
+
+    def view(role, i, n, lead):
+        pool = pools[role]
+        base = pool.data_ptr() // pool.element_size()
+        shift = (lead - (base + offs[i])) % 256 if role in ("p", "m", "v", "gf") else lead
+        return pool[offs[i] + shift: offs[i] + shift + n]
+
+    params, work, grads = [], [], []
+    for i, ((n, leads, f32), h) in enumerate(zip(specs, host)):
+        pv = view("p", i, n, leads.get("p", 0))
+        pv.copy_(torch.from_numpy(h["p"]))
+        p = torch.nn.Parameter(pv)
+        w = view("w", i, n, leads.get("w", 0))
+        w.copy_(pv.to(torch.bfloat16))
+        p._tm_working = w
+        if f32:
+            g = view("gf", i, n, leads.get("g", 0))
+            g.copy_(torch.from_numpy(h["g"]))
+            p.grad = g
+        else:
+            g = view("g", i, n, leads.get("g", 0))
+            g.copy_(H.to_dev_bf16(h["g"], (n,), DEV))
+            w.grad = g
+        params.append(p)
+        work.append(w)
+    opt = ta.AdamW([{"params": params, "weight_decay": H.WD}], lr=H.HYPER["lr"],
+                   betas=(H.HYPER["beta1"], H.HYPER["beta2"]), fused=True,
+                   **({"chunk_elems": chunk_elems} if chunk_elems else {}))
+    for i, ((n, leads, _), p, h) in enumerate(zip(specs, params, host)):
+        st = opt.state[p]
+        st["step"] = torch.tensor(h["step"], dtype=torch.float32, device=DEV)
+        st["exp_avg"] = view("m", i, n, leads.get("m", 0))
+        st["exp_avg"].copy_(torch.from_numpy(h["m"]))
+        st["exp_avg_sq"] = view("v", i, n, leads.get("v", 0))
+        st["exp_avg_sq"].copy_(torch.from_numpy(h["v"]))
+    # views of one pool share one autograd version counter: mark the copies current only
+    # after the last write into the pools
+    for p, w in zip(params, work):
+        mark_current(p, w)
+    torch.cuda.synchronize()
+    return pools, params, work, opt, host
+
+
+@pytest.mark.parametrize("chunk_elems", [None, 2048])
+def test_views_off_their_1kib_boundaries_match_oracle(chunk_elems):
+    """The update lays each tensor's slices on its fp32 arrays' 1 KiB boundaries, wrapping the
+    last elements into the first slice's head. Tensors whose fp32 views start 4 to 252 elements
+    past such a boundary, with master, m and v at a shared phase or at different ones, lengths
+    that make the wrap take 0, some or all of the head (a whole number of chunks, one element
+    past, odd lengths, tensors shorter than the head), an fp32 grad, and a view off 16 bytes
+    (element at a time): every element bit for bit against the oracle after a clipped step and
+    after a second, unclipped one (the masters are views of one buffer and share one autograd
+    version counter, which the working-copy bookkeeping has to follow), and no element outside
+    the views written."""
+    import torchure_amd as ta
+
+    ce = chunk_elems or 16384
+    specs = []
+    for ph in (4, 64, 128, 252):
+        for n in (1, 3, 5, 100, 252 - ph + 4, 255, 256, 257, ce - ph, ce - ph + 1, ce, ce + 7,
+                  3 * ce + 130, 2 * ce - 3, 40003):
+            specs.append((n, dict(p=ph, m=ph, v=ph, g=ph, w=ph), False))
+    specs += [
+        (5 * ce + 77, dict(p=64, m=128, v=128), False),  # m and v agree: their phase
+        (5 * ce + 77, dict(p=64, m=64, v=128), False),  # master's phase
+        (5 * ce + 77, dict(p=4, m=128, v=252), False),  # all differ: master's phase
+        (3 * ce + 11, dict(p=128, m=128, v=128, g=64), True),  # fp32 grad at another phase
+        (3 * ce + 11, dict(p=64, m=128, v=128, g=64), True),  # fp32 grad siding with the master
+        (2 * ce + 9, dict(p=1, m=1, v=1), False),  # 4 bytes off: element at a time
+        (4 * ce, dict(p=0, m=0, v=0), False),  # on the boundary
+    ]
+    pools, params, work, opt, host = _views_at_phases(specs, seed=77, chunk_elems=chunk_elems)
+    print(f"phase views: {len(specs)} tensors, chunk_elems {ce}", flush=True)
+    norm = ta.clip_grad_norm(params, None, 0.05)
+    coef = float(opt._pending[0].item())
+    assert coef < 1.0
+    opt.step()
+    torch.cuda.synchronize()
+    tens = H.oracle_tensors(host)
+    ref_norm, _ = oracle.reference_step(tens, H.HYPER, 0.05, clip_override=coef)
+    assert abs(float(norm.item()) - float(ref_norm)) <= 1e-6 * float(ref_norm)
+    w = H.compare_state(params, work, opt, tens)
+    assert w == {"p": 0, "m": 0, "v": 0, "bf16": 0, "step": 0}, w
+    opt.step()  # same grads, no clip
+    torch.cuda.synchronize()
+    oracle.reference_step(tens, H.HYPER, None)
+    w = H.compare_state(params, work, opt, tens)
+    assert w == {"p": 0, "m": 0, "v": 0, "bf16": 0, "step": 0}, w
+
+    # the guards: everything outside the views still holds its sentinel
+    for role, pool in pools.items():
+        mask = torch.ones(pool.numel(), dtype=torch.bool, device=DEV)
+        for i, p in enumerate(params):
+            t = {"p": p, "m": opt.state[p]["exp_avg"], "v": opt.state[p]["exp_avg_sq"],
+                 "w": work[i], "g": work[i].grad, "gf": p.grad}[role]
+            if t is None or t.untyped_storage().data_ptr() != pool.untyped_storage().data_ptr():
+                continue
+            o = t.storage_offset()
+            mask[o: o + t.numel()] = False
+        rest = pool[mask]
+        if pool.dtype == torch.float32:
+            assert torch.isnan(rest).all(), role
+        else:
+            assert (rest.float() == 7.0).all(), role

@@ -374,3 +374,37 @@ def test_working_copy_freshness_rule():
     p3 = p.double()
     p3._tm_working = w
     assert current_copy(p3) is None  # not an fp32 master
+
+
+def test_host_version_stamps_follow_shared_counters():
+    """``stamp`` records each master's and copy's current autograd version on the copy and
+    ``stamped`` compares them again; masters that are views of one buffer share one counter,
+    so bumping all of them raises each one's version by their number, and the stamps taken
+    after the bumps (what the step does) still match."""
+    from torchure_amd import _native
+    from torchure_amd.optimizer.working import current_copy
+
+    h = _native.host()
+    pool = torch.zeros(12)
+    ps = [torch.nn.Parameter(pool[4 * i: 4 * i + 4]) for i in range(3)]
+    cpool = torch.zeros(12, dtype=torch.bfloat16)
+    ws = [cpool[4 * i: 4 * i + 4] for i in range(3)]
+    for p, w in zip(ps, ws):
+        p._tm_working = w
+    assert not h.stamped(ps, ws)  # never stamped
+    h.stamp(ps, ws)
+    assert h.stamped(ps, ws)
+    assert all(w._tm_master_version == p._version and w._tm_copy_version == w._version
+               for p, w in zip(ps, ws))
+    assert all(current_copy(p) is w for p, w in zip(ps, ws))
+    v0 = ps[0]._version
+    h.bump(ps + ws)  # what a step does after writing masters and copies
+    assert ps[0]._version == v0 + 3 and ps[2]._version == v0 + 3  # one counter for the pool
+    assert not h.stamped(ps, ws)
+    h.stamp(ps, ws)
+    assert h.stamped(ps, ws) and all(current_copy(p) is w for p, w in zip(ps, ws))
+    with torch.no_grad():
+        ps[1].add_(1)  # any in-place write into the pool makes every copy of it stale
+    assert not h.stamped(ps, ws) and current_copy(ps[0]) is None
+    with pytest.raises(ValueError):
+        h.stamp(ps, ws[:2])

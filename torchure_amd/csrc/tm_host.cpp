@@ -15,6 +15,7 @@
 
 #include <cstdint>
 #include <stdexcept>
+#include <utility>
 
 namespace py = pybind11;
 
@@ -187,6 +188,52 @@ void bump(const py::list& ts) {
     if (const at::Tensor* t = tensor_or_null(list_item(ts, i))) torch::autograd::impl::bump_version(*t);
 }
 
+// Working-copy bookkeeping: works[i]._tm_master_version = params[i]._version and
+// works[i]._tm_copy_version = works[i]._version, the versions read now. Views of one buffer
+// share one counter, so a step that bumps several such masters raises each one's version by
+// more than one: the versions are read back after the bumps rather than counted.
+void stamp(const py::list& params, const py::list& works) {
+  const Py_ssize_t n = PyList_GET_SIZE(params.ptr());
+  if (PyList_GET_SIZE(works.ptr()) != n) throw py::value_error("params and works differ in length");
+  static PyObject* k_master = PyUnicode_InternFromString("_tm_master_version");
+  static PyObject* k_copy = PyUnicode_InternFromString("_tm_copy_version");
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    const at::Tensor* p = tensor_or_null(list_item(params, i));
+    const at::Tensor* w = tensor_or_null(list_item(works, i));
+    if (!p || !w) throw py::value_error("torchure_amd._tm_host.stamp: None in a pair");
+    for (auto [key, t] : {std::pair{k_master, p}, std::pair{k_copy, w}}) {
+      PyObject* v = PyLong_FromLongLong(static_cast<long long>(t->_version()));
+      if (!v) throw py::error_already_set();
+      const int rc = PyObject_SetAttr(list_item(works, i), key, v);
+      Py_DECREF(v);
+      if (rc != 0) throw py::error_already_set();
+    }
+  }
+}
+
+// True if works[i]._tm_master_version equals params[i]._version for every i (the master has
+// not been modified in place since its working copy was last written).
+bool stamped(const py::list& params, const py::list& works) {
+  const Py_ssize_t n = PyList_GET_SIZE(params.ptr());
+  if (PyList_GET_SIZE(works.ptr()) != n) return false;
+  static PyObject* k_master = PyUnicode_InternFromString("_tm_master_version");
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    const at::Tensor* p = tensor_or_null(list_item(params, i));
+    if (!p) return false;
+    PyObject* a = PyObject_GetAttr(list_item(works, i), k_master);  // new reference
+    if (!a) {
+      if (!PyErr_ExceptionMatches(PyExc_AttributeError)) throw py::error_already_set();
+      PyErr_Clear();
+      return false;
+    }
+    const long long v = PyLong_Check(a) ? PyLong_AsLongLong(a) : -1;
+    Py_DECREF(a);
+    if (v == -1 && PyErr_Occurred()) PyErr_Clear();
+    if (v != static_cast<long long>(p->_version())) return false;
+  }
+  return true;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_tm_host, m) {
@@ -198,6 +245,8 @@ PYBIND11_MODULE(_tm_host, m) {
   m.def("dense_contiguous", &dense_contiguous, "all dense and contiguous");
   m.def("same", &same, "element-wise object identity of two lists");
   m.def("bump", &bump, "bump the autograd version of each tensor");
+  m.def("stamp", &stamp, "record each master's and working copy's current version on the copy");
+  m.def("stamped", &stamped, "every working copy's recorded master version is the master's current one");
   m.def("grad_fields", &grad_fields, "(data_ptr, numel, dtype code) of each grad");
   m.def("states_same", &states_same, "optimizer state dicts and their tensors are the given objects");
   m.def("attrs_same", &attrs_same, "getattr(obj, name, None) of each object is the given object");

@@ -8,13 +8,14 @@
 //                         sqrt and the clip coefficient, both on device.
 //   adamw_prep_kernel     one thread per tensor: step += 1, bias corrections in fp64,
 //                         per-tensor constants for the update.
-//   adamw_update_kernel   one wave per 256-element slice of a chunk: reads grad, master,
-//                         m, v once, writes master, m, v and the bf16 working copy once,
-//                         16-byte accesses.
-//   grad_scale_kernel     eager in-place clip (grad *= coef), one wave per slice.
-//   accumulate_list_kernel / accumulate_list_norm_kernel
+//   adamw_update_kernel   one wave per 256-element slice of a chunk, on a grid shifted to
+//                         the fp32 arrays' 1 KiB boundaries: reads grad, master, m, v once,
+//                         writes master, m, v and the bf16 working copy once, 16-byte accesses.
+//   grad_scale_kernel     eager in-place clip (grad *= coef), one wave per 512-element slice.
+//   accumulate_list_kernel / accumulate_list_sumsq_kernel + slice_reduce_kernel
 //                         fp32 accumulation buffers += bf16 micro-step grads over a list;
-//                         the norm variant (last micro-step) uses the norm's partition.
+//                         on the last micro-step each slice also writes its fp64 sum of
+//                         squares, which slice_reduce_kernel sums in the norm's fixed order.
 //   accumulate_kernel     one fp32 accumulation buffer += bf16 micro-step grad.
 //   cast_bf16_kernel      bf16 working copy = RNE(master).
 //
@@ -87,8 +88,16 @@ struct alignas(16) TensorScal {
   float step_size;  // float(lr / double(float(1 - beta1^step)))
   float bc2s;       // float(sqrt(1 - beta2^step))
   uint32_t decay;   // weight_decay != 0
-  uint32_t pad;
+  uint32_t mode;    // the update's per-tensor launch decisions (kMode* bits, grid phase)
 };
+
+// TensorScal::mode: bits 0-7 hold the grid phase (elements, a multiple of 4, below 256) of a
+// tensor updated with 16-byte vectors; the rest are flags.
+constexpr uint32_t kModePhase = 0xFFu;
+constexpr uint32_t kModeVec = 1u << 8;    // every array aligned for the vector path
+constexpr uint32_t kModeF32 = 1u << 9;    // fp32 grad (else bf16)
+constexpr uint32_t kModeOut = 1u << 10;   // bf16 working copy written
+constexpr uint32_t kModeClip = 1u << 11;  // TM_FLAG_CLIP set on the record
 
 constexpr size_t kPartialBytes = sizeof(double) * TM_NORM_PARTIALS;
 
@@ -605,6 +614,30 @@ struct HyperArgs {
 };
 
 // step += 1 and the per-tensor constants (fused_adam_utils.cuh:128-139; adam.py:877).
+// Elements from the 1 KiB boundary at or before a 16-byte aligned fp32 array's start to that
+// start (a multiple of 4, below kSlice): element e sits e + phase elements past the boundary.
+__device__ __forceinline__ uint32_t fp32_phase(uint64_t a) {
+  return static_cast<uint32_t>((a >> 2) & static_cast<uint64_t>(kSlice - 1));
+}
+
+// The update's decisions for one tensor, made once here instead of in each of its slices'
+// workgroups: whether all its arrays take 16-byte vectors, its grad type, whether a bf16 copy
+// is written, its clip flag, and its grid phase (adamw_update_kernel): the phase of the
+// master, or that of m and v where those two agree and outvote it.
+__device__ __forceinline__ uint32_t update_mode(const tm_tensor_t& d) {
+  const bool f32 = (d.flags & TM_GRAD_F32) != 0;
+  const bool out = d.param_bf16 != 0;
+  uint32_t mode = (f32 ? kModeF32 : 0u) | (out ? kModeOut : 0u) | ((d.flags & TM_FLAG_CLIP) ? kModeClip : 0u);
+  const bool grad_ok = f32 ? aligned16(d.grad) : aligned8(d.grad);
+  if (aligned16(d.master) && aligned16(d.exp_avg) && aligned16(d.exp_avg_sq) && grad_ok &&
+      (!out || aligned8(d.param_bf16))) {
+    const uint32_t pp = fp32_phase(d.master), pm = fp32_phase(d.exp_avg), pv = fp32_phase(d.exp_avg_sq);
+    const bool mv = pm == pv && pp != pm && !(f32 && fp32_phase(d.grad) == pp);
+    mode |= kModeVec | (mv ? pm : pp);
+  }
+  return mode;
+}
+
 __global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
     const tm_tensor_t* __restrict__ tensors, int64_t n_tensors, HyperArgs hyper,
     TensorScal* __restrict__ scal) {
@@ -620,7 +653,8 @@ __global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
     // constants make the update write NaN into its master, moments and bf16 copy.
     const double nan = __builtin_nan("");
     *step_p = __builtin_nanf("");
-    scal[t] = TensorScal{nan, nan, nan, nan, nan, nan, __builtin_nanf(""), __builtin_nanf(""), 1u, 0u};
+    scal[t] = TensorScal{nan, nan, nan, nan, nan, nan, __builtin_nanf(""), __builtin_nanf(""), 1u,
+                         (d.param_bf16 != 0 ? kModeOut : 0u) | ((d.flags & TM_GRAD_F32) ? kModeF32 : 0u)};
     return;
   }
   const tm_hyper_t h = hyper.g[gi];
@@ -639,16 +673,17 @@ __global__ __launch_bounds__(kThreads) void adamw_prep_kernel(
   s.step_size = static_cast<float>(h.lr / static_cast<double>(bc1f));
   s.bc2s = static_cast<float>(sqrt(bc2));
   s.decay = h.weight_decay != 0.0;
-  s.pad = 0;
+  s.mode = update_mode(d);
   scal[t] = s;
 }
 
 // ------------------------------------------------------------------- AdamW update
 
 // Lane mapping. A lane owns one group of 4 consecutive elements: lane t of the wave that
-// covers a slice starting at `start` takes [start + 4t, +4). Each load or store instruction
-// of the wave is one contiguous span (1 KiB of an fp32 array, 512 B of a bf16 array), whole
-// cache lines, so the stores never leave partially written lines behind. All accesses are
+// covers a slice starting at virtual position `start` takes [start + 4t - ph, +4), ph being
+// the tensor's grid phase (below). Each load or store instruction of the wave is one
+// contiguous span (1 KiB of an fp32 array, 512 B of a bf16 array) of whole cache lines when
+// the arrays sit on those boundaries, so the stores leave no partially written lines behind. All accesses are
 // non-temporal: the streams are touched once (measured 7% faster than temporal accesses).
 struct Group4 {
   f32x4 p, m, v;
@@ -729,6 +764,40 @@ __device__ __forceinline__ void update_scalar(const tm_tensor_t& d, int64_t star
   }
 }
 
+// The elements [e, n) of one lane's last, partial group of 4 (a tensor whose length is not
+// a multiple of 4), element by element by that lane alone.
+__device__ __forceinline__ void update_lane_tail(const tm_tensor_t& d, int64_t e, int64_t n,
+                                                 const TensorScal& c, bool clip, float coef) {
+  float* P = reinterpret_cast<float*>(d.master);
+  float* M = reinterpret_cast<float*>(d.exp_avg);
+  float* V = reinterpret_cast<float*>(d.exp_avg_sq);
+  uint16_t* O = reinterpret_cast<uint16_t*>(d.param_bf16);
+  const bool f32 = (d.flags & TM_GRAD_F32) != 0;
+  for (int64_t i = e; i < n; ++i) {
+    float g = f32 ? reinterpret_cast<const float*>(d.grad)[i]
+                  : bf16_at(reinterpret_cast<const uint16_t*>(d.grad), i);
+    if (clip) g = g * coef;
+    float p = P[i], m = M[i], v = V[i];
+    adamw_elem(p, m, v, g, c);
+    P[i] = p;
+    M[i] = m;
+    V[i] = v;
+    if (O) O[i] = static_cast<uint16_t>(bf16_rne(p));
+  }
+}
+
+// Slice grid on 1 KiB boundaries. A wave's fp32 access is one 1 KiB span per array; measured on
+// MI355X (4e9 elements, the same memory viewed at other offsets), the update runs about 1.5%
+// slower for each of master, m and v whose spans are not 1 KiB aligned (5.7% for all three),
+// while the bf16 arrays' 512-byte spans cost nothing off their boundary. So a tensor is covered
+// in a shifted grid: element e sits at virtual position e + ph, where ph is the phase (above)
+// of the master, or that of m and v where those two agree and outvote it, so that virtual
+// slice s, the elements [256 s - ph, 256 s + 256 - ph), starts on a 1 KiB boundary of the
+// arrays that have that phase. The chunk table still gives the tensor
+// ceil(n / chunk_elems) chunks, which cover virtual [0, covered) with covered = that count
+// times chunk_elems; the last L = n + ph - covered elements (L <= ph) fall past it and take the
+// first L virtual positions of slice 0, which the shift left empty. Every element lands in
+// exactly one lane's group of 4, whose fp32 addresses stay 16-byte aligned.
 __global__ __launch_bounds__(kWave) void adamw_update_kernel(
     const tm_tensor_t* __restrict__ tensors, int64_t n_tensors,
     const tm_chunk_t* __restrict__ chunks, uint32_t first_chunk, uint32_t slices_per_chunk,
@@ -738,31 +807,31 @@ __global__ __launch_bounds__(kWave) void adamw_update_kernel(
   slice_of(chunks, first_chunk, slices_per_chunk, chunk_elems, ck, start);
   if (ck.tensor >= n_tensors) return;
   const tm_tensor_t d = tensors[ck.tensor];
-  if (start >= d.numel) return;
-  const int64_t end = min(start + kSlice, d.numel);
   const TensorScal c = scal[ck.tensor];
-  const bool clip = (d.flags & TM_FLAG_CLIP) != 0 && coef_p != nullptr;
-  const float coef = clip ? *coef_p : 1.0f;
-  const bool out = d.param_bf16 != 0;
-  const bool f32 = (d.flags & TM_GRAD_F32) != 0;
-  const bool grad_ok = f32 ? aligned16(d.grad) : aligned8(d.grad);
-  const bool vec = aligned16(d.master) && aligned16(d.exp_avg) && aligned16(d.exp_avg_sq) &&
-                   grad_ok && (!out || aligned8(d.param_bf16));
-  int64_t vend = start;
-  if (vec) {
-    vend = start + ((end - start) & ~int64_t(3));
-    const int64_t e = start + static_cast<int64_t>(threadIdx.x) * 4;
-    if (e < vend) {
-      if (f32) {
-        if (out) update_group<true, true>(d, e, c, clip, coef);
-        else update_group<true, false>(d, e, c, clip, coef);
-      } else {
-        if (out) update_group<false, true>(d, e, c, clip, coef);
-        else update_group<false, false>(d, e, c, clip, coef);
-      }
-    }
+  const int64_t n = d.numel;
+  const uint32_t mode = c.mode;
+  const bool clip = (mode & kModeClip) && coef_p != nullptr;
+  if (!(mode & kModeVec)) {  // element at a time, unshifted
+    if (start >= n) return;
+    update_scalar(d, start, min(start + kSlice, n), c, clip, clip ? *coef_p : 1.0f);
+    return;
   }
-  if (vend < end) update_scalar(d, vend, end, c, clip, coef);
+  const int64_t ph = mode & kModePhase;
+  if (start - ph >= n && start > 0) return;
+  const float coef = clip ? *coef_p : 1.0f;
+  int64_t e = start + static_cast<int64_t>(threadIdx.x) * 4 - ph;
+  if (e < 0) e += (n + chunk_elems - 1) / chunk_elems * chunk_elems;  // slice 0's wrapped tail
+  if (e + 4 <= n) {
+    if (mode & kModeF32) {
+      if (mode & kModeOut) update_group<true, true>(d, e, c, clip, coef);
+      else update_group<true, false>(d, e, c, clip, coef);
+    } else {
+      if (mode & kModeOut) update_group<false, true>(d, e, c, clip, coef);
+      else update_group<false, false>(d, e, c, clip, coef);
+    }
+  } else if (e < n) {
+    update_lane_tail(d, e, n, c, clip, coef);
+  }
 }
 
 // ------------------------------------------------------- micro-step accumulation

@@ -316,16 +316,12 @@ class AdamW(torch.optim.Optimizer):
                         flags |= clip_flag
                         vsum += g._version
                         matched.append(k)
-                if work is not None:
-                    v = p._version
-                    if v != ent.expect:
-                        if getattr(work, "_tm_master_version", None) != v:
-                            raise RuntimeError(
-                                "torchure_amd.AdamW: a fp32 master was modified in place since its "
-                                "bf16 working copy was last written, so the forward ran on stale "
-                                "weights; call torchure_amd.refresh_bf16_working_params(params) "
-                                "after changing masters (e.g. after model.load_state_dict)")
-                        ent.expect = v
+                if work is not None and getattr(work, "_tm_master_version", None) != p._version:
+                    raise RuntimeError(
+                        "torchure_amd.AdamW: a fp32 master was modified in place since its "
+                        "bf16 working copy was last written, so the forward ran on stale "
+                        "weights; call torchure_amd.refresh_bf16_working_params(params) "
+                        "after changing masters (e.g. after model.load_state_dict)")
                 bucket = per_dev.get(ent.device)
                 if bucket is None:
                     bucket = per_dev[ent.device] = ([], [], [])
@@ -381,10 +377,8 @@ class AdamW(torch.optim.Optimizer):
             return None
         if not host.states_same(self.state, plan.params, plan.states, plan.ms, plan.vs, plan.ss):
             return None
-        if plan.wents:
-            want = np.fromiter((e.expect for e in plan.wents), dtype=np.int64, count=len(plan.wents))
-            if not np.array_equal(host.versions(plan.wparams), want):
-                return None
+        if plan.wparams and not host.stamped(plan.wparams, plan.wworks):
+            return None
         flags = plan.flags
         if coef is not None and clip_ids:
             if not isinstance(clip_ids, _ClipRecord) or len(clip_ids.grads) != len(gl):
@@ -410,7 +404,7 @@ class AdamW(torch.optim.Optimizer):
         tables.make_ready(plan.chunks, device)
         return [StepLaunch(device, self._uploader(rows, device), plan.n, plan.chunks, plan.n_chunks,
                            self.chunk_elems, _native.hyper_array(hyper), len(hyper), coef,
-                           plan.written, plan.wents)]
+                           plan.written, (plan.wparams, plan.wworks))]
 
     def _verify_param(self, p: torch.Tensor, state: dict, work) -> "_ParamEntry":
         """Full checks of a param, its working copy and its state (created lazily,
@@ -464,7 +458,8 @@ class AdamW(torch.optim.Optimizer):
                 raise RuntimeError("torchure_amd.AdamW: clip coefficient on another device")
             chunks, n_chunks = tables.CHUNKS.get(rows["numel"], self.chunk_elems, device)
             launch = StepLaunch(device, self._uploader(rows, device), n, chunks, n_chunks,
-                                self.chunk_elems, groups_c, len(hyper), coef, written, pairs)
+                                self.chunk_elems, groups_c, len(hyper), coef, written,
+                                ([e.param for e in pairs], [e.work for e in pairs]))
             launch.host_rows = rows.tobytes()
             out.append(launch)
         return out
@@ -503,7 +498,7 @@ class _ParamEntry:
     """Verified per-param record: the objects it was built from and their pointers."""
 
     __slots__ = ("param", "work", "step", "m", "v", "p_ptr", "m_ptr", "v_ptr", "s_ptr", "w_ptr",
-                 "numel", "device", "dev_index", "written", "expect")
+                 "numel", "device", "dev_index", "written")
 
     def __init__(self, p, work, step, m, v):
         self.param, self.work, self.step, self.m, self.v = p, work, step, m, v
@@ -518,8 +513,6 @@ class _ParamEntry:
         self.numel = p.numel()
         self.device = p.device
         self.dev_index = p.get_device()
-        # autograd version of the master when the working copy last held RNE(master)
-        self.expect = getattr(work, "_tm_master_version", None) if work is not None else None
 
 
 class _ClipRecord:
@@ -547,7 +540,7 @@ class _Plan:
     """The table of the last full step and what it was built from, for the fast path."""
 
     __slots__ = ("groups", "all_params", "all_works", "src", "params", "statics", "static_ptrs",
-                 "states", "ms", "vs", "ss", "wents", "wparams", "rows", "flags", "n", "device",
+                 "states", "ms", "vs", "ss", "wparams", "wworks", "rows", "flags", "n", "device",
                  "chunks", "n_chunks", "chunk_elems", "written", "clip_holders", "clip_perm")
 
     def __init__(self, opt: "AdamW", order: list, launch: "StepLaunch"):
@@ -565,8 +558,7 @@ class _Plan:
         self.ms = [e.m for e in ents]
         self.vs = [e.v for e in ents]
         self.ss = [e.step for e in ents]
-        self.wents = launch.pairs
-        self.wparams = [e.param for e in self.wents]
+        self.wparams, self.wworks = launch.pair_params, launch.pair_works
         self.n = launch.n
         self.device = launch.device
         self.chunks, self.n_chunks, self.chunk_elems = launch.chunks, launch.n_chunks, launch.chunk_elems
@@ -588,9 +580,10 @@ class StepLaunch:
     """
 
     def __init__(self, device, d_rows, n, chunks, n_chunks, chunk_elems, groups_c, n_groups, coef,
-                 written=(), pairs=()):
+                 written=(), pairs=((), ())):
         self.written = written if isinstance(written, list) else list(written)
-        self.pairs = pairs if isinstance(pairs, list) else list(pairs)  # entries with a working copy
+        # the masters with a working copy, and those copies
+        self.pair_params, self.pair_works = (x if isinstance(x, list) else list(x) for x in pairs)
         self.host_rows = None  # the uploaded table's bytes, when the caller keeps them
         self.device = device
         self.d_rows = d_rows
@@ -621,10 +614,8 @@ class StepLaunch:
         _native.check(rc, "tm_adamw_step")
         if self.written:
             _native.host().bump(self.written)
-        for e in self.pairs:  # the bump above made each master's version one higher
-            e.expect += 1
-            e.work._tm_master_version = e.expect
-            e.work._tm_copy_version = e.work._version
+        if self.pair_params:  # the copies now hold RNE(master) as of the versions after the bump
+            _native.host().stamp(self.pair_params, self.pair_works)
 
 
 def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out: bool = True) -> int:
