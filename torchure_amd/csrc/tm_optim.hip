@@ -741,9 +741,8 @@ __device__ __forceinline__ void update_group(const tm_tensor_t& d, int64_t e, co
   store_group<kOut>(r, d, e);
 }
 
-// Element-at-a-time path: the tail of a tensor whose length is not a multiple of 4,
-// and whole tensors whose fp32 pointers are not 16-byte aligned (or bf16 pointers
-// not 8-byte aligned). Lane t takes elements start + t, start + t + 64, ...
+// Element-at-a-time path for whole tensors whose fp32 pointers are not 16-byte aligned
+// (or bf16 pointers not 8-byte aligned). Lane t takes elements start + t, start + t + 64, ...
 __device__ __forceinline__ void update_scalar(const tm_tensor_t& d, int64_t start, int64_t end,
                                               const TensorScal& c, bool clip, float coef) {
   float* P = reinterpret_cast<float*>(d.master);
