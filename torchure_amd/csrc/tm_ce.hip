@@ -537,104 +537,64 @@ __global__ __launch_bounds__(256) void ce_scale_kernel(uint16_t* __restrict__ gh
       gw[i] = gw[i] * scale;
 }
 
-// grad_W hand-over, fused_linear_ce.py:80-81,126: the fp32 accumulator gets one more
-// chunk, acc = acc + float(chunk) (kAccumulate) or acc = 0 + float(chunk) (first chunk:
-// the reference adds into a zero-filled buffer, and +0 + x also maps -0 to +0), and with
-// kTwo a second chunk after it, acc = (acc + float(chunk)) + float(chunk2), so two chunks
-// cost one pass over the accumulator. Then, with kScale (the backward of the last chunk),
-// acc *= g / n_valid. Each element sees the same fp32 operations in the same order as the
-// reference's `+=` per chunk, then `mul_`.
-
-template <bool kAccumulate, bool kScale, bool kTwo>
-__global__ __launch_bounds__(256) void ce_grad_w_kernel(float* __restrict__ acc,
-                                                        const uint16_t* __restrict__ chunk,
-                                                        const uint16_t* __restrict__ chunk2, int64_t n,
-                                                        const float* __restrict__ grad_out,
-                                                        const float* __restrict__ n_valid) {
-  const float scale = kScale ? *grad_out / *n_valid : 1.0f;
-  const uint64_t addr_bits = reinterpret_cast<uint64_t>(acc) | reinterpret_cast<uint64_t>(chunk) |
-                             (kTwo ? reinterpret_cast<uint64_t>(chunk2) : 0u);
-  const bool vec = (addr_bits & 15u) == 0;
-  const int64_t vend = vec ? (n & ~int64_t(7)) : 0;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * 8;
-  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8; i < vend; i += stride) {
-    const u32x4 w = *reinterpret_cast<const u32x4*>(chunk + i);
-    u32x4 w2 = {0u, 0u, 0u, 0u};
-    if constexpr (kTwo) w2 = *reinterpret_cast<const u32x4*>(chunk2 + i);
-    f32x4 a = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 b = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i + 4) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    a.x = a.x + lo16(w.x); a.y = a.y + hi16(w.x);
-    a.z = a.z + lo16(w.y); a.w = a.w + hi16(w.y);
-    b.x = b.x + lo16(w.z); b.y = b.y + hi16(w.z);
-    b.z = b.z + lo16(w.w); b.w = b.w + hi16(w.w);
-    if constexpr (kTwo) {
-      a.x = a.x + lo16(w2.x); a.y = a.y + hi16(w2.x);
-      a.z = a.z + lo16(w2.y); a.w = a.w + hi16(w2.y);
-      b.x = b.x + lo16(w2.z); b.y = b.y + hi16(w2.z);
-      b.z = b.z + lo16(w2.w); b.w = b.w + hi16(w2.w);
-    }
-    if (kScale) {
-      a.x = a.x * scale; a.y = a.y * scale; a.z = a.z * scale; a.w = a.w * scale;
-      b.x = b.x * scale; b.y = b.y * scale; b.z = b.z * scale; b.w = b.w * scale;
-    }
-    *reinterpret_cast<f32x4*>(acc + i) = a;
-    *reinterpret_cast<f32x4*>(acc + i + 4) = b;
-  }
-  for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * 256) {
-    float x = (kAccumulate ? acc[i] : 0.0f) + __uint_as_float(static_cast<uint32_t>(chunk[i]) << 16);
-    if constexpr (kTwo) x = x + __uint_as_float(static_cast<uint32_t>(chunk2[i]) << 16);
-    if (kScale) x = x * scale;
-    acc[i] = x;
-  }
-}
-
-// grad_W hand-over of up to kMaxFold chunks in one pass (fused_linear_ce.py:80-81 for each of
-// them in order, and :126 with kScale): acc = ((((kAccumulate ? acc : +0) + float(c[0])) +
-// float(c[1])) + ...) [* g / n_valid]. The reference's fp32 additions in its order, so the bits
-// of one `+=` per chunk, for one read and one write of the fp32 accumulator per n chunks.
+// grad_W hand-over (fused_linear_ce.py:80-81 for each chunk in order, and :126 with kScale):
+// acc = ((((kAccumulate ? acc : +0) + float(c[0])) + float(c[1])) + ...) [* g / n_valid] over
+// n chunks (1 to kMaxFold) in one pass. The reference adds each chunk into a zero-filled
+// buffer (+0 + x also maps -0 to +0), so every element sees its fp32 operations in its order:
+// the bits of one `+=` per chunk, then `mul_`, for one read and one write of the accumulator
+// per n chunks. One wave per 256-element slice and one group of 4 per lane: each load or store
+// instruction of the wave is one contiguous span (1 KiB of the fp32 accumulator, 512 B of each
+// bf16 chunk), non-temporal, as in the optimizer's update. The slice that holds the end of a
+// length not a multiple of 4, and every slice when a pointer is not aligned for the vectors,
+// goes element by element.
 constexpr int kMaxFold = 8;
 struct FoldChunks {
   const uint16_t* p[kMaxFold];
 };
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define CE_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ T ld_nt(const T* p) {
+  return __builtin_nontemporal_load((const CE_GLOBAL T*)p);
+}
+template <typename T>
+__device__ __forceinline__ void st_nt(T* p, T v) {
+  __builtin_nontemporal_store(v, (CE_GLOBAL T*)p);
+}
 
 template <bool kAccumulate, bool kScale>
-__global__ __launch_bounds__(256) void ce_grad_w_fold_kernel(float* __restrict__ acc, FoldChunks ch, int n,
-                                                             int64_t nw, const float* __restrict__ grad_out,
-                                                             const float* __restrict__ n_valid) {
+__global__ __launch_bounds__(64) void ce_grad_w_fold_kernel(float* __restrict__ acc, FoldChunks ch, int n,
+                                                            int64_t nw, int64_t first_slice,
+                                                            const float* __restrict__ grad_out,
+                                                            const float* __restrict__ n_valid) {
   const float scale = kScale ? *grad_out / *n_valid : 1.0f;
-  uint64_t addr_bits = reinterpret_cast<uint64_t>(acc);
+  uint64_t misaligned = reinterpret_cast<uint64_t>(acc) & 15u;
 #pragma unroll
   for (int c = 0; c < kMaxFold; ++c)
-    if (c < n) addr_bits |= reinterpret_cast<uint64_t>(ch.p[c]);
-  const bool vec = (addr_bits & 15u) == 0;
-  const int64_t vend = vec ? (nw & ~int64_t(7)) : 0;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * 8;
-  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 8; i < vend; i += stride) {
-    u32x4 w[kMaxFold];
+    if (c < n) misaligned |= reinterpret_cast<uint64_t>(ch.p[c]) & 7u;
+  const int64_t e = (first_slice + blockIdx.x) * 256 + static_cast<int64_t>(threadIdx.x) * 4;
+  if (misaligned == 0 && e + 4 <= nw) {
+    u32x2 w[kMaxFold];
 #pragma unroll
     for (int c = 0; c < kMaxFold; ++c)
-      if (c < n) w[c] = *reinterpret_cast<const u32x4*>(ch.p[c] + i);
-    f32x4 a = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 b = kAccumulate ? *reinterpret_cast<const f32x4*>(acc + i + 4) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (c < n) w[c] = ld_nt(reinterpret_cast<const u32x2*>(ch.p[c] + e));
+    f32x4 a = kAccumulate ? ld_nt(reinterpret_cast<const f32x4*>(acc + e)) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int c = 0; c < kMaxFold; ++c) {
       if (c < n) {
         a.x = a.x + lo16(w[c].x); a.y = a.y + hi16(w[c].x);
         a.z = a.z + lo16(w[c].y); a.w = a.w + hi16(w[c].y);
-        b.x = b.x + lo16(w[c].z); b.y = b.y + hi16(w[c].z);
-        b.z = b.z + lo16(w[c].w); b.w = b.w + hi16(w[c].w);
       }
     }
     if (kScale) {
       a.x = a.x * scale; a.y = a.y * scale; a.z = a.z * scale; a.w = a.w * scale;
-      b.x = b.x * scale; b.y = b.y * scale; b.z = b.z * scale; b.w = b.w * scale;
     }
-    *reinterpret_cast<f32x4*>(acc + i) = a;
-    *reinterpret_cast<f32x4*>(acc + i + 4) = b;
+    st_nt(reinterpret_cast<f32x4*>(acc + e), a);
+    return;
   }
-  for (int64_t i = vend + static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < nw;
-       i += static_cast<int64_t>(gridDim.x) * 256) {
+  const int64_t end = e + 4 < nw ? e + 4 : nw;
+  for (int64_t i = e; i < end; ++i) {
     float x = kAccumulate ? acc[i] : 0.0f;
 #pragma unroll
     for (int c = 0; c < kMaxFold; ++c)
@@ -724,6 +684,35 @@ int ce_rows_f32_launch(float* d_logits, int64_t ld, const int64_t* d_labels, int
   return TM_OK;
 }
 
+// One ce_grad_w_fold_kernel pass over nw elements: one 64-thread workgroup per 256-element
+// slice, over as many launches as the 2^32 work-item limit of a launch requires.
+int fold_launch(float* d_grad_w, const FoldChunks& ch, int n_chunks, int64_t nw, int accumulate,
+                const float* d_grad_out, const float* d_n_valid, void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool scale = d_grad_out != nullptr;
+  const int64_t slices = (nw + 255) / 256;
+  constexpr int64_t kMaxSlicesPerLaunch = int64_t(1) << 25;  // 2^31 work-items
+  for (int64_t first = 0; first < slices; first += kMaxSlicesPerLaunch) {
+    const int64_t count = slices - first < kMaxSlicesPerLaunch ? slices - first : kMaxSlicesPerLaunch;
+    const dim3 grid(static_cast<uint32_t>(count)), block(64);
+    if (accumulate && scale)
+      hipLaunchKernelGGL((ce_grad_w_fold_kernel<true, true>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                         first, d_grad_out, d_n_valid);
+    else if (accumulate)
+      hipLaunchKernelGGL((ce_grad_w_fold_kernel<true, false>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                         first, d_grad_out, d_n_valid);
+    else if (scale)
+      hipLaunchKernelGGL((ce_grad_w_fold_kernel<false, true>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                         first, d_grad_out, d_n_valid);
+    else
+      hipLaunchKernelGGL((ce_grad_w_fold_kernel<false, false>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
+                         first, d_grad_out, d_n_valid);
+    const int rc = ce_check_launch("ce_grad_w_fold_kernel");
+    if (rc != TM_OK) return rc;
+  }
+  return TM_OK;
+}
+
 template <bool kTwo>
 int ce_grad_w_launch(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d_chunk2, int64_t nw,
                      int accumulate, const float* d_grad_out, const float* d_n_valid, void* stream,
@@ -732,24 +721,10 @@ int ce_grad_w_launch(float* d_grad_w, const uint16_t* d_chunk, const uint16_t* d
   if (nw == 0) return TM_OK;
   if (!d_grad_w || !d_chunk || (kTwo && !d_chunk2) || (d_grad_out != nullptr) != (d_n_valid != nullptr))
     return ce_fail(TM_EINVAL, "%s: null pointer", who);
-  int64_t blocks = (nw + 256 * 8 - 1) / (256 * 8);
-  if (blocks > 65536) blocks = 65536;
-  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool scale = d_grad_out != nullptr;
-  if (accumulate && scale)
-    hipLaunchKernelGGL((ce_grad_w_kernel<true, true, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
-                       nw, d_grad_out, d_n_valid);
-  else if (accumulate)
-    hipLaunchKernelGGL((ce_grad_w_kernel<true, false, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
-                       nw, d_grad_out, d_n_valid);
-  else if (scale)
-    hipLaunchKernelGGL((ce_grad_w_kernel<false, true, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
-                       nw, d_grad_out, d_n_valid);
-  else
-    hipLaunchKernelGGL((ce_grad_w_kernel<false, false, kTwo>), grid, block, 0, s, d_grad_w, d_chunk, d_chunk2,
-                       nw, d_grad_out, d_n_valid);
-  return ce_check_launch("ce_grad_w_kernel");
+  FoldChunks ch = {};
+  ch.p[0] = d_chunk;
+  if (kTwo) ch.p[1] = d_chunk2;
+  return fold_launch(d_grad_w, ch, kTwo ? 2 : 1, nw, accumulate, d_grad_out, d_n_valid, stream);
 }
 
 int ce_grad_w_fold_launch(float* d_grad_w, const uint16_t* const* h_chunks, int n_chunks, int64_t nw,
@@ -765,24 +740,7 @@ int ce_grad_w_fold_launch(float* d_grad_w, const uint16_t* const* h_chunks, int 
     ch.p[c] = h_chunks[c];
   }
   if (nw == 0) return TM_OK;
-  int64_t blocks = (nw + 256 * 8 - 1) / (256 * 8);
-  if (blocks > 65536) blocks = 65536;
-  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool scale = d_grad_out != nullptr;
-  if (accumulate && scale)
-    hipLaunchKernelGGL((ce_grad_w_fold_kernel<true, true>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
-                       d_grad_out, d_n_valid);
-  else if (accumulate)
-    hipLaunchKernelGGL((ce_grad_w_fold_kernel<true, false>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
-                       d_grad_out, d_n_valid);
-  else if (scale)
-    hipLaunchKernelGGL((ce_grad_w_fold_kernel<false, true>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
-                       d_grad_out, d_n_valid);
-  else
-    hipLaunchKernelGGL((ce_grad_w_fold_kernel<false, false>), grid, block, 0, s, d_grad_w, ch, n_chunks, nw,
-                       d_grad_out, d_n_valid);
-  return ce_check_launch("ce_grad_w_fold_kernel");
+  return fold_launch(d_grad_w, ch, n_chunks, nw, accumulate, d_grad_out, d_n_valid, stream);
 }
 
 }  // namespace
