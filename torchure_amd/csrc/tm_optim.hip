@@ -194,13 +194,21 @@ constexpr int kUpdateLds = 13312;
 constexpr int64_t kMaxSliceBlocks = 0xFFFFFFFFll / kWave;
 
 // Chunk and first element of this workgroup's slice, in a launch that starts at chunk
-// first_chunk with slices_per_chunk = chunk_elems / kS workgroups per chunk.
+// first_chunk with slices_per_chunk = chunk_elems / kS workgroups per chunk. A power of two
+// (64 at the default chunk size) takes a shift and a mask instead of the integer division,
+// which costs about 25 instructions in every one-wave workgroup.
 template <int kS = kSlice>
 __device__ __forceinline__ void slice_of(const tm_chunk_t* __restrict__ chunks, uint32_t first_chunk,
                                          uint32_t slices_per_chunk, int64_t chunk_elems,
                                          tm_chunk_t& ck, int64_t& start) {
-  const uint32_t local = blockIdx.x / slices_per_chunk;
-  const uint32_t sub = blockIdx.x - local * slices_per_chunk;
+  uint32_t local, sub;
+  if ((slices_per_chunk & (slices_per_chunk - 1)) == 0) {
+    local = blockIdx.x >> __builtin_ctz(slices_per_chunk);
+    sub = blockIdx.x & (slices_per_chunk - 1);
+  } else {
+    local = blockIdx.x / slices_per_chunk;
+    sub = blockIdx.x - local * slices_per_chunk;
+  }
   ck = chunks[first_chunk + local];
   start = static_cast<int64_t>(ck.chunk) * chunk_elems + static_cast<int64_t>(sub) * kS;
 }
