@@ -98,3 +98,68 @@ def compare_state(params, work, opt, tens, *, max_ulp=0):
             worst["bf16"] += int((from_dev_bf16(work[i]) != t["out"]).sum())
         worst["step"] = max(worst["step"], abs(float(st["step"].item()) - t["step"]))
     return worst
+
+
+def views_at_phases(specs, dev, seed, chunk_elems=None):
+    """Tensors as views of one pool per role (master, m, v fp32; grad and working copy bf16, or
+    an fp32 grad on the master), each placed so that its fp32 views start the given number of
+    elements past a 1 KiB boundary. ``specs``: (numel, {role: elements past 1 KiB}, fp32 grad).
+    Every view is surrounded by guard elements holding a sentinel. Returns the pools, the views
+    and the host state."""
+    import torchure_amd as ta
+    from torchure_amd.optimizer.working import mark_current
+
+    host = make_host_set([(n,) for n, _, _ in specs], seed=seed)
+    for h, (_, _, f32) in zip(host, specs):
+        h["wd"] = WD  # every view is stepped in the decay group (one-element tensors included)
+        if f32:
+            h["g"] = oracle.bf16_to_f32(h["g"]).copy()
+    gap = 1024  # guard elements between views (a multiple of 256)
+    offs, total = [], gap
+    for n, _, _ in specs:
+        offs.append(total)
+        total += (n + 256 + gap + 255) // 256 * 256
+    pools = {r: torch.full((total,), float("nan"), device=dev) for r in ("p", "m", "v", "gf")}
+    pools["g"] = torch.full((total,), 7.0, device=dev).to(torch.bfloat16)
+    pools["w"] = torch.full((total,), 7.0, device=dev).to(torch.bfloat16)
+
+    def view(role, i, n, lead):
+        pool = pools[role]
+        base = pool.data_ptr() // pool.element_size()
+        shift = (lead - (base + offs[i])) % 256 if role in ("p", "m", "v", "gf") else lead
+        return pool[offs[i] + shift: offs[i] + shift + n]
+
+    params, work, grads = [], [], []
+    for i, ((n, leads, f32), h) in enumerate(zip(specs, host)):
+        pv = view("p", i, n, leads.get("p", 0))
+        pv.copy_(torch.from_numpy(h["p"]))
+        p = torch.nn.Parameter(pv)
+        w = view("w", i, n, leads.get("w", 0))
+        w.copy_(pv.to(torch.bfloat16))
+        p._tm_working = w
+        if f32:
+            g = view("gf", i, n, leads.get("g", 0))
+            g.copy_(torch.from_numpy(h["g"]))
+            p.grad = g
+        else:
+            g = view("g", i, n, leads.get("g", 0))
+            g.copy_(to_dev_bf16(h["g"], (n,), dev))
+            w.grad = g
+        params.append(p)
+        work.append(w)
+    opt = ta.AdamW([{"params": params, "weight_decay": WD}], lr=HYPER["lr"],
+                   betas=(HYPER["beta1"], HYPER["beta2"]), fused=True,
+                   **({"chunk_elems": chunk_elems} if chunk_elems else {}))
+    for i, ((n, leads, _), p, h) in enumerate(zip(specs, params, host)):
+        st = opt.state[p]
+        st["step"] = torch.tensor(h["step"], dtype=torch.float32, device=dev)
+        st["exp_avg"] = view("m", i, n, leads.get("m", 0))
+        st["exp_avg"].copy_(torch.from_numpy(h["m"]))
+        st["exp_avg_sq"] = view("v", i, n, leads.get("v", 0))
+        st["exp_avg_sq"].copy_(torch.from_numpy(h["v"]))
+    # views of one pool share one autograd version counter: mark the copies current only
+    # after the last write into the pools
+    for p, w in zip(params, work):
+        mark_current(p, w)
+    torch.cuda.synchronize()
+    return pools, params, work, opt, host

@@ -129,3 +129,34 @@ def test_noalloc_step_captured_in_a_hip_graph():
         assert torch.randn(4096, device=DEV).abs().sum().item() > 0  # eager work between replays
         _assert_same(graph_set, eager_set)
         assert float(graph_set[2].state[graph_set[0][0]]["step"].item()) == 1000.0 + k + 1
+
+
+def test_noalloc_step_on_views_off_their_1kib_boundaries():
+    """The same comparison on tensors that are views of pooled buffers starting 4 to 252
+    elements past a 1 KiB boundary, with lengths that make the update's shifted slice grid
+    wrap its last elements into the first slice: tm_adamw_step_noalloc and tm_adamw_step give
+    the same bits on two identical copies."""
+    import torchure_amd as ta
+    from torchure_amd import _native
+
+    specs = [(n, dict(p=ph, m=ph, v=ph, g=ph, w=ph), False)
+             for ph in (4, 128, 252) for n in (5, 255, 16384 - ph + 1, 16384, 3 * 16384 + 130)]
+    specs.append((2 * 16384 + 9, dict(p=64, m=128, v=128), False))
+    a = H.views_at_phases(specs, DEV, seed=97)
+    b = H.views_at_phases(specs, DEV, seed=97)
+    print(f"noalloc views: {len(specs)} tensors", flush=True)
+    (_, pa, wa, oa, _), (_, pb, wb, ob, _) = a, b
+    ta.clip_grad_norm(pa, None, 0.05)
+    for launch in oa.plan_step(oa._pending[0], {id(p) for p in pa}):
+        launch()
+    oa._pending = None
+    ta.clip_grad_norm(pb, None, 0.05)
+    coef = ob._pending[0]
+    (sl,) = ob.plan_step(coef, {id(p) for p in pb})
+    rc = _native.lib().tm_adamw_step_noalloc(sl.d_rows.data_ptr(), sl.n, sl.chunks.data_ptr(), sl.n_chunks,
+                                             sl.chunk_elems, sl.groups_c, sl.n_groups, coef.data_ptr(),
+                                             _native.stream_handle(DEV))
+    _native.check(rc, "tm_adamw_step_noalloc")
+    ob._pending = None
+    torch.cuda.synchronize()
+    _assert_same((pa, wa, oa), (pb, wb, ob))
