@@ -85,8 +85,16 @@ typedef struct tm_tensor {
   uint32_t flags;
 } tm_tensor_t;
 
-/* One work item: elements [chunk*chunk_elems, min((chunk+1)*chunk_elems, numel))
- * of tensor `tensor`. A call takes at most 4,294,967,295 chunks (32-bit indices); larger
+/* One work item: chunk `chunk` of tensor `tensor`. For the norm, scale, cast and accumulate
+ * entry points it covers elements [chunk*chunk_elems, min((chunk+1)*chunk_elems, numel)),
+ * so a table may list any subset of a tensor's chunks. tm_adamw_step and
+ * tm_adamw_step_noalloc are different: their table must list every chunk of each tensor,
+ * 0 .. ceil(numel/chunk_elems)-1, exactly once, as tm_fill_chunks writes it. The update lays
+ * a tensor's slices on 1 KiB boundaries of its arrays, so the elements one of its chunks
+ * covers are shifted by up to 255 and chunk 0 also takes the tensor's last elements; that
+ * mapping is internal to the kernel, and only the whole set of a tensor's chunks is
+ * guaranteed to cover each element once.
+ * A call takes at most 4,294,967,295 chunks (32-bit indices); larger
  * tables return TM_EINVAL. The streaming kernels cover a chunk with chunk_elems / 256
  * one-wave workgroups and split a table over as many launches as the 2^32 work-item
  * limit of a launch requires. */
@@ -168,6 +176,7 @@ int tm_grad_scale(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
  * the deferred clip scale (tensors with TM_FLAG_CLIP read *d_coef) and the bf16
  * working-copy refresh (param_bf16 != 0).
  *   h_groups  n_groups (1..TM_MAX_GROUPS) host records; tm_tensor_t.group indexes them
+ *   d_chunks  every chunk of every tensor exactly once (tm_fill_chunks), see tm_chunk_t
  *   d_coef    clip coefficient (device fp32) applied to TM_FLAG_CLIP tensors; NULL means
  *             no tensor is scaled (TM_FLAG_CLIP is then ignored)
  *   d_ws      at least tm_workspace_bytes(n_tensors) bytes
@@ -187,7 +196,11 @@ int tm_adamw_step(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chun
  * process ends); a call with more tensors returns TM_EINVAL. It calls no allocating routine.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
  * or two host threads) race and must be serialised by the caller. Results equal
- * tm_adamw_step's, bit for bit.
+ * tm_adamw_step's, bit for bit. The chunk table follows tm_adamw_step's rule (every chunk of
+ * every tensor exactly once). The hyper-parameters (h_groups: lr, betas, weight decay, eps)
+ * are copied into the launch's kernel arguments at call time: a captured HIP graph replays
+ * the lr it was captured with, so a schedule (WSD or any other) needs the graph captured
+ * again, or its prep kernel node's parameters updated, whenever lr changes.
  */
 int tm_adamw_step_noalloc(const tm_tensor_t* d_tensors, int64_t n_tensors, const tm_chunk_t* d_chunks,
                           int64_t n_chunks, int64_t chunk_elems, const tm_hyper_t* h_groups,

@@ -73,11 +73,17 @@ def device_setup(host, dev, *, working=True, grad_on_master=False):
     opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
                              {"lr": HYPER["lr"], "weight_decay": WD,
                               "betas": (HYPER["beta1"], HYPER["beta2"]), "fused": True})
+    opt.init_state()  # the optimizer's own (pooled) layout, filled in place below
     for p, h in zip(params, host):
         st = opt.state[p]
-        st["step"] = torch.tensor(h["step"], dtype=torch.float32, device=dev)
-        st["exp_avg"] = torch.from_numpy(h["m"].copy()).view(h["shape"]).to(dev)
-        st["exp_avg_sq"] = torch.from_numpy(h["v"].copy()).view(h["shape"]).to(dev)
+        if st:
+            st["step"].fill_(float(h["step"]))
+            st["exp_avg"].copy_(torch.from_numpy(h["m"].copy()).view(h["shape"]))
+            st["exp_avg_sq"].copy_(torch.from_numpy(h["v"].copy()).view(h["shape"]))
+        else:  # no grad, so no lazy state: primed as separate tensors
+            st["step"] = torch.tensor(h["step"], dtype=torch.float32, device=dev)
+            st["exp_avg"] = torch.from_numpy(h["m"].copy()).view(h["shape"]).to(dev)
+            st["exp_avg_sq"] = torch.from_numpy(h["v"].copy()).view(h["shape"]).to(dev)
     return params, work, opt
 
 

@@ -846,3 +846,79 @@ def test_fp32_weight_with_current_working_copy():
         copy.add_(1.0)
     assert current_copy(master) is None
     assert same(run(master), run(plain))
+
+
+def test_offset_working_copy_is_not_taken():
+    """A current bf16 working copy that starts 2 bytes past a 16-byte boundary (the optimizer
+    accepts copies at any offset) is not read by the op, whose kernels read the weight in
+    16-byte vectors: the op casts the master instead and gives the bits of a weight without a
+    copy, training and loss-only."""
+    from torchure_amd.loss import fused_linear_cross_entropy
+    from torchure_amd.loss.fused_linear_ce import _bf16_weight
+    from torchure_amd.optimizer.working import current_copy, mark_current
+
+    g = torch.Generator(device=DEV).manual_seed(37)
+    n, d, v = 1024, 256, 4096
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    master = torch.nn.Parameter(torch.randn(v, d, device=DEV, generator=g) * 0.05)
+    pool = torch.zeros(v * d + 8, dtype=torch.bfloat16, device=DEV)
+    copy = pool[1:1 + v * d].view(v, d)
+    assert copy.data_ptr() % 16 == 2
+    copy.copy_(master.detach().to(torch.bfloat16))
+    master._tm_working = copy
+    mark_current(master, copy)
+    assert current_copy(master) is copy
+    assert _bf16_weight(master).data_ptr() % 16 == 0
+    plain = torch.nn.Parameter(master.detach().clone())
+
+    def run(weight):
+        h = hidden.clone().requires_grad_(True)
+        loss = fused_linear_cross_entropy(h, weight, labels, -100, 512)
+        gh, gw = torch.autograd.grad(loss, (h, weight))
+        with torch.no_grad():
+            eval_loss = fused_linear_cross_entropy(hidden, weight, labels, -100, 512)
+        return loss.detach(), gh, gw, eval_loss
+
+    for x, y in zip(run(master), run(plain)):
+        assert torch.equal(x, y)
+
+
+def test_two_calls_on_two_streams_equal_sequential():
+    """Two calls issued back to back from the host on two streams, with no synchronisation
+    between them, give the bits of the same two calls run one after the other on one stream:
+    each call's stream waits for the previous call's work on the device (CallOrder), so the
+    two calls' GEMMs never run at the same time. The shapes use the Qwen3 head's width and the
+    reference's 1024-row chunks."""
+    from torchure_amd.loss import fused_linear_cross_entropy
+
+    g = torch.Generator(device=DEV).manual_seed(41)
+    n, d, v = 2048, 1024, 32768
+    inputs = []
+    for _ in range(2):
+        hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+        weight = (torch.randn(v, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+        labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+        inputs.append((hidden, weight, labels))
+
+    def one(hidden, weight, labels):
+        h = hidden.clone().requires_grad_(True)
+        w = weight.clone().requires_grad_(True)
+        loss = fused_linear_cross_entropy(h, w, labels, -100, 1024)
+        loss.backward()
+        return loss.detach(), h.grad, w.grad
+
+    torch.cuda.synchronize()
+    seq = [one(*x) for x in inputs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(DEV), torch.cuda.Stream(DEV)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(DEV))
+    out = []
+    for s, x in zip(streams, inputs):
+        with torch.cuda.stream(s):
+            out.append(one(*x))
+    torch.cuda.synchronize()
+    for a, b in zip(seq, out):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)

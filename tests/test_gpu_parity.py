@@ -620,11 +620,14 @@ def test_full_size_steady_state(config):
     grads = [w.grad for w in work]
     opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
                              {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True})
+    opt.init_state()  # the optimizer's pooled layout, filled in place with the steady state
     for p in params:
         st = opt.state[p]
-        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=DEV)
-        st["exp_avg"] = torch.randn(p.shape, device=DEV, generator=g) * 1e-4
-        st["exp_avg_sq"] = torch.randn(p.shape, device=DEV, generator=g).abs_() * 1e-8
+        st["step"].fill_(1000.0)
+        st["exp_avg"].copy_(torch.randn(p.shape, device=DEV, generator=g) * 1e-4)
+        st["exp_avg_sq"].copy_(torch.randn(p.shape, device=DEV, generator=g).abs_() * 1e-8)
+    for k in ("exp_avg", "exp_avg_sq"):  # one pool per role
+        assert len({opt.state[p][k].untyped_storage().data_ptr() for p in params}) == 1
     sample = [0, 1, 5, 6, 200, len(shapes) - 1]
 
     def host(t):
@@ -678,11 +681,14 @@ def test_full_size_every_element_matches_torch_rocm_fused_adamw(config):
         w.grad = (torch.randn(w.shape, device=DEV, generator=g) * 1e-3).to(torch.bfloat16)
     opt = ta.build_optimizer(torch.nn.ParameterList(params), "adamw",
                              {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True})
+    opt.init_state()  # the optimizer's pooled layout, filled in place with the steady state
     for p in params:
         st = opt.state[p]
-        st["step"] = torch.tensor(1000.0, dtype=torch.float32, device=DEV)
-        st["exp_avg"] = torch.randn(p.shape, device=DEV, generator=g) * 1e-4
-        st["exp_avg_sq"] = torch.randn(p.shape, device=DEV, generator=g).abs_() * 1e-8
+        st["step"].fill_(1000.0)
+        st["exp_avg"].copy_(torch.randn(p.shape, device=DEV, generator=g) * 1e-4)
+        st["exp_avg_sq"].copy_(torch.randn(p.shape, device=DEV, generator=g).abs_() * 1e-8)
+    for k in ("exp_avg", "exp_avg_sq"):  # one pool per role
+        assert len({opt.state[p][k].untyped_storage().data_ptr() for p in params}) == 1
     ref = [torch.nn.Parameter(p.detach().clone()) for p in params]
     topt = torch.optim.AdamW([{"params": [q for q in ref if q.dim() >= 2], "weight_decay": 0.1},
                               {"params": [q for q in ref if q.dim() < 2], "weight_decay": 0.0}],
@@ -993,6 +999,97 @@ def test_checkpoint_file_roundtrip_continues_bit_exact(tmp_path):
         for k in ("step", "exp_avg", "exp_avg_sq"):
             assert torch.equal(oa.state[a][k], ob.state[b][k])
             assert ob.state[b][k].device == b.device
+
+
+def test_pooled_state_checkpoint_size_and_torch_interop(tmp_path):
+    """The lazy state is pooled (one fp32 buffer per role, each moment a view at the same
+    distance from a 1 KiB boundary as its master, 16-byte aligned). torchure's Checkpointer flow still works both ways with torch.optim.AdamW
+    (torchure/checkpoint/checkpointer.py:43-60,81-82): for the Qwen3-shaped set the saved file is
+    not larger than the same state saved as separate tensors; torch's fused AdamW loads it with
+    torch.load(weights_only=True) and continues bit for bit with this optimizer; and this
+    optimizer loads torch's checkpoint back into its pooled layout and continues bit for bit."""
+    import os
+
+    import torchure_amd as ta
+
+    shapes = shapes_for("tiny") + [(1001,), (3, 333), (128,), (7,)]
+    gen = torch.Generator(device=DEV).manual_seed(43)
+    init = [torch.randn(sh, device=DEV, generator=gen) * 0.02 for sh in shapes]
+    grads = [[torch.randn(sh, device=DEV, generator=gen) * 1e-3 for sh in shapes] for _ in range(3)]
+
+    def groups_of(ps):
+        return [{"params": [p for p in ps if p.dim() >= 2], "weight_decay": 0.1},
+                {"params": [p for p in ps if p.dim() < 2], "weight_decay": 0.0}]
+
+    def ours(ps):
+        return ta.build_optimizer(torch.nn.ParameterList(ps), "adamw",
+                                  {"lr": 3e-4, "weight_decay": 0.1, "betas": (0.9, 0.95), "fused": True})
+
+    def torch_fused(ps):
+        return torch.optim.AdamW(groups_of(ps), lr=3e-4, betas=(0.9, 0.95), eps=1e-8, fused=True)
+
+    def step(ps, opt, k):
+        for p, g in zip(ps, grads[k]):
+            p.grad = g.clone()
+        opt.step()
+
+    pa = [torch.nn.Parameter(t.clone()) for t in init]
+    oa = ours(pa)
+    step(pa, oa, 0)
+    for k in ("exp_avg", "exp_avg_sq"):
+        assert len({oa.state[p][k].untyped_storage().data_ptr() for p in pa}) == 1
+    for p in pa:
+        m, v = oa.state[p]["exp_avg"], oa.state[p]["exp_avg_sq"]
+        assert m.data_ptr() % 1024 == v.data_ptr() % 1024
+        assert m.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0
+        if p.data_ptr() % 16 == 0 and p.numel() >= 256:  # the master's phase (from a 1 KiB boundary)
+            assert m.data_ptr() % 1024 == p.data_ptr() % 1024
+
+    # file size, on the Qwen3-shaped set alone (its moments need no padding in the pool)
+    pq = [torch.nn.Parameter(torch.randn(sh, device=DEV, generator=gen) * 0.02) for sh in shapes_for("tiny")]
+    oq = ours(pq)
+    for p in pq:
+        p.grad = torch.randn(p.shape, device=DEV, generator=gen) * 1e-3
+    oq.step()
+    sq = oq.state_dict()
+    torch.save(sq, tmp_path / "pooled_q.pt")
+    torch.save({"state": {i: {k: t.clone() for k, t in st.items()} for i, st in sq["state"].items()},
+                "param_groups": sq["param_groups"]}, tmp_path / "separate_q.pt")
+    assert os.path.getsize(tmp_path / "pooled_q.pt") <= os.path.getsize(tmp_path / "separate_q.pt")
+    del pq, oq, sq
+
+    sd = oa.state_dict()
+    torch.save(sd, tmp_path / "pooled.pt")
+
+    # torch's fused AdamW resumes from the pooled file and continues like this optimizer
+    pb = [torch.nn.Parameter(p.detach().clone()) for p in pa]
+    ob = torch_fused(pb)
+    ob.load_state_dict(torch.load(tmp_path / "pooled.pt", map_location="cpu", weights_only=True))
+    step(pa, oa, 1)
+    step(pb, ob, 1)
+    torch.cuda.synchronize()
+    i32 = torch.int32
+    for a, b in zip(pa, pb):
+        assert torch.equal(a.detach().view(i32), b.detach().view(i32))
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(oa.state[a][k].view(i32), ob.state[b][k].view(i32))
+        assert oa.state[a]["step"].item() == ob.state[b]["step"].item() == 2.0
+
+    # and this optimizer resumes from torch's file, into its pooled layout
+    torch.save(ob.state_dict(), tmp_path / "torch.pt")
+    pc = [torch.nn.Parameter(p.detach().clone()) for p in pb]
+    oc = ours(pc)
+    oc.load_state_dict(torch.load(tmp_path / "torch.pt", map_location="cpu", weights_only=True))
+    for k in ("exp_avg", "exp_avg_sq"):
+        assert len({oc.state[p][k].untyped_storage().data_ptr() for p in pc}) == 1
+    step(pb, ob, 2)
+    step(pc, oc, 2)
+    torch.cuda.synchronize()
+    for b, c in zip(pb, pc):
+        assert torch.equal(b.detach().view(i32), c.detach().view(i32))
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(ob.state[b][k].view(i32), oc.state[c][k].view(i32))
+        assert oc.state[c]["step"].item() == 3.0 and oc.state[c]["step"].device == c.device
 
 
 def test_checkpoint_from_non_fused_torch_adamw(tmp_path):

@@ -408,3 +408,197 @@ def test_host_version_stamps_follow_shared_counters():
     assert not h.stamped(ps, ws) and current_copy(ps[0]) is None
     with pytest.raises(ValueError):
         h.stamp(ps, ws[:2])
+
+
+def test_fused_ce_calls_are_ordered_per_device():
+    """CallOrder (torchure_amd/loss/fused_linear_ce.py) with stand-in streams and events: the
+    first call on a device waits for nothing; a call on another stream waits for the event
+    recorded at the end of the previous call on that device (and on no other device's); a
+    call on the same stream as the previous one adds no wait; every call records its event
+    after its work; a call that raises still records it. Also that the op holds its ordering
+    lock while the host issues a call's work, so two host threads cannot interleave calls."""
+    from torchure_amd.loss.fused_linear_ce import CallOrder
+
+    log = []
+
+    class Ev:
+        n = 0
+
+        def __init__(self):
+            Ev.n += 1
+            self.name = f"e{Ev.n}"
+
+        def record(self, stream):
+            log.append(("record", stream.name, self.name))
+
+    class St:
+        def __init__(self, name):
+            self.name = name
+
+        def wait_event(self, ev):
+            log.append(("wait", self.name, ev.name))
+
+        def __eq__(self, other):
+            return isinstance(other, St) and other.name == self.name
+
+        def __ne__(self, other):
+            return not self == other
+
+        def __hash__(self):
+            return hash(self.name)
+
+    cur = {"s": St("A")}
+    order = CallOrder(current_stream=lambda dev: cur["s"], make_event=Ev)
+    d0, d1 = torch.device("cuda", 0), torch.device("cuda", 1)
+
+    def call(dev, stream, fail=False):
+        cur["s"] = St(stream)
+        with order.call(dev) as s:
+            assert s.name == stream
+            log.append(("work", stream))
+            if fail:
+                raise ValueError("planted")
+
+    call(d0, "A")
+    assert log == [("work", "A"), ("record", "A", "e1")]
+    log.clear()
+    call(d0, "B")  # another stream: waits for the previous call's end event
+    assert log == [("wait", "B", "e1"), ("work", "B"), ("record", "B", "e2")]
+    log.clear()
+    call(d0, "B")  # same stream: in order already, no wait
+    assert log == [("work", "B"), ("record", "B", "e3")]
+    log.clear()
+    call(d1, "C")  # another device: nothing to wait for
+    assert log == [("work", "C"), ("record", "C", "e4")]
+    log.clear()
+    with pytest.raises(ValueError, match="planted"):
+        call(d0, "A", fail=True)
+    assert log == [("wait", "A", "e3"), ("work", "A"), ("record", "A", "e5")]
+    log.clear()
+    call(d0, "C")  # waits for the failed call's event, not an older one
+    assert log[0] == ("wait", "C", "e5")
+    log.clear()
+    with order.call(torch.device("cpu")) as s:  # no GPU: nothing to order (the op raises later)
+        assert s is None
+    assert log == []
+
+    # the lock is held while a call issues its work: another thread's call waits for it
+    import threading
+
+    inside = threading.Event()
+    release = threading.Event()
+    seen = []
+
+    def first():
+        with order.call(d0):
+            inside.set()
+            release.wait(10)
+            seen.append("first done")
+
+    def second():
+        inside.wait(10)
+        with order.call(d0):
+            seen.append("second")
+
+    t1, t2 = threading.Thread(target=first), threading.Thread(target=second)
+    t1.start()
+    t2.start()
+    inside.wait(10)
+    t2.join(0.2)
+    assert seen == [] and t2.is_alive()
+    release.set()
+    t1.join(10)
+    t2.join(10)
+    assert seen == ["first done", "second"]
+
+
+def test_update_shifted_grid_covers_every_element_once():
+    """The update kernel's slice rules (torchure_amd/csrc/tm_optim.hip, adamw_update_kernel and
+    slice_of), restated in numpy: with chunks of C elements cut into C / 256 one-wave slices,
+    slice s of chunk c starting at start = c*C + 256*s, and a tensor of n elements at grid phase
+    ph (a multiple of 4 below 256), the wave returns when start - ph >= n and start > 0; lane t
+    takes e = start + 4t - ph, wrapped by ceil(n/C)*C when negative; it updates [e, e+4) when
+    e + 4 <= n, else [e, n) element by element when e < n. Every element of [0, n) must be
+    updated exactly once, every group of 4 must start 16-byte aligned in arrays at that phase
+    ((e + ph) % 4 == 0), and only the last group of the tensor may be partial. Lengths around
+    the chunk boundaries (1..3C+300 at C = 2048, around k*C at C = 4096 and 16,384) and every
+    phase 0..252."""
+    import numpy as np
+
+    def check(n, C):
+        n_chunks = -(-n // C)
+        spc = C // 256
+        start = (np.arange(n_chunks)[:, None] * C + np.arange(spc)[None, :] * 256).reshape(-1)
+        phs = np.arange(0, 256, 4)
+        lanes = np.arange(64) * 4
+        # (phase, slice, lane)
+        st = np.broadcast_to(start[None, :, None], (phs.size, start.size, 64))
+        ph = np.broadcast_to(phs[:, None, None], st.shape)
+        alive = ~((st - ph >= n) & (st > 0))
+        e = st + lanes[None, None, :] - ph
+        e = np.where(e < 0, e + n_chunks * C, e)
+        full = alive & (e + 4 <= n)
+        tail = alive & (e < n) & ~full
+        assert not np.any(full & ((e + ph) % 4 != 0)), (n, C)
+        assert np.all(e[tail] + 4 > n), (n, C)
+        counts = np.zeros((phs.size, n), dtype=np.int64)
+        pidx = np.broadcast_to(np.arange(phs.size)[:, None, None], st.shape)
+        for j in range(4):
+            m = (full | tail) & (e + j < n)
+            np.add.at(counts, (pidx[m], e[m] + j), 1)
+        assert np.all(counts == 1), (n, C, np.argwhere(counts != 1)[:4])
+
+    for n in range(1, 3 * 2048 + 301, 7):
+        check(n, 2048)
+    for n in list(range(1, 40)) + [2047, 2048, 2049, 6143, 6144, 6145]:
+        check(n, 2048)
+    for C in (4096, 16384):
+        for k in (1, 2, 3):
+            for n in range(k * C - 260, k * C + 261, 13):
+                check(n, C)
+
+
+def test_pooled_state_layout(tmp_path):
+    """pooled_layout / pooled_moments (torchure_amd/optimizer/adamw.py): views never overlap and
+    stay inside the pool; every view starts 16-byte aligned; a tensor given a phase starts that
+    many elements past a 1 KiB boundary of the pool (so a param's moments share its master's
+    phase); the two roles share one layout; Qwen3 sets with 1 KiB-aligned masters need no
+    padding; random phases need little; and torch.save of pooled moments is not larger than of
+    the same moments as separate tensors."""
+    import numpy as np
+
+    from torchure_amd.optimizer.adamw import master_phase, pooled_layout, pooled_moments
+    from torchure_amd.workloads import shapes_for
+
+    rng = np.random.default_rng(5)
+    numels = [int(x) for x in rng.integers(0, 5000, 300)] + [256, 512, 128, 1, 3, 4, 0, 1024 * 1024]
+    for phases in (None, [int(x) * 4 for x in rng.integers(0, 64, len(numels))],
+                   [None if k % 5 == 0 else 128 * (k % 2) for k in range(len(numels))]):
+        offs, total = pooled_layout(numels, phases)
+        spans = sorted((o, o + n) for o, n in zip(offs, numels) if n)
+        assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:])) and spans[-1][1] <= total
+        assert all(o % 4 == 0 for o in offs)
+        want = phases if phases is not None else [0 if n % 256 == 0 else None for n in numels]
+        assert all(ph is None or o % 256 == ph for o, ph in zip(offs, want))
+        assert total <= sum((n + 3) // 4 * 4 for n in numels) + 256 * len(numels)
+    for cfg in ("tiny", "qwen3-0.6b", "qwen3-4b"):
+        ns = [int(np.prod(s)) for s in shapes_for(cfg)]
+        assert pooled_layout(ns, [0 if n >= 256 else None for n in ns])[1] == sum(ns)  # no padding
+    ps = [torch.zeros(s) for s in [(3, 5), (256,), (7,), (2, 128), (64, 64), (1001,)]]
+    views = pooled_moments(ps, zero=True)
+    for p, m, v in views:
+        assert m.shape == p.shape and v.shape == p.shape and m.dtype == torch.float32
+        assert m.data_ptr() % 1024 == v.data_ptr() % 1024
+        assert m.data_ptr() % 16 == 0 and not m.any()
+        if master_phase(p) is not None and p.numel() >= 256:
+            assert (m.data_ptr() // 4) % 256 == master_phase(p)
+    assert len({m.untyped_storage().data_ptr() for _, m, _ in views}) == 1
+    # torch.save writes a pool once (one record per storage): with no padding, as for Qwen3 sets
+    # on 1 KiB-aligned masters, the file is not larger than with one tensor per moment
+    ns = [int(np.prod(s)) for s in shapes_for("tiny")]
+    offs, total = pooled_layout(ns, [0 if n >= 256 else None for n in ns])
+    pools = torch.zeros(total), torch.zeros(total)
+    state = {i: {"exp_avg": pools[0][o:o + n], "exp_avg_sq": pools[1][o:o + n]} for i, (o, n) in enumerate(zip(offs, ns))}
+    torch.save(state, tmp_path / "pooled.pt")
+    torch.save({i: {k: t.clone() for k, t in st.items()} for i, st in state.items()}, tmp_path / "separate.pt")
+    assert os.path.getsize(tmp_path / "pooled.pt") <= os.path.getsize(tmp_path / "separate.pt")

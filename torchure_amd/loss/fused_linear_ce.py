@@ -52,7 +52,9 @@ for every fold of 1024-row chunks, and the GEMMs get large M.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import threading
 
 import torch
 
@@ -61,6 +63,53 @@ from torchure_amd.core import tables
 from torchure_amd.optimizer.working import current_copy
 
 DEFAULT_LOGITS_BYTES = 4 << 30
+
+
+class CallOrder:
+    """Puts the GPU work of this op's calls on one device in host call order.
+
+    hipBLASLt's gfx950 solutions for this op's products are stream-K kernels (``SK3`` in
+    their names): a persistent grid of one workgroup per CU in which workgroups spin on
+    flags until other workgroups of the same launch have written their partial tiles, so
+    every workgroup of the launch must be resident at once. Two such launches running at
+    the same time on two streams can each hold CUs with spinning workgroups while the
+    workgroups they wait for cannot be placed, and neither finishes. So each call's stream
+    first waits for an event recorded at the end of the previous call's GPU work on that
+    device (skipped when both run on one stream), and the host side of a call runs under a
+    lock, so that calls from two host threads cannot interleave either. The event is
+    always recorded before the next call waits on it, so a wait never sits in front of the
+    work that signals it. GEMMs that a caller runs on other streams are not ordered by
+    this; they must not overlap a call.
+
+    ``current_stream`` and ``make_event`` are injectable so the ordering can be checked on
+    the CPU with stand-in streams and events."""
+
+    def __init__(self, current_stream=None, make_event=None):
+        self._current_stream = current_stream or torch.cuda.current_stream
+        self._make_event = make_event or torch.cuda.Event
+        self._lock = threading.RLock()
+        self._last: dict = {}  # device index -> (stream, event) of the last call there
+
+    @contextlib.contextmanager
+    def call(self, device: torch.device):
+        if device.type != "cuda":  # the call raises on its argument checks; nothing to order
+            yield None
+            return
+        key = device.index if device.index is not None else -1
+        with self._lock:
+            stream = self._current_stream(device)
+            prev = self._last.get(key)
+            if prev is not None and prev[0] != stream:
+                stream.wait_event(prev[1])
+            try:
+                yield stream
+            finally:
+                done = self._make_event()
+                done.record(stream)
+                self._last[key] = (stream, done)
+
+
+CALL_ORDER = CallOrder()
 
 
 def auto_chunk_rows(n_rows: int, vocab: int, logits_bytes: int = DEFAULT_LOGITS_BYTES) -> int:
@@ -199,10 +248,13 @@ def _bf16_weight(weight: torch.Tensor) -> torch.Tensor:
     """The contiguous bf16 weight the products run on: ``weight.to(bf16)`` (RNE, as autocast
     casts), or, for an fp32 master whose bf16 working copy is current (attached with
     torchure_amd.attach_bf16_working_params and rewritten by each AdamW step), that copy, which
-    holds the same bits, so the cast's read of 4 and write of 2 bytes per element is skipped."""
+    holds the same bits, so the cast's read of 4 and write of 2 bytes per element is skipped.
+    A copy that does not start on a 16-byte boundary (the optimizer accepts copies at any
+    offset) is not taken: this op's kernels read the weight in 16-byte vectors, and the cast
+    gives a fresh, aligned buffer with the same bits."""
     if weight.dtype == torch.float32:
         w = current_copy(weight)
-        if w is not None:
+        if w is not None and w.data_ptr() % 16 == 0:
             return w.detach()
     return weight.to(torch.bfloat16).contiguous()
 
@@ -389,6 +441,7 @@ def fused_linear_cross_entropy(
         hidden = hidden.reshape(-1, hidden.shape[-1])
         labels = labels.reshape(-1)
     hidden, labels = hidden.contiguous(), labels.contiguous()
-    if not (torch.is_grad_enabled() and (hidden.requires_grad or weight.requires_grad)):
-        return _loss_only(hidden, weight, labels, ignore_index, chunk_size)
-    return _FusedLinearCE.apply(hidden, weight, labels, ignore_index, chunk_size)
+    with CALL_ORDER.call(hidden.device):  # one call's GEMMs at a time per device
+        if not (torch.is_grad_enabled() and (hidden.requires_grad or weight.requires_grad)):
+            return _loss_only(hidden, weight, labels, ignore_index, chunk_size)
+        return _FusedLinearCE.apply(hidden, weight, labels, ignore_index, chunk_size)

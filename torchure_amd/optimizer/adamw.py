@@ -253,6 +253,7 @@ class AdamW(torch.optim.Optimizer):
         if fast is not None:
             return fast
         self._plan = None
+        self._init_states_pooled()
         order = []  # (param, entry) of every param with a grad, in table order
         rec = clip_ids if isinstance(clip_ids, _ClipRecord) else None
         if rec is not None:
@@ -406,6 +407,37 @@ class AdamW(torch.optim.Optimizer):
                            self.chunk_elems, _native.hyper_array(hyper), len(hyper), coef,
                            plan.written, (plan.wparams, plan.wworks))]
 
+    @torch.no_grad()
+    def init_state(self) -> None:
+        """Create the lazy state of every param that has a grad and no state yet, as the next
+        step() would (step 0, zero moments, in the pooled layout), without stepping. Lets a
+        caller place or fill the state (a resume, a benchmark) before the first step."""
+        self._init_states_pooled()
+
+    def _init_states_pooled(self) -> None:
+        """Lazy state of every param that has a grad and no state yet (torch creates it at
+        the first step that sees a grad, adam.py:139-212), created together: per device, one
+        fp32 buffer per role (exp_avg, exp_avg_sq) holds all of them, and each param's moment
+        is a view of it (``pooled_layout``), so the update streams two large arrays laid out
+        the same way instead of hundreds of allocations wherever the caching allocator put
+        them. ``step`` stays a 0-d fp32 tensor per param, as torch keeps it."""
+        fresh = []
+        state_map = self.state
+        for group in self.param_groups:
+            for p in group["params"]:
+                if state_map.get(p):
+                    continue
+                work = getattr(p, "_tm_working", None)
+                if p.grad is None and (work is None or work.grad is None):
+                    continue
+                if p.is_cuda and p.dtype == torch.float32 and p.is_contiguous() and not p.is_sparse:
+                    fresh.append(p)  # anything else is refused, precisely, by _verify_param
+        if fresh:
+            with torch.no_grad():
+                for p, m, v in pooled_moments(fresh, zero=True):
+                    state_map[p] = {"step": torch.zeros((), dtype=torch.float32, device=p.device),
+                                    "exp_avg": m, "exp_avg_sq": v}
+
     def _verify_param(self, p: torch.Tensor, state: dict, work) -> "_ParamEntry":
         """Full checks of a param, its working copy and its state (created lazily,
         moved to fp32 on the param's device when loaded from elsewhere); cached
@@ -447,6 +479,29 @@ class AdamW(torch.optim.Optimizer):
         for group in self.param_groups:
             group["fused"] = True
             group["foreach"] = None
+        self._repack_states()
+
+    def _repack_states(self) -> None:
+        """Moments loaded from a checkpoint (separate tensors, or views of a loaded storage)
+        are copied into this optimizer's pooled layout, as if created by its first step."""
+        held = []
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if not st or not (p.is_cuda and p.dtype == torch.float32 and p.is_contiguous()):
+                    continue
+                m, v = st.get("exp_avg"), st.get("exp_avg_sq")
+                if (isinstance(m, torch.Tensor) and isinstance(v, torch.Tensor) and m.numel() == p.numel()
+                        and v.numel() == p.numel() and m.dtype == v.dtype == torch.float32
+                        and m.device == v.device == p.device):
+                    held.append((p, st, m, v))
+        if not held:
+            return
+        with torch.no_grad():
+            for (p, st, m, v), (_, pm, pv) in zip(held, pooled_moments([h[0] for h in held], zero=False)):
+                pm.copy_(m.reshape(pm.shape))
+                pv.copy_(v.reshape(pv.shape))
+                st["exp_avg"], st["exp_avg_sq"] = pm, pv
 
     def _plan_launches(self, per_dev, hyper, coef) -> list["StepLaunch"]:
         groups_c = _native.hyper_array(hyper)
@@ -618,10 +673,99 @@ class StepLaunch:
             _native.host().stamp(self.pair_params, self.pair_works)
 
 
+POOL_ALIGN_ELEMS = 256  # 1 KiB of fp32: the update's slices start on these boundaries
+
+
+def pooled_layout(numels, phases=None) -> tuple[list[int], int]:
+    """Offsets (elements) of tensors of ``numels`` elements in one fp32 pool that starts on a
+    1 KiB boundary, and the pool's length.
+
+    ``phases[i]`` is the position (elements, a multiple of 4 below 256) past a 1 KiB boundary
+    at which tensor i must start, or None for any 16-byte aligned start. The optimizer passes
+    each master's own phase, so that a param's master, exp_avg and exp_avg_sq all sit at the
+    same distance from a 1 KiB boundary and the update's slices start on one in all three.
+    Tensors are placed greedily: the next one is a tensor whose phase is the current
+    position's, lengths that are multiples of 256 first (they keep the position's phase), in
+    the given order; when none is left for the current phase, the position moves to the
+    nearest phase ahead that still has tensors. Tensors with no phase come last, each rounded
+    up to 4 elements. With ``phases`` None every tensor whose length is a multiple of 256 gets
+    phase 0 and the others none. Qwen3 sets need no padding when their masters sit on 1 KiB
+    boundaries (the 128-wide q/k norms, shorter than a slice, take no phase)."""
+    n_t = len(numels)
+    if phases is None:
+        phases = [0 if n % POOL_ALIGN_ELEMS == 0 else None for n in numels]
+    offs = [0] * n_t
+    buckets: dict = {}
+    free = []
+    for i, (n, ph) in enumerate(zip(numels, phases)):
+        if ph is None:
+            free.append(i)
+        else:
+            buckets.setdefault(int(ph) % POOL_ALIGN_ELEMS, ([], []))[0 if n % POOL_ALIGN_ELEMS == 0 else 1].append(i)
+    for whole, rest in buckets.values():  # popped from the end: keep the given order
+        whole.reverse()
+        rest.reverse()
+    pos, left = 0, n_t - len(free)
+    while left:
+        b = buckets.get(pos % POOL_ALIGN_ELEMS)
+        if b is not None and (b[0] or b[1]):
+            i = b[0].pop() if b[0] else b[1].pop()
+            offs[i] = pos
+            pos += (numels[i] + 3) // 4 * 4
+            left -= 1
+            continue
+        cur = pos % POOL_ALIGN_ELEMS
+        pos += min((ph - cur) % POOL_ALIGN_ELEMS for ph, bb in buckets.items() if bb[0] or bb[1])
+    for i in free:
+        offs[i] = pos
+        pos += (numels[i] + 3) // 4 * 4
+    return offs, pos
+
+
+def master_phase(p: torch.Tensor):
+    """Elements from the 1 KiB boundary at or before ``p``'s first element, for a 16-byte
+    aligned fp32 tensor (the update's grid phase of that array); None otherwise."""
+    ptr = p.data_ptr()
+    return (ptr // 4) % POOL_ALIGN_ELEMS if ptr % 16 == 0 else None
+
+
+def _aligned_pool(total: int, device, zero: bool) -> torch.Tensor:
+    """An fp32 buffer of ``total`` elements starting on a 1 KiB boundary. Large blocks from the
+    caching allocator already do; a block that does not is allocated again with 1 KiB more and
+    viewed from its first boundary."""
+    make = torch.zeros if zero else torch.empty
+    buf = make(max(total, 1), dtype=torch.float32, device=device)
+    if buf.data_ptr() % (4 * POOL_ALIGN_ELEMS) == 0:
+        return buf
+    buf = make(total + POOL_ALIGN_ELEMS, dtype=torch.float32, device=device)
+    skip = (-buf.data_ptr() // 4) % POOL_ALIGN_ELEMS
+    return buf[skip: skip + total]
+
+
+def pooled_moments(params, zero: bool = True):
+    """(param, exp_avg view, exp_avg_sq view) for ``params``: per device, one pool per role
+    with ``pooled_layout`` at the params' own phases, the same layout in both pools, so each
+    param's master and two moments sit at the same distance from a 1 KiB boundary."""
+    per_dev: dict = {}
+    for p in params:
+        per_dev.setdefault(p.device, []).append(p)
+    out = {}
+    for device, ps in per_dev.items():
+        # a tensor shorter than one 256-element slice is covered by one wave wherever it sits
+        phases = [master_phase(p) if p.numel() >= POOL_ALIGN_ELEMS else None for p in ps]
+        offs, total = pooled_layout([p.numel() for p in ps], phases)
+        pm, pv = _aligned_pool(total, device, zero), _aligned_pool(total, device, zero)
+        for p, o in zip(ps, offs):
+            n = p.numel()
+            out[id(p)] = (pm[o: o + n].view(p.shape), pv[o: o + n].view(p.shape))
+    return [(p, *out[id(p)]) for p in params]
+
+
 def step_bytes_per_param(grad_bytes: int, with_norm: bool = True, with_bf16_out: bool = True) -> int:
     """Algorithmic HBM bytes per parameter of one step (norm pass + update)."""
     upd = grad_bytes + 3 * 4 + 3 * 4 + (2 if with_bf16_out else 0)
     return upd + (grad_bytes if with_norm else 0)
 
 
-__all__ = ["AdamW", "owner_of", "owners_of", "materialize_pending_for", "step_bytes_per_param"]
+__all__ = ["AdamW", "owner_of", "owners_of", "materialize_pending_for", "step_bytes_per_param",
+           "pooled_layout", "pooled_moments", "master_phase"]
