@@ -365,6 +365,27 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
                       int64_t vocab, int64_t dim, void* d_ws, size_t ws_bytes, void* stream);
 
 /*
+ * The logits of one chunk, fused_linear_ce.py:38 `logits = h @ w.t()` (a bf16 matmul: fp32
+ * accumulation, bf16 result): d_logits (rows x vocab) = bf16(d_hidden (rows x dim) @ d_weight^T)
+ * with d_weight the vocab x dim head, all three contiguous and 16-byte aligned, dim a positive
+ * multiple of 64 (rows and vocab any positive sizes). RNE rounding of the fp32 sum over dim;
+ * deterministic. Replaces the library GEMM torch.matmul dispatches there.
+ */
+int tm_ce_logits_bf16(uint16_t* d_logits, const uint16_t* d_hidden, const uint16_t* d_weight, int64_t rows,
+                      int64_t vocab, int64_t dim, void* stream);
+
+/*
+ * The weight gradient of one chunk, fused_linear_ce.py:57 `gw = grad_logits.t() @ h` (a bf16
+ * matmul: fp32 accumulation, bf16 result): d_grad_w (vocab x dim) = bf16(d_grad_logits^T @
+ * d_hidden) with d_grad_logits rows x vocab and d_hidden rows x dim, all contiguous and 16-byte
+ * aligned, rows a positive multiple of 64, vocab and dim positive multiples of 8. RNE rounding
+ * of the fp32 sum over rows; deterministic. Replaces the library GEMM torch.matmul dispatches
+ * there; the fp32 accumulation of the chunks stays tm_ce_grad_w_fold's.
+ */
+int tm_ce_grad_w_bf16(uint16_t* d_grad_w, const uint16_t* d_grad_logits, const uint16_t* d_hidden, int64_t rows,
+                      int64_t vocab, int64_t dim, void* stream);
+
+/*
  * d_dst (cols x rows) = d_src (rows x cols) transposed, bf16, both contiguous, rows and cols
  * multiples of 64, pointers 8-byte aligned: the W^T operand of tm_ce_grad_h_bf16, made once per
  * forward (fused_linear_ce.py:65 casts the weight once for all chunks; this is the same

@@ -205,3 +205,180 @@ def test_op_mixes_the_gemm_and_the_library_on_ragged_chunks():
     want.mul_((torch.tensor(1.0, device=DEV) / n_valid).to(torch.bfloat16))
     torch.cuda.synchronize()
     assert torch.equal(h1.grad.view(torch.int16), want.view(torch.int16))
+
+
+def _logits(h, w, pad=64, sentinel=0x7BCD):
+    """tm_ce_logits_bf16 into a view with `pad` guard elements on both sides (sentinel bits),
+    returning (logits, guard intact)."""
+    native, lib, stream = _lib()
+    rows, vocab = h.shape[0], w.shape[0]
+    buf = torch.full((rows * vocab + 2 * pad,), sentinel, dtype=torch.int16, device=DEV)
+    out = buf[pad: pad + rows * vocab].view(torch.bfloat16).view(rows, vocab)
+    native.check(lib.tm_ce_logits_bf16(out.data_ptr(), h.data_ptr(), w.data_ptr(), rows, vocab, h.shape[1], stream),
+                 "tm_ce_logits_bf16")
+    torch.cuda.synchronize()
+    guard = bool((buf[:pad] == sentinel).all()) and bool((buf[pad + rows * vocab:] == sentinel).all())
+    return out, guard
+
+
+@pytest.mark.parametrize("rows,vocab,dim", [
+    (1, 1, 64),              # one element
+    (7, 100, 64),            # vocab not a multiple of 8: element-wise stores
+    (255, 4095, 128),        # rows and vocab one short of tile multiples
+    (257, 4097, 128),        # one past: mostly empty edge tiles
+    (1000, 1001, 192),
+    (1024, 151936, 1024),    # the Qwen3-0.6B head at the reference's 1024-row chunk
+    (4096, 151936, 1024),
+    (1500, 32768, 2560),     # Qwen3-4B width, ragged rows
+])
+def test_logits_gemm_vs_fp64_and_library(rows, vocab, dim):
+    """logits = h @ W^T (fused_linear_ce.py:38) on this build's GEMM: every element within one
+    bf16 ulp of the exact product of the same bf16 operands plus 2^-20 of sum_k |h_ik w_jk| (the
+    fp32 accumulation), within one ulp plus both budgets of torch.matmul's, equal to it on at
+    least 99% of the elements, no write outside the output, and the same bits on a repeat."""
+    g = torch.Generator(device=DEV).manual_seed(rows * 3 + vocab + dim)
+    h = torch.randn(rows, dim, device=DEV, generator=g).to(torch.bfloat16)
+    w = (torch.randn(vocab, dim, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    out, guard = _logits(h, w)
+    assert guard
+    exact = torch.matmul(h.double(), w.double().t())
+    absum = torch.matmul(h.double().abs(), w.double().abs().t())
+    lib_out = torch.matmul(h, w.t())
+    torch.cuda.synchronize()
+    err = (out.double() - exact).abs()
+    bound = _bf16_ulp(exact) + absum * 2.0 ** -20
+    worst = float((err / bound).max())
+    print(f"{rows}x{vocab}x{dim}: worst |err| / bound {worst:.3f}")
+    assert worst <= 1.0
+    d = (out.double() - lib_out.double()).abs()
+    assert bool((d <= _bf16_ulp(torch.maximum(out.double().abs(), lib_out.double().abs())) + absum * 2.0 ** -19).all())
+    same = float((out.view(torch.int16) == lib_out.view(torch.int16)).double().mean())
+    print(f"  equal to torch.matmul on {same:.5f} of the elements")
+    assert same >= 0.99
+    again, _ = _logits(h, w)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+
+
+def test_logits_gemm_full_chunk_vs_library():
+    """The whole 8192-token Qwen3-0.6B head in one chunk (the op's MI355X sizing): against
+    torch.matmul row block by row block, within one bf16 ulp plus both fp32 budgets, equal on
+    at least 99% of the elements."""
+    rows, vocab, dim = 8192, 151936, 1024
+    g = torch.Generator(device=DEV).manual_seed(8192)
+    h = torch.randn(rows, dim, device=DEV, generator=g).to(torch.bfloat16)
+    w = (torch.randn(vocab, dim, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    out, guard = _logits(h, w)
+    assert guard
+    same = 0.0
+    for s in range(0, rows, 1024):
+        lib_out = torch.matmul(h[s:s + 1024], w.t())
+        o = out[s:s + 1024]
+        absum = torch.matmul(h[s:s + 1024].float().abs(), w.float().abs().t()).double()
+        d = (o.double() - lib_out.double()).abs()
+        assert bool((d <= _bf16_ulp(torch.maximum(o.double().abs(), lib_out.double().abs())) + absum * 2.0 ** -19).all())
+        same += float((o.view(torch.int16) == lib_out.view(torch.int16)).double().mean()) / (rows // 1024)
+    print(f"equal to torch.matmul on {same:.5f} of the elements")
+    assert same >= 0.99
+
+
+def test_logits_gemm_argument_checks():
+    """Shapes the GEMM does not take and misaligned pointers are refused before any launch."""
+    native, lib, stream = _lib()
+    t = torch.empty(1 << 16, dtype=torch.bfloat16, device=DEV)
+    p = t.data_ptr()
+    for rows, vocab, dim in ((0, 64, 64), (64, 0, 64), (64, 64, 100), (64, 64, 0)):
+        assert lib.tm_ce_logits_bf16(p, p, p, rows, vocab, dim, stream) < 0
+    assert lib.tm_ce_logits_bf16(p + 2, p, p, 8, 8, 64, stream) < 0
+    assert b"aligned" in lib.tm_last_error()
+
+
+def _grad_w(gl, h, pad=64, sentinel=0x7BCD):
+    """tm_ce_grad_w_bf16 into a view with guard elements on both sides."""
+    native, lib, stream = _lib()
+    rows, vocab = gl.shape
+    dim = h.shape[1]
+    buf = torch.full((vocab * dim + 2 * pad,), sentinel, dtype=torch.int16, device=DEV)
+    out = buf[pad: pad + vocab * dim].view(torch.bfloat16).view(vocab, dim)
+    native.check(lib.tm_ce_grad_w_bf16(out.data_ptr(), gl.data_ptr(), h.data_ptr(), rows, vocab, dim, stream),
+                 "tm_ce_grad_w_bf16")
+    torch.cuda.synchronize()
+    guard = bool((buf[:pad] == sentinel).all()) and bool((buf[pad + vocab * dim:] == sentinel).all())
+    return out, guard
+
+
+@pytest.mark.parametrize("rows,vocab,dim,softmax", [
+    (64, 8, 8, False),            # one K stage, one tile mostly past vocab and dim
+    (128, 4104, 264, False),      # vocab and dim one group of 8 past tile multiples
+    (192, 1000, 136, True),
+    (1024, 151936, 1024, True),   # the Qwen3-0.6B head at the reference's 1024-row chunk
+    (4096, 32768, 2560, True),    # a 4096-row chunk at the Qwen3-4B width
+])
+def test_grad_w_gemm_vs_fp64_and_library(rows, vocab, dim, softmax):
+    """A chunk's gw = grad_logits^T @ h (fused_linear_ce.py:57) on this build's transposed-read
+    GEMM: every element within one bf16 ulp of the exact product of the same bf16 operands plus
+    2^-20 of sum_k |g_kv h_kd|, within one ulp plus both budgets of torch.matmul's, equal to it
+    on at least 99% of the elements, no write outside the output, the same bits on a repeat."""
+    g = torch.Generator(device=DEV).manual_seed(rows + vocab * 5 + dim)
+    if softmax:  # grad_logits as the row kernel writes them
+        x = torch.randn(rows, vocab, device=DEV, generator=g) * 3.0
+        p = torch.softmax(x, dim=1)
+        lab = torch.randint(0, vocab, (rows,), device=DEV, generator=g)
+        p[torch.arange(rows, device=DEV), lab] -= 1.0
+        p[::7] = 0.0
+        gl = p.to(torch.bfloat16)
+        del x, p
+    else:
+        gl = torch.randn(rows, vocab, device=DEV, generator=g).to(torch.bfloat16)
+    h = torch.randn(rows, dim, device=DEV, generator=g).to(torch.bfloat16)
+    out, guard = _grad_w(gl, h)
+    assert guard
+    exact = torch.matmul(gl.double().t(), h.double())
+    absum = torch.matmul(gl.double().abs().t(), h.double().abs())
+    lib_out = torch.matmul(gl.t(), h)
+    torch.cuda.synchronize()
+    err = (out.double() - exact).abs()
+    bound = _bf16_ulp(exact) + absum * 2.0 ** -20
+    worst = float((err / bound).max())
+    print(f"{rows}x{vocab}x{dim}: worst |err| / bound {worst:.3f}")
+    assert worst <= 1.0
+    d = (out.double() - lib_out.double()).abs()
+    assert bool((d <= _bf16_ulp(torch.maximum(out.double().abs(), lib_out.double().abs())) + absum * 2.0 ** -19).all())
+    same = float((out.view(torch.int16) == lib_out.view(torch.int16)).double().mean())
+    print(f"  equal to torch.matmul on {same:.5f} of the elements")
+    assert same >= 0.99
+    again, _ = _grad_w(gl, h)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+
+
+def test_grad_w_gemm_full_chunk_vs_library():
+    """The 8192-row chunk of the Qwen3-0.6B head (the op's MI355X sizing): against torch.matmul,
+    within one bf16 ulp plus both fp32 budgets, equal on at least 99% of the elements."""
+    rows, vocab, dim = 8192, 151936, 1024
+    g = torch.Generator(device=DEV).manual_seed(81920)
+    gl = (torch.randn(rows, vocab, device=DEV, generator=g) * 1e-3).to(torch.bfloat16)
+    h = torch.randn(rows, dim, device=DEV, generator=g).to(torch.bfloat16)
+    out, guard = _grad_w(gl, h)
+    assert guard
+    lib_out = torch.matmul(gl.t(), h)
+    same = 0.0
+    for s in range(0, vocab, 16384):
+        e = min(s + 16384, vocab)
+        absum = torch.matmul(gl[:, s:e].float().abs().t(), h.float().abs()).double()
+        o, l_ = out[s:e].double(), lib_out[s:e].double()
+        assert bool(((o - l_).abs() <= _bf16_ulp(torch.maximum(o.abs(), l_.abs())) + absum * 2.0 ** -19).all())
+        same += float((out[s:e].view(torch.int16) == lib_out[s:e].view(torch.int16)).double().sum())
+    same /= vocab * dim
+    print(f"equal to torch.matmul on {same:.5f} of the elements")
+    assert same >= 0.99
+
+
+def test_grad_w_gemm_argument_checks():
+    """Row counts off a multiple of 64, vocab or dim off a multiple of 8 and misaligned pointers
+    are refused before any launch."""
+    native, lib, stream = _lib()
+    t = torch.empty(1 << 16, dtype=torch.bfloat16, device=DEV)
+    p = t.data_ptr()
+    for rows, vocab, dim in ((0, 64, 64), (100, 64, 64), (64, 60, 64), (64, 64, 60), (64, 0, 64)):
+        assert lib.tm_ce_grad_w_bf16(p, p, p, rows, vocab, dim, stream) < 0
+    assert lib.tm_ce_grad_w_bf16(p + 2, p, p, 64, 8, 8, stream) < 0
+    assert b"aligned" in lib.tm_last_error()

@@ -284,7 +284,7 @@ def test_ce_grad_w_fold_bit_exact(k, accumulate, scaled, n, offset):
     assert np.array_equal(a, w), np.argwhere(a != w)[:5]
 
 
-@pytest.mark.parametrize("chunk", [700, 350, 256, 175, 100, 80, 40])
+@pytest.mark.parametrize("chunk", [700, 350, 256, 175, 128, 100, 80, 64, 40])
 def test_fused_linear_ce_grad_w_equals_chunkwise_reference_ops(chunk):
     """Folding the chunks' hand-overs and deferring the last chunk change nothing: grad_W of
     the op with 1, 2, 3, 4, 7, 9 and 18 chunks (folds of 8 in forward, the rest with the last
@@ -316,7 +316,7 @@ def _chunk_loop_on_the_same_kernels(hidden, weight, labels, chunk, grad_out):
     and row kernel: a zero fp32 grad_W, `+=` of each chunk's bf16 grad_W, `grad_hidden[s:e] =
     gh`, then both scaled by grad_out / n_valid (grad_h by its bf16 rounding)."""
     from torchure_amd import _native
-    from torchure_amd.loss.fused_linear_ce import GradHidden
+    from torchure_amd.loss.fused_linear_ce import GradHidden, _grad_w, _logits
 
     n, v = hidden.shape[0], weight.shape[0]
     lib = _native.lib()
@@ -328,13 +328,13 @@ def _chunk_loop_on_the_same_kernels(hidden, weight, labels, chunk, grad_out):
     grad_h = GradHidden(w, [min(chunk, n - s) for s in range(0, n, chunk)], lib, stream)
     for s in range(0, n, chunk):
         e = min(s + chunk, n)
-        logits = torch.matmul(hidden[s:e], w.t())
+        logits = _logits(hidden[s:e], w, lib, stream)
         _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, -100,
                                           row_loss[s:].data_ptr(), stream), "tm_ce_rows_bf16")
         gh = torch.empty((e - s, w.shape[1]), dtype=torch.bfloat16, device=DEV)
         grad_h(logits, gh)
         gh_ref[s:e] = gh
-        gw_ref += torch.matmul(logits.t(), hidden[s:e])
+        gw_ref += _grad_w(logits, hidden[s:e], lib, stream)
     n_valid = (labels != -100).sum().clamp_min(1)
     scale = torch.tensor(grad_out, device=DEV) / n_valid
     gw_ref.mul_(scale)

@@ -109,6 +109,8 @@ _SIGNATURES = {
     "tm_ce_grad_h_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "tm_ce_grad_h_bf16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp]),
     "tm_ce_transpose_bf16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
+    "tm_ce_logits_bf16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "tm_ce_grad_w_bf16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
 }
 
 EXPORTED = tuple(_SIGNATURES)

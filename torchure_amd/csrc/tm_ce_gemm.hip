@@ -1,4 +1,5 @@
-// tm_ce_gemm.hip -- gfx950 bf16 MFMA GEMM for grad_hidden of the fused linear + cross-entropy.
+// tm_ce_gemm.hip -- gfx950 bf16 MFMA GEMMs of the fused linear + cross-entropy: the logits
+// (logits_gemm_kernel, below) and grad_hidden (grad_h_gemm_kernel).
 //
 // Per chunk of rows the reference computes grad_h = grad_logits @ W
 // (torchure/loss/fused_linear_ce.py:55, a bf16 matmul: fp32 accumulation, bf16 result), with
@@ -39,6 +40,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 template <typename... A>
 int gemm_fail(int code, const char* fmt, A... args) {
@@ -201,6 +204,382 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(uint16_t* __restric
   }
 }
 
+// ------------------------------------------------------------------ logits = hidden @ W^T
+//
+// fused_linear_ce.py:38 `logits = h @ w.t()` per chunk: C (rows x vocab) = A (rows x dim) times
+// B (vocab x dim) transposed, both operands K-contiguous (K = dim), bf16 in and out, fp32
+// accumulation. A 256 x 256 output tile per workgroup of 4 wave64 (2 x 2), each wave 128 x 128
+// with 256 fp32 accumulators (the AGPRs) on v_mfma_f32_32x32x16_bf16. Operands stream
+// global -> LDS (global_load_lds, 16 bytes a lane, 1 KB = 8 rows of a 64-deep K slice per
+// instruction) into two 64 KB stages whose 128-byte rows hold their 16-byte chunks at slot
+// c ^ ((row >> 1) & 7), as in grad_h_gemm_kernel. Schedule per 64-deep stage (4 K16 steps):
+//   - the next step's 8 fragments (16-byte LDS reads, inline asm) are issued one per two MFMAs
+//     of the current step, so the reads run under the MFMAs; sched_barrier pins that order and
+//     an `s_waitcnt lgkmcnt(0)` that names the fragments as operands keeps every MFMA behind
+//     the wait for its data;
+//   - the stage barrier sits at the start of the last K16 step: after it, that step's MFMAs
+//     run while the next stage's first fragments are read and the 16 loads of the stage after
+//     next are issued into the buffer just finished. No step waits on LDS right after a barrier.
+// Operand roles are swapped (the MFMA's first operand is the weight tile), so a lane holds 4
+// consecutive output columns of one row; the tile is converted to bf16 (RNE, v_cvt_pk_bf16_f32)
+// into LDS rows of 256 B (+16 B pad) and written back in whole rows, 16 bytes a lane: writing
+// 8-byte pieces of 32 rows per instruction straight from the accumulators made the L2 take
+// 16-byte partial-line writes, twice as many L2 requests as the operand reads, and cost 12%.
+// Rows past `rows` and columns past `vocab` load a clamped (valid) row and are not stored.
+// Tile order: workgroup w runs on XCD w % 8, which takes a contiguous range of tile positions;
+// within it, groups of gm x gn tiles (gm * gn = 32, one per CU of the XCD) run together so that
+// their operand panels are read from HBM about once per group and served from that XCD's L2.
+
+constexpr int kLgTile = 256;                                    // output tile edge
+constexpr int kLgStage = 2 * kLgTile * kSliceK * 2;             // 64 KB: A and B slices
+constexpr int kLgPitch = 272;                                   // output staging row pitch
+constexpr int kLgLds = 4 * 128 * kLgPitch > 2 * kLgStage ? 4 * 128 * kLgPitch : 2 * kLgStage;  // 139,264 B
+
+// Tile of position p: n-blocks of gn tile columns; inside each, m-blocks of gm tile rows, a
+// block's gm x gn tiles consecutive in p.
+__device__ __forceinline__ void lg_tile_of(int p, int tiles_m, int tiles_n, int gm, int gn, int& tm, int& tn) {
+  const int per_nb = tiles_m * gn;
+  const int nb = p / per_nb, rem = p - nb * per_nb;
+  const int gn_eff = min(gn, tiles_n - nb * gn);
+  const int mb = rem / (gm * gn_eff), rem2 = rem - mb * gm * gn_eff;
+  tm = mb * gm + rem2 / gn_eff;
+  tn = nb * gn + rem2 % gn_eff;
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2 h = __builtin_convertvector(f32x2{a, b}, bf16x2);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+template <bool kN, bool kN2>
+struct LgFlags {
+  static constexpr bool kNextV = kN, kNext2V = kN2;
+};
+
+__global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                                          uint16_t* __restrict__ C, int M, int N, int K, int tiles_m,
+                                                          int tiles_n, int gm, int gn) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int T = tiles_m * tiles_n;
+  const int t8 = (T + 7) / 8;
+  const int p = (blockIdx.x % 8) * t8 + blockIdx.x / 8;  // XCD blockIdx % 8 takes positions [x t8, (x+1) t8)
+  if (p >= T) return;
+  int tm, tn;
+  lg_tile_of(p, tiles_m, tiles_n, gm, gn, tm, tn);
+  const int m0 = tm * kLgTile, n0 = tn * kLgTile;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n_it = K / kSliceK;
+
+  // Load j of this wave fills LDS rows 8 q .. 8 q + 7 of [A tile; B tile], q = 16 wave + j; the
+  // lane loads 16-byte chunk (lane % 8) ^ ((row >> 1) & 7) of row 8 q + lane / 8 into slot lane % 8.
+  const uint16_t* src[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int q = wave * 16 + j;
+    const int r = (q % 32) * 8 + lane / 8;
+    const int c = (lane % 8) ^ ((r >> 1) & 7);
+    src[j] = (q < 32 ? A + static_cast<int64_t>(min(m0 + r, M - 1)) * K
+                     : B + static_cast<int64_t>(min(n0 + r, N - 1)) * K) + c * 8;
+  }
+  auto load = [&](int it, int stage, int j) {
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[j] + it * kSliceK),
+                                     (void __attribute__((address_space(3)))*)(smem + stage * kLgStage + (wave * 16 + j) * 1024),
+                                     16, 0, 0);
+  };
+  // Fragment reads: lane reads row R0 + lane % 32 (R0 a multiple of 32), chunk 2 kk + lane / 32,
+  // at slot (2 kk) ^ tx with tx = (lane / 32) ^ ((lane >> 1) & 7).
+  const int tx = (lane >> 5) ^ ((lane >> 1) & 7);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + (lane & 31) * 128;
+  uint32_t vk[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) vk[kk] = lds0 + (((2 * kk) ^ tx) * 16);
+  const uint32_t offA = wm * 128 * 128, offB = kLgTile * 128 + wn * 128 * 128;
+
+  f32x16 acc[4][4];  // [n block][m block]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+#define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
+#define TM_WAIT8(f)                                                                                       \
+  asm volatile("s_waitcnt lgkmcnt(0)"                                                                   \
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]))
+  // fragment g: g < 4 -> weight (n) block g, g >= 4 -> hidden (m) block g - 4
+  bf16x8 f0[8], f1[8];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) load(0, 0, j);
+  if (n_it > 1) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) load(1, 1, j);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int g = 0; g < 8; ++g) TM_RD(f0[g], vk[0] + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+  TM_WAIT8(f0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto stage = [&](int i, auto step) {
+    constexpr bool kNext = decltype(step)::kNextV, kNext2 = decltype(step)::kNext2V;
+    const int s = i & 1;
+    const uint32_t soff = s * kLgStage, noff = (s ^ 1) * kLgStage;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x8* cur = (kk & 1) ? f1 : f0;
+      bf16x8* nxt = (kk & 1) ? f0 : f1;
+      if (kk == 3 && kNext) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wave's loads of stage i + 1 are in LDS
+        __builtin_amdgcn_s_barrier();               // every wave's; and stage i's reads are done
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        if (kk < 3) {
+          TM_RD(nxt[g], vk[kk + 1] + soff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+        } else if (kNext) {
+          TM_RD(nxt[g], vk[0] + noff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+        }
+        if (kk == 3 && kNext2) {
+          load(i + 2, s, 2 * g);
+          load(i + 2, s, 2 * g + 1);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int idx = 2 * g + h, ii = idx / 4, jj = idx % 4;
+          acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], acc[ii][jj], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (kk < 3 || kNext) {
+        TM_WAIT8(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  int i = 0;
+  for (; i + 2 < n_it; ++i) stage(i, LgFlags<true, true>{});
+  if (i + 1 < n_it) stage(i++, LgFlags<true, false>{});
+  if (i < n_it) stage(i, LgFlags<false, false>{});
+#undef TM_RD
+#undef TM_WAIT8
+
+  // D[n][m] of a 32 x 32 block: register r of lane l holds n = 8 (r / 4) + 4 (l / 32) + r % 4,
+  // m = l % 32. Each wave stages its 128 x 128 bf16 tile in LDS, then writes whole rows.
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();  // every wave is done reading the operand stages
+  uint8_t* tile = smem + wave * 128 * kLgPitch;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int mr = jj * 32 + (lane & 31), nc = ii * 32 + 8 * q + 4 * (lane >> 5);
+        u32x2 o;
+        o.x = pack_bf16x2(acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1]);
+        o.y = pack_bf16x2(acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]);
+        *(u32x2*)(tile + mr * kLgPitch + nc * 2) = o;
+      }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave reads back only its own rows
+  const int mb = m0 + wm * 128, nb = n0 + wn * 128;
+  const bool vec = (N & 7) == 0;
+#pragma unroll 4
+  for (int it = 0; it < 32; ++it) {
+    const int mr = it * 4 + (lane >> 4), ch = lane & 15;
+    const int m = mb + mr, n = nb + ch * 8;
+    if (m >= M) continue;
+    const u32x4 v = *(const u32x4*)(tile + mr * kLgPitch + ch * 16);
+    uint16_t* dst = C + static_cast<int64_t>(m) * N + n;
+    if (vec && n + 8 <= N) {
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst));  // streamed out: keep L2 for operands
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1)));
+    }
+  }
+}
+
+// ------------------------------------------------------- grad_W = grad_logits^T @ hidden
+//
+// fused_linear_ce.py:57 `gw = grad_logits.t() @ h` per chunk: C (vocab x dim) = G^T H with
+// G = grad_logits (rows x vocab) and H = hidden (rows x dim), both stored with the contraction
+// (rows) outermost. Same 256 x 256 tiles, 4 waves of 128 x 128, two 64 KB stages and the same
+// schedule as logits_gemm_kernel; a stage holds 64 rows x 256 columns of each operand, 512-byte
+// LDS rows whose 16-byte chunks sit at slot c ^ (4 (row & 3)). MFMA operands need 8 consecutive
+// rows of one column per lane: gfx950's transposing LDS read ds_read_b64_tr_b16 gives, in each
+// 16-lane group, lane i element i % 4 of the 8-byte pieces addressed by lanes i/4, i/4 + 4,
+// i/4 + 8 and i/4 + 12, so with lane s addressing row s/4 at column 4 (s % 4) lane i receives
+// rows 0-3 of column i; two such reads (rows +0 and +4) make a fragment. The slot swizzle puts
+// the 4 rows of a read, and the 32 columns two 16-lane groups read together, on 16 different
+// 16-byte bank groups. Columns past vocab or dim load a clamped (valid) column and are not stored.
+
+constexpr int kGwOp = 64 * 512;       // one operand's stage: 64 rows x 256 bf16
+constexpr int kGwStage = 2 * kGwOp;   // 64 KB
+
+__global__ __launch_bounds__(256) void grad_w_gemm_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ H,
+                                                          uint16_t* __restrict__ C, int V, int D, int K, int tiles_v,
+                                                          int tiles_d, int gm, int gn) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int T = tiles_v * tiles_d;
+  const int t8 = (T + 7) / 8;
+  const int p = (blockIdx.x % 8) * t8 + blockIdx.x / 8;
+  if (p >= T) return;
+  int tv, td;
+  lg_tile_of(p, tiles_v, tiles_d, gm, gn, tv, td);
+  const int v0 = tv * kLgTile, d0 = td * kLgTile;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;  // vocab half, dim half
+  const int n_it = K / kSliceK;
+
+  // Load j of this wave, q = 16 wave + j: operand q / 32 (G, then H), rows 2 (q % 32) and
+  // 2 (q % 32) + 1 of the stage; slot lane % 32 of row 2 (q % 32) + lane / 32 takes logical chunk
+  // (lane % 32) ^ (4 (row & 3)).
+  const uint16_t* src[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int q = wave * 16 + j;
+    const int kr = 2 * (q % 32) + lane / 32;
+    const int c = (lane % 32) ^ (4 * (kr & 3));
+    src[j] = q < 32 ? G + static_cast<int64_t>(kr) * V + min(v0 + 8 * c, V - 8)
+                    : H + static_cast<int64_t>(kr) * D + min(d0 + 8 * c, D - 8);
+  }
+  const int64_t step_g = static_cast<int64_t>(kSliceK) * V, step_h = static_cast<int64_t>(kSliceK) * D;
+  auto load = [&](int it, int stage, int j) {
+    const int q = wave * 16 + j;
+    __builtin_amdgcn_global_load_lds(
+        (const void __attribute__((address_space(1)))*)(src[j] + it * (q < 32 ? step_g : step_h)),
+        (void __attribute__((address_space(3)))*)(smem + stage * kGwStage + q * 1024), 16, 0, 0);
+  };
+  // Fragment of 32-column block b at K16 step kk: lane l (s = l % 16) reads row
+  // 16 kk + 8 (l / 32) + s / 4 (+4 for the second half) at column 32 b + 16 ((l / 16) % 2) + 4 (s % 4),
+  // whose physical chunk is 4 (b ^ (s / 4)) + ((l / 16) % 2) * 2 + (s % 4) / 2 past the wave's 16.
+  const int s16 = lane & 15, s4 = s16 >> 2;
+  const int lc = ((lane >> 4) & 1) * 2 + ((s16 & 3) >> 1);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const uint32_t rowb = (8 * (lane >> 5) + s4) * 512 + (s16 & 1) * 8;
+  uint32_t bv[4], bd[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    bv[b] = lds0 + rowb + (16 * wm + 4 * (b ^ s4) + lc) * 16;
+    bd[b] = lds0 + kGwOp + rowb + (16 * wn + 4 * (b ^ s4) + lc) * 16;
+  }
+
+  f32x16 acc[4][4];  // [dim block][vocab block]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+#define TM_TR(dst, base, imm) asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
+#define TM_WAIT16(f)                                                                                        \
+  asm volatile("s_waitcnt lgkmcnt(0)"                                                                     \
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), \
+                 "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]),      \
+                 "+v"(f[15]))
+  // half-fragment h = 2 g + r: g < 4 -> dim block g, g >= 4 -> vocab block g - 4; r: rows +0 / +4
+  bf16x4 f0[16], f1[16];
+  auto rd = [&](bf16x4* f, uint32_t soff, int kk, int h) {
+    const int g = h >> 1, r = h & 1;
+    TM_TR(f[h], (g < 4 ? bd[g] : bv[g - 4]) + soff, kk * 16 * 512 + r * 4 * 512);
+  };
+#pragma unroll
+  for (int j = 0; j < 16; ++j) load(0, 0, j);
+  if (n_it > 1) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) load(1, 1, j);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int h = 0; h < 16; ++h) rd(f0, 0, 0, h);
+  TM_WAIT16(f0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto stage = [&](int i, auto step) {
+    constexpr bool kNext = decltype(step)::kNextV, kNext2 = decltype(step)::kNext2V;
+    const int s = i & 1;
+    const uint32_t soff = s * kGwStage, noff = (s ^ 1) * kGwStage;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x4* cur = (kk & 1) ? f1 : f0;
+      bf16x4* nxt = (kk & 1) ? f0 : f1;
+      if (kk == 3 && kNext) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {  // one half-fragment read, at most one load, one MFMA
+        if (kk < 3) rd(nxt, soff, kk + 1, q);
+        else if (kNext) rd(nxt, noff, 0, q);
+        if (kk == 3 && kNext2) load(i + 2, s, q);
+        const int ii = q / 4, jj = q % 4;
+        const bf16x8 a = __builtin_shufflevector(cur[2 * ii], cur[2 * ii + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+        const bf16x8 b = __builtin_shufflevector(cur[8 + 2 * jj], cur[9 + 2 * jj], 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[ii][jj], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (kk < 3 || kNext) {
+        TM_WAIT16(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  int i = 0;
+  for (; i + 2 < n_it; ++i) stage(i, LgFlags<true, true>{});
+  if (i + 1 < n_it) stage(i++, LgFlags<true, false>{});
+  if (i < n_it) stage(i, LgFlags<false, false>{});
+#undef TM_TR
+#undef TM_WAIT16
+
+  // D[d][v] of a block: lane holds 4 consecutive dim columns of one vocab row (as the logits)
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  uint8_t* tile = smem + wave * 128 * kLgPitch;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int vr = jj * 32 + (lane & 31), dc = ii * 32 + 8 * q + 4 * (lane >> 5);
+        u32x2 o;
+        o.x = pack_bf16x2(acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1]);
+        o.y = pack_bf16x2(acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]);
+        *(u32x2*)(tile + vr * kLgPitch + dc * 2) = o;
+      }
+  __builtin_amdgcn_s_waitcnt(0);
+  const int vb = v0 + wm * 128, db = d0 + wn * 128;
+#pragma unroll 4
+  for (int it = 0; it < 32; ++it) {
+    const int vr = it * 4 + (lane >> 4), ch = lane & 15;
+    const int v = vb + vr, d = db + ch * 8;
+    if (v >= V || d >= D) continue;  // D is a multiple of 8: a group is whole or out
+    const u32x4 val = *(const u32x4*)(tile + vr * kLgPitch + ch * 16);
+    __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(C + static_cast<int64_t>(v) * D + d));
+  }
+}
+
+// Tile groups per XCD round: with few row tiles the whole hidden chunk sits in every XCD's L2,
+// so a round takes one row of 32 weight panels (measured 0.334 ms at 1024 x 151,936 x 1024
+// against 0.365 for 4 x 8); with more, 4 x 8 keeps the panels of a round within the L2.
+void logits_groups(int64_t tiles_m, int& gm, int& gn) {
+  gm = tiles_m <= 4 ? 1 : (tiles_m <= 8 ? 2 : 4);
+  gn = 32 / gm;
+}
+
 // Splits of the K range: a multiple of 8 (one group of splits per XCD), chosen by a cost model
 // of the launch. One 128 KB-LDS workgroup fits a CU, so tiles x S workgroups run in
 // ceil(tiles x S / 256) rounds; a workgroup takes about 2 us per 64-deep K slice (256 x 256 x 64
@@ -227,30 +606,34 @@ int64_t splits_for(int64_t rows, int64_t vocab, int64_t dim) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The kernel's 128 KB of dynamic LDS exceeds the 64 KB default: the attribute is set once per
-// device, with that device current, before the first launch there.
+// The GEMM kernels' dynamic LDS (128 KB, 136 KB, 136 KB) exceeds the 64 KB default: the attribute is set
+// once per device and kernel, with that device current, before the first launch there.
 constexpr int kMaxDevices = 64;
 std::mutex g_lds_mu;
-bool g_lds_set[kMaxDevices] = {};
+bool g_lds_set[3][kMaxDevices] = {};
 
-hipError_t allow_lds(hipStream_t stream) {
+hipError_t allow_lds(hipStream_t stream, int which) {
   int dev = -1;
   hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_lds_mu);
-  if (g_lds_set[dev]) return hipSuccess;
+  if (g_lds_set[which][dev]) return hipSuccess;
   int cur = -1;
   e = hipGetDevice(&cur);
   if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
   if (e == hipSuccess)
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(grad_h_gemm_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+    e = which == 0   ? hipFuncSetAttribute(reinterpret_cast<const void*>(grad_h_gemm_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds)
+        : which == 1 ? hipFuncSetAttribute(reinterpret_cast<const void*>(logits_gemm_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLgLds)
+                     : hipFuncSetAttribute(reinterpret_cast<const void*>(grad_w_gemm_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLgLds);
   if (cur >= 0 && cur != dev) {
     const hipError_t back = hipSetDevice(cur);
     if (e == hipSuccess) e = back;
   }
-  if (e == hipSuccess) g_lds_set[dev] = true;
+  if (e == hipSuccess) g_lds_set[which][dev] = true;
   return e;
 }
 
@@ -280,7 +663,7 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
     return gemm_fail(TM_EINVAL, "tm_ce_grad_h_bf16: workspace of %zu bytes, %zu needed", ws_bytes,
                      tm_ce_grad_h_workspace_bytes(rows, vocab, dim));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t lds = allow_lds(s);
+  const hipError_t lds = allow_lds(s, 0);
   if (lds != hipSuccess)
     return gemm_fail(TM_ELAUNCH, "tm_ce_grad_h_bf16: LDS attribute: %s", hipGetErrorString(lds));
   const int64_t splits = splits_for(rows, vocab, dim);
@@ -298,6 +681,59 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
                      partials, d_grad_h, n, static_cast<int>(splits));
   e = hipGetLastError();
   if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "grad_h_reduce_kernel: launch failed: %s", hipGetErrorString(e));
+  return TM_OK;
+}
+
+int tm_ce_logits_bf16(uint16_t* d_logits, const uint16_t* d_hidden, const uint16_t* d_weight, int64_t rows,
+                      int64_t vocab, int64_t dim, void* stream) {
+  if (rows <= 0 || vocab <= 0 || dim <= 0 || dim % kSliceK)
+    return gemm_fail(TM_EINVAL, "tm_ce_logits_bf16: rows %lld and vocab %lld must be positive, dim %lld a positive "
+                     "multiple of %d", (long long)rows, (long long)vocab, (long long)dim, kSliceK);
+  const int64_t tiles_m = (rows + kLgTile - 1) / kLgTile, tiles_n = (vocab + kLgTile - 1) / kLgTile;
+  if (rows > 0x7FFFFFFF || vocab > 0x7FFFFFFF || dim > 0x7FFFFFFF || tiles_m * tiles_n > 0x7FFFFFF0)
+    return gemm_fail(TM_EINVAL, "tm_ce_logits_bf16: %lld x %lld x %lld is too large", (long long)rows,
+                     (long long)vocab, (long long)dim);
+  if (!d_logits || !d_hidden || !d_weight) return gemm_fail(TM_EINVAL, "tm_ce_logits_bf16: null pointer");
+  if (!aligned16(d_logits) || !aligned16(d_hidden) || !aligned16(d_weight))
+    return gemm_fail(TM_EINVAL, "tm_ce_logits_bf16: pointers must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t lds = allow_lds(s, 1);
+  if (lds != hipSuccess)
+    return gemm_fail(TM_ELAUNCH, "tm_ce_logits_bf16: LDS attribute: %s", hipGetErrorString(lds));
+  int gm, gn;
+  logits_groups(tiles_m, gm, gn);
+  const int64_t grid = (tiles_m * tiles_n + 7) / 8 * 8;
+  hipLaunchKernelGGL(logits_gemm_kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), kLgLds, s, d_hidden, d_weight,
+                     d_logits, static_cast<int>(rows), static_cast<int>(vocab), static_cast<int>(dim),
+                     static_cast<int>(tiles_m), static_cast<int>(tiles_n), gm, gn);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "logits_gemm_kernel: launch failed: %s", hipGetErrorString(e));
+  return TM_OK;
+}
+
+int tm_ce_grad_w_bf16(uint16_t* d_grad_w, const uint16_t* d_grad_logits, const uint16_t* d_hidden, int64_t rows,
+                      int64_t vocab, int64_t dim, void* stream) {
+  if (rows <= 0 || vocab <= 0 || dim <= 0 || rows % kSliceK || vocab % 8 || dim % 8)
+    return gemm_fail(TM_EINVAL, "tm_ce_grad_w_bf16: rows %lld must be a positive multiple of %d, vocab %lld and dim "
+                     "%lld positive multiples of 8", (long long)rows, kSliceK, (long long)vocab, (long long)dim);
+  const int64_t tiles_v = (vocab + kLgTile - 1) / kLgTile, tiles_d = (dim + kLgTile - 1) / kLgTile;
+  if (rows > 0x7FFFFFFF || vocab > 0x7FFFFFFF || dim > 0x7FFFFFFF || tiles_v * tiles_d > 0x7FFFFFF0)
+    return gemm_fail(TM_EINVAL, "tm_ce_grad_w_bf16: %lld x %lld x %lld is too large", (long long)rows,
+                     (long long)vocab, (long long)dim);
+  if (!d_grad_w || !d_grad_logits || !d_hidden) return gemm_fail(TM_EINVAL, "tm_ce_grad_w_bf16: null pointer");
+  if (!aligned16(d_grad_w) || !aligned16(d_grad_logits) || !aligned16(d_hidden))
+    return gemm_fail(TM_EINVAL, "tm_ce_grad_w_bf16: pointers must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t lds = allow_lds(s, 2);
+  if (lds != hipSuccess)
+    return gemm_fail(TM_ELAUNCH, "tm_ce_grad_w_bf16: LDS attribute: %s", hipGetErrorString(lds));
+  const int gn = static_cast<int>(tiles_d < 4 ? tiles_d : 4), gm = 32 / gn;  // a round of 32: 8 x 4
+  const int64_t grid = (tiles_v * tiles_d + 7) / 8 * 8;
+  hipLaunchKernelGGL(grad_w_gemm_kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), kLgLds, s, d_grad_logits,
+                     d_hidden, d_grad_w, static_cast<int>(vocab), static_cast<int>(dim), static_cast<int>(rows),
+                     static_cast<int>(tiles_v), static_cast<int>(tiles_d), gm, gn);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "grad_w_gemm_kernel: launch failed: %s", hipGetErrorString(e));
   return TM_OK;
 }
 

@@ -7,14 +7,17 @@ semantics, :22-24), computes grad_hidden and grad_weight during the forward pass
 (:42-58) and scales them in place by grad_out / n_valid in backward (:94-127).
 
 Per chunk of rows:
-  logits = h @ W^T                  bf16 GEMM (hipBLASLt, through torch.matmul)
+  logits = h @ W^T                  bf16 GEMM: tm_ce_logits_bf16, this build's MFMA GEMM, for dim a
+                                    multiple of 64 (torch.matmul on other shapes)
   tm_ce_rows_bf16                   one fused kernel: logsumexp, per-row loss and
                                     grad_logits = bf16(softmax - onehot), in place
   grad_h = grad_logits @ W          bf16 GEMM: tm_ce_grad_h_bf16, a split-K MFMA GEMM with a
                                     fixed-order reduction, on chunks with at most 64 output tiles
                                     of 256 x 256 (rows and D multiples of 256, V of 64: up to 4096
                                     rows for D = 1024); hipBLASLt on other shapes
-  grad_W += grad_logits^T @ h       bf16 GEMM, then tm_ce_grad_w_fold into fp32
+  grad_W += grad_logits^T @ h       bf16 GEMM: tm_ce_grad_w_bf16, this build's MFMA GEMM, for rows a
+                                    multiple of 64 (torch.matmul on other shapes), then
+                                    tm_ce_grad_w_fold into fp32
 then tm_ce_loss sums the per-row losses in a fixed order (deterministic).
 
 The last chunk's bf16 grad_W is not added in forward: it waits for backward, where
@@ -185,6 +188,46 @@ def _mean_loss(row_loss, labels, n, ignore_index, lib, stream):
     return out3[2].clone(), out3[1:2]
 
 
+def logits_gemm_fits(h: torch.Tensor, w: torch.Tensor) -> bool:
+    """Chunks whose logits run on this build's GEMM (tm_ce_logits_bf16): bf16 operands, both
+    contiguous and 16-byte aligned, dim a multiple of 64. Other shapes take torch.matmul."""
+    return (h.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and h.dim() == 2 and w.dim() == 2
+            and h.shape[1] == w.shape[1] and h.shape[1] % 64 == 0 and h.shape[0] > 0 and w.shape[0] > 0
+            and h.is_contiguous() and w.is_contiguous() and h.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+
+
+def _logits(h: torch.Tensor, w: torch.Tensor, lib, stream) -> torch.Tensor:
+    """logits = h @ w.T (fused_linear_ce.py:38): a bf16 GEMM, fp32 accumulation, bf16 result."""
+    if not logits_gemm_fits(h, w):
+        return _bf16(torch.matmul(h, w.t()))
+    rows, dim = h.shape
+    out = torch.empty((rows, w.shape[0]), dtype=torch.bfloat16, device=h.device)
+    _native.check(lib.tm_ce_logits_bf16(out.data_ptr(), h.data_ptr(), w.data_ptr(), rows, w.shape[0], dim, stream),
+                  "tm_ce_logits_bf16")
+    return out
+
+
+def grad_w_gemm_fits(g: torch.Tensor, h: torch.Tensor) -> bool:
+    """Chunks whose grad_W runs on this build's GEMM (tm_ce_grad_w_bf16): bf16 operands, both
+    contiguous and 16-byte aligned, rows a multiple of 64, vocab and dim multiples of 8. Other
+    shapes take torch.matmul."""
+    return (g.dtype == torch.bfloat16 and h.dtype == torch.bfloat16 and g.dim() == 2 and h.dim() == 2
+            and g.shape[0] == h.shape[0] and g.shape[0] > 0 and g.shape[0] % 64 == 0 and g.shape[1] % 8 == 0
+            and h.shape[1] % 8 == 0 and g.shape[1] > 0 and h.shape[1] > 0 and g.is_contiguous() and h.is_contiguous()
+            and g.data_ptr() % 16 == 0 and h.data_ptr() % 16 == 0)
+
+
+def _grad_w(g: torch.Tensor, h: torch.Tensor, lib, stream) -> torch.Tensor:
+    """A chunk's gw = grad_logits.t() @ h (fused_linear_ce.py:57): bf16 GEMM, bf16 result (V x D)."""
+    if not grad_w_gemm_fits(g, h):
+        return torch.matmul(g.t(), h)
+    rows, vocab = g.shape
+    out = torch.empty((vocab, h.shape[1]), dtype=torch.bfloat16, device=g.device)
+    _native.check(lib.tm_ce_grad_w_bf16(out.data_ptr(), g.data_ptr(), h.data_ptr(), rows, vocab, h.shape[1], stream),
+                  "tm_ce_grad_w_bf16")
+    return out
+
+
 SPLITK_GRAD_H_MAX_TILES = 64
 
 
@@ -274,7 +317,7 @@ def _loss_only(hidden, weight, labels, ignore_index, chunk_size):
     row_loss = torch.empty(n, dtype=torch.float32, device=hidden.device)
     for s in range(0, n, chunk):
         e = min(s + chunk, n)
-        logits = _bf16(torch.matmul(hb[s:e], w.t()), dt)
+        logits = _logits(hb[s:e], w, lib, stream) if dt == torch.bfloat16 else _bf16(torch.matmul(hb[s:e], w.t()), dt)
         _native.check(rows_loss(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, int(ignore_index),
                                 row_loss[s:].data_ptr(), stream), "tm_ce_rows_loss")
         del logits
@@ -337,14 +380,14 @@ class _FusedLinearCE(torch.autograd.Function):
         for s in range(0, n, chunk):
             e = min(s + chunk, n)
             h = hb[s:e]
-            logits = _bf16(torch.matmul(h, w.t()))  # (C, V) bf16
+            logits = _logits(h, w, lib, stream)  # (C, V) bf16
             _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v,
                                               int(ignore_index), row_loss[s:].data_ptr(), stream),
                           "tm_ce_rows_bf16")
             if want_h:
                 grad_h_of(logits, grad_hidden[s:e])
             if want_w:
-                gw = torch.matmul(logits.t(), h)  # (V, D) bf16
+                gw = _grad_w(logits, h, lib, stream)  # (V, D) bf16
                 if e == n:
                     last_gw = gw
                 else:
