@@ -271,7 +271,9 @@ __global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __rest
   int tm, tn;
   lg_tile_of(p, tiles_m, tiles_n, gm, gn, tm, tn);
   const int m0 = tm * kLgTile, n0 = tn * kLgTile;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  // wave-uniform in a scalar register, so each load's LDS destination (M0) is scalar arithmetic
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int n_it = K / kSliceK;
 
@@ -436,7 +438,8 @@ __global__ __launch_bounds__(256) void grad_w_gemm_kernel(const uint16_t* __rest
   int tv, td;
   lg_tile_of(p, tiles_v, tiles_d, gm, gn, tv, td);
   const int v0 = tv * kLgTile, d0 = td * kLgTile;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;  // vocab half, dim half
   const int n_it = K / kSliceK;
 
