@@ -670,10 +670,11 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
 
 
 def run_ce_gemm(shapes, reps: int, dev, vocab: int = 151936):
-    """The fused CE's grad_h = grad_logits @ W (torchure/loss/fused_linear_ce.py:52) per chunk
-    shape: this build's split-K MFMA GEMM (tm_ce_grad_h_bf16, its fixed-order reduction
-    included) against torch.matmul (hipBLASLt) on the same bf16 operands, each timed over
-    `reps` launches after one warm-up, plus the once-per-call W^T transpose."""
+    """The fused CE's three products per chunk shape (rows x dim), each this build's MFMA GEMM
+    against torch.matmul (hipBLASLt) on the same bf16 operands, timed over `reps` launches after
+    one warm-up: logits = h @ W^T (fused_linear_ce.py:38, tm_ce_logits_bf16), grad_h =
+    grad_logits @ W (:52, the split-K tm_ce_grad_h_bf16 with its fixed-order reduction) and
+    grad_W = grad_logits^T @ h (:57, tm_ce_grad_w_bf16), plus the once-per-call W^T transpose."""
     import torch
 
     from torchure_amd import _native
@@ -709,11 +710,24 @@ def run_ce_gemm(shapes, reps: int, dev, vocab: int = 151936):
                                                "tm_ce_grad_h_bf16"))
             ms_l = timed(lambda: torch.matmul(a, w, out=o))
             fl = 2.0 * rows * vocab * dim
+            h = torch.randn(rows, dim, device=dev, generator=g).to(torch.bfloat16)
+            logits = torch.empty((rows, vocab), dtype=torch.bfloat16, device=dev)
+            ms_lg = timed(lambda: _native.check(lib.tm_ce_logits_bf16(logits.data_ptr(), h.data_ptr(), w.data_ptr(),
+                                                                      rows, vocab, dim, stream), "tm_ce_logits_bf16"))
+            ms_lg_l = timed(lambda: torch.matmul(h, w.t(), out=logits))
+            gw = torch.empty((vocab, dim), dtype=torch.bfloat16, device=dev)
+            ms_gw = timed(lambda: _native.check(lib.tm_ce_grad_w_bf16(gw.data_ptr(), a.data_ptr(), h.data_ptr(), rows,
+                                                                      vocab, dim, stream), "tm_ce_grad_w_bf16"))
+            ms_gw_l = timed(lambda: torch.matmul(a.t(), h, out=gw))
             out["shapes"]["%dx%d" % (rows, dim)] = {
                 "splitk_ms": round(ms_s, 4), "splitk_TFLOPs": round(fl / ms_s / 1e9, 1),
                 "hipblaslt_ms": round(ms_l, 4), "hipblaslt_TFLOPs": round(fl / ms_l / 1e9, 1),
-                "splits": nb // (rows * dim * 4)}
-            del a, o, ws
+                "splits": nb // (rows * dim * 4),
+                "logits_ms": round(ms_lg, 4), "logits_TFLOPs": round(fl / ms_lg / 1e9, 1),
+                "logits_hipblaslt_ms": round(ms_lg_l, 4), "logits_hipblaslt_TFLOPs": round(fl / ms_lg_l / 1e9, 1),
+                "grad_w_ms": round(ms_gw, 4), "grad_w_TFLOPs": round(fl / ms_gw / 1e9, 1),
+                "grad_w_hipblaslt_ms": round(ms_gw_l, 4), "grad_w_hipblaslt_TFLOPs": round(fl / ms_gw_l / 1e9, 1)}
+            del a, o, ws, h, logits, gw
         del w, wt
     return out
 

@@ -1,5 +1,6 @@
 // tm_ce_gemm.hip -- gfx950 bf16 MFMA GEMMs of the fused linear + cross-entropy: the logits
-// (logits_gemm_kernel, below) and grad_hidden (grad_h_gemm_kernel).
+// (logits_gemm_kernel), grad_W (grad_w_gemm_kernel), both further below, and grad_hidden
+// (grad_h_gemm_kernel, split-K, next).
 //
 // Per chunk of rows the reference computes grad_h = grad_logits @ W
 // (torchure/loss/fused_linear_ce.py:55, a bf16 matmul: fp32 accumulation, bf16 result), with
