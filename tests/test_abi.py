@@ -115,18 +115,20 @@ def test_argument_validation_without_gpu():
 
 
 def test_grad_h_gemm_workspace_and_shape_checks_without_gpu():
-    """The split-K grad_h GEMM: K splits a multiple of 8 (one group per XCD) picked by the
-    launch's cost model, fp32 partials of rows x dim per split; shapes it does not tile,
-    misaligned pointers and short workspaces are refused before any HIP call."""
+    """The split-K grad_h GEMM: K splits picked by the launch's cost model, fp32 partials of
+    rows x dim per split; shapes it does not tile, misaligned pointers and short workspaces are
+    refused before any HIP call."""
     lib = _native.lib()
     ws = lib.tm_ce_grad_h_workspace_bytes
     v = 151936
     assert ws(1024, v, 1024) == 16 * 1024 * 1024 * 4  # 16 tiles x 16 splits: one round of 256 CUs
     assert ws(2048, v, 1024) == 8 * 2048 * 1024 * 4
-    assert ws(1024, v, 2560) == 32 * 1024 * 2560 * 4  # 40 tiles x 32 splits: five full rounds
+    assert ws(4096, v, 1024) == 4 * 4096 * 1024 * 4
+    assert ws(8192, v, 1024) == 2 * 8192 * 1024 * 4  # 128 tiles x 2 splits
+    assert ws(1024, v, 2560) == 6 * 1024 * 2560 * 4  # 40 tiles x 6 splits: 240 workgroups
     assert ws(3072, v, 1024) == 16 * 3072 * 1024 * 4  # 48 x 16: three full rounds
-    assert ws(8192, v, 4096) == 8 * 8192 * 4096 * 4
-    assert ws(256, 640, 256) == 16 * 256 * 256 * 4  # 10 K slices: more splits only add partials
+    assert ws(8192, v, 4096) == 1 * 8192 * 4096 * 4  # 512 tiles fill two rounds by themselves
+    assert ws(256, 640, 256) == 10 * 256 * 256 * 4  # 10 K slices: one per split
     assert ws(1000, v, 1024) == 0 and ws(1024, v, 1000) == 0 and ws(0, v, 256) == 0 and ws(256, 100, 256) == 0
     fake = ctypes.c_void_p(0x1000)
     big = 1 << 40

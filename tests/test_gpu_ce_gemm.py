@@ -6,7 +6,7 @@ Checks:
 - the transpose bit for bit against torch's;
 - the GEMM against an fp64 product of the same bf16 operands: every element within one bf16
   ulp of the exact value plus 2^-20 of sum_k |a_ik b_kj| (the fp32 accumulation), at chunk
-  shapes from one output tile with more splits than K slices up to the Qwen3 head's 1024 x
+  shapes from one output tile split into single K slices up to the Qwen3 head's 1024 x
   151,936 x 1024 and a 4096-row chunk of a 2560-wide head;
 - against torch.matmul (hipBLASLt) on the same operands: within one bf16 ulp plus the two
   fp32 accumulation budgets everywhere, and equal on at least 99% of the elements (the two
@@ -82,7 +82,7 @@ def test_transpose_is_exact(rows, cols):
 
 
 @pytest.mark.parametrize("rows,vocab,dim,softmax", [
-    (256, 640, 256, False),        # one tile, 256 splits over 10 K slices: most splits empty
+    (256, 640, 256, False),        # one tile, 10 splits of one K slice each
     (256, 4096, 512, False),
     (512, 2048, 768, True),
     (1024, 151936, 1024, True),    # the Qwen3-0.6B head at the reference's 1024-row chunk

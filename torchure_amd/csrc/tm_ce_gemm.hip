@@ -1,30 +1,27 @@
-// tm_ce_gemm.hip -- gfx950 bf16 MFMA GEMMs of the fused linear + cross-entropy: the logits
-// (logits_gemm_kernel), grad_W (grad_w_gemm_kernel), both further below, and grad_hidden
-// (grad_h_gemm_kernel, split-K, next).
+// tm_ce_gemm.hip -- gfx950 bf16 MFMA GEMMs of the fused linear + cross-entropy, per chunk of rows
+// (torchure/loss/fused_linear_ce.py:38,52,57: bf16 matmuls, fp32 accumulation, bf16 results):
+//   logits_gemm_kernel   logits = h W^T         (rows x V, K = D)
+//   grad_h_gemm_kernel   grad_h = grad_logits W (rows x D, K = V), split over K, with
+//   grad_h_reduce_kernel summing the fp32 partials of each element over the splits in a fixed
+//                        order (split 0 first) and rounding once to bf16 (RNE), so the result
+//                        does not depend on scheduling
+//   grad_w_gemm_kernel   grad_W = grad_logits^T h (V x D, K = rows)
+// and transpose_bf16_kernel, which makes W^T (D x V) once per call for grad_h.
 //
-// Per chunk of rows the reference computes grad_h = grad_logits @ W
-// (torchure/loss/fused_linear_ce.py:55, a bf16 matmul: fp32 accumulation, bf16 result), with
-// grad_logits (rows x V) and W (V x D). For the reference's default chunk of 1024 rows this is
-// a long-K GEMM (K = V = 151,936 for the Qwen3 head) with a small output (1024 x 1024): 16
-// tiles of 256 x 256, far too few for 256 CUs, and the library GEMM reached about 470 TFLOP/s
-// on it. This kernel splits the K range instead:
-//   grad_h_gemm_kernel   workgroup (tile, split) computes a 256 x 256 output tile over one
-//                        K range with v_mfma_f32_32x32x16_bf16, 8 wave64 (2 x 4, each 128 x 64),
-//                        fp32 accumulators, and writes the fp32 partial tile;
-//   grad_h_reduce_kernel sums the partials of each element over the splits in a fixed order
-//                        (split 0 first) and rounds to bf16 (RNE), so the result does not depend
-//                        on scheduling.
-// Operands: grad_logits row-major (K contiguous) and W^T (D x V, K contiguous, made by
-// transpose_bf16_kernel), both streamed global -> LDS with direct loads (global_load_lds,
-// 16 bytes a lane) into a two-stage ring of 64-deep K slices. gfx950's LDS has 64 four-byte
-// banks and serves a 16-byte-per-lane read 16 lanes at a time, so the 16 lanes reading 16
-// consecutive 128-byte rows must hit 16 different 16-byte bank groups: a row's chunk c sits at
-// slot c ^ ((row >> 1) & 7), which gives rows 2j and 2j+1 (one even, one odd: the two halves
-// of the banks) the slot pattern c ^ j. (The 32-bank pattern c ^ (row & 7) put rows r and r+8
-// on one bank group and doubled the read time; rocprof counted half the LDS cycles as bank
-// conflicts.) All the
-// workgroups of one split run on one XCD (workgroup w runs on XCD w % 8), so that split's
-// K slices of both operands are read from HBM about once and then served from that XCD's L2.
+// All three are 256 x 256 output tiles per workgroup of 4 wave64 (each 128 x 128, 256 fp32
+// accumulators) on v_mfma_f32_32x32x16_bf16. Operands stream global -> LDS with direct loads
+// (global_load_lds, 16 bytes a lane) into two 64 KB stages of 64-deep K slices. gfx950's LDS has
+// 64 four-byte banks and serves a 16-byte-per-lane read 16 lanes at a time, so the 16 lanes
+// reading 16 consecutive 128-byte rows must hit 16 different 16-byte bank groups: a row's chunk c
+// sits at slot c ^ ((row >> 1) & 7), which gives rows 2j and 2j+1 (one even, one odd: the two
+// halves of the banks) the slot pattern c ^ j. (The 32-bank pattern c ^ (row & 7) put rows r and
+// r+8 on one bank group and doubled the read time.) Workgroup w runs on XCD w % 8; each XCD takes
+// a contiguous range of tiles (or of split-tile pairs), so the operand panels its 32 CUs share
+// are read from HBM about once and then served from that XCD's L2.
+//
+// For the reference's default chunk of 1024 rows, grad_h is a long-K GEMM (K = V = 151,936 for
+// the Qwen3 head) with a small output (1024 x 1024): 16 tiles for 256 CUs, which the library GEMM
+// ran at about 450 TFLOP/s. Splitting K gives every CU a (split, tile) pair.
 
 #include <hip/hip_runtime.h>
 
@@ -51,108 +48,10 @@ int gemm_fail(int code, const char* fmt, A... args) {
 
 constexpr int kTile = 256;      // output tile edge (rows and columns)
 constexpr int kSliceK = 64;     // K depth of one LDS stage (128 bytes of bf16 per row)
-constexpr int kStages = 2;
-constexpr int kWavesM = 2, kWavesN = 4;
-constexpr int kGemmThreads = 64 * kWavesM * kWavesN;
-constexpr int kStageBytes = 2 * kTile * kSliceK * 2;  // A and B slices, 64 KB
-constexpr int kGemmLds = kStages * kStageBytes;        // 128 KB of the 160 KB per CU
-constexpr int kLoadsPerWave = 2 * kTile / 8 / (kWavesM * kWavesN);  // 1 KB load instructions per stage
-constexpr int kBlocksM = kTile / kWavesM / 32, kBlocksN = kTile / kWavesN / 32;  // 32x32 blocks per wave
 
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt bits 3:0 and
 // 15:14; expcnt and lgkmcnt at their maxima, so they are not waited for).
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
-// Output tile and K range of workgroup w in a launch of tiles x splits workgroups (splits a
-// multiple of 8): w % 8 is the XCD w runs on; split s = w % 8 + 8 * (w / (8 * tiles)).
-__global__ __launch_bounds__(kGemmThreads) void grad_h_gemm_kernel(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ Bt, float* __restrict__ partials,
-    int rows, int dim, int64_t K, int splits, int iters_per_split) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int tiles_n = dim / kTile;
-  const int tiles = (rows / kTile) * tiles_n;
-  const int w = blockIdx.x;
-  const int s = (w % 8) + 8 * (w / (8 * tiles));
-  const int tile = (w / 8) % tiles;
-  const int m0 = (tile / tiles_n) * kTile, n0 = (tile % tiles_n) * kTile;
-  const int total_iters = static_cast<int>(K / kSliceK);
-  const int it0 = s * iters_per_split;
-  const int it1 = min(it0 + iters_per_split, total_iters);
-  const int n_it = it1 > it0 ? it1 - it0 : 0;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave / kWavesN, wn = wave % kWavesN;
-  const int lrow = lane >> 3, lpos = lane & 7;
-
-  // One stage: kTile rows of A then kTile rows of Bt, 64 bf16 each; load instruction q of the
-  // stage fills rows 8q .. 8q+7 (1 KB, lane i -> row 8q + i/8, chunk slot i%8), loading the
-  // row's 16-byte chunk (i%8) ^ ((row >> 1) & 7), so that chunk c ends up in slot
-  // c ^ ((row >> 1) & 7).
-  auto issue = [&](int it, int stage) {
-    const int64_t k0 = static_cast<int64_t>(it) * kSliceK;
-    uint8_t* base = smem + stage * kStageBytes;
-#pragma unroll
-    for (int j = 0; j < kLoadsPerWave; ++j) {
-      const int q = wave * kLoadsPerWave + j;  // 0 .. 63: A rows for q < 32, Bt rows after
-      const int r = (q & 31) * 8 + lrow;
-      const int c = lpos ^ ((r >> 1) & 7);
-      const uint16_t* src = q < 32 ? A + static_cast<int64_t>(m0 + r) * K : Bt + static_cast<int64_t>(n0 + r) * K;
-      __builtin_amdgcn_global_load_lds(
-          (const void __attribute__((address_space(1)))*)(src + k0 + c * 8),
-          (void __attribute__((address_space(3)))*)(base + q * 1024), 16, 0, 0);
-    }
-  };
-
-  f32x16 acc[kBlocksM][kBlocksN];
-#pragma unroll
-  for (int i = 0; i < kBlocksM; ++i)
-#pragma unroll
-    for (int j = 0; j < kBlocksN; ++j) acc[i][j] = f32x16{};
-
-  if (n_it > 0) issue(it0, 0);
-  for (int i = 0; i < n_it; ++i) {
-    // This wave's loads of stage i are the only ones in flight (two stages): wait for them,
-    // then a bare barrier makes every wave's loads of the stage visible and ensures every wave
-    // has consumed its reads of the stage the next issue overwrites (they fed the MFMAs). A
-    // __syncthreads() would add a fence that drains every load in flight.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    __builtin_amdgcn_s_barrier();
-    if (i + 1 < n_it) issue(it0 + i + 1, (i + 1) & 1);
-    const uint8_t* base = smem + (i & 1) * kStageBytes;
-#pragma unroll
-    for (int kk = 0; kk < kSliceK / 16; ++kk) {
-      const int kc = kk * 2 + (lane >> 5);  // this lane's 16-byte chunk of the 128-byte row
-      bf16x8 a[kBlocksM], b[kBlocksN];
-#pragma unroll
-      for (int mi = 0; mi < kBlocksM; ++mi) {
-        const int r = wm * (kTile / kWavesM) + mi * 32 + (lane & 31);
-        a[mi] = *(const bf16x8*)(base + r * 128 + ((kc ^ ((r >> 1) & 7)) * 16));
-      }
-#pragma unroll
-      for (int ni = 0; ni < kBlocksN; ++ni) {
-        const int r = wn * (kTile / kWavesN) + ni * 32 + (lane & 31);
-        b[ni] = *(const bf16x8*)(base + kTile * 128 + r * 128 + ((kc ^ ((r >> 1) & 7)) * 16));
-      }
-#pragma unroll
-      for (int mi = 0; mi < kBlocksM; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < kBlocksN; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], b[ni], acc[mi][ni], 0, 0, 0);
-    }
-  }
-  // D layout of v_mfma_f32_32x32x16_bf16: register r of lane l holds
-  // D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
-  float* P = partials + static_cast<int64_t>(s) * rows * dim;
-#pragma unroll
-  for (int mi = 0; mi < kBlocksM; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < kBlocksN; ++ni)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (kTile / kWavesM) + mi * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
-        const int col = n0 + wn * (kTile / kWavesN) + ni * 32 + (lane & 31);
-        P[static_cast<int64_t>(row) * dim + col] = acc[mi][ni][r];
-      }
-}
 
 __device__ __forceinline__ uint32_t rne_bf16(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -261,22 +160,16 @@ struct LgFlags {
   static constexpr bool kNextV = kN, kNext2V = kN2;
 };
 
-__global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                                                          uint16_t* __restrict__ C, int M, int N, int K, int tiles_m,
-                                                          int tiles_n, int gm, int gn) {
-  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  const int T = tiles_m * tiles_n;
-  const int t8 = (T + 7) / 8;
-  const int p = (blockIdx.x % 8) * t8 + blockIdx.x / 8;  // XCD blockIdx % 8 takes positions [x t8, (x+1) t8)
-  if (p >= T) return;
-  int tm, tn;
-  lg_tile_of(p, tiles_m, tiles_n, gm, gn, tm, tn);
-  const int m0 = tm * kLgTile, n0 = tn * kLgTile;
+// Main loop of the NT GEMMs (logits_gemm_kernel, grad_h_gemm_kernel): acc[n block][m block] of a
+// 256 x 256 tile, rows m0.. of A and n0.. of B (`ld` elements apart, rows past M or N clamped to
+// the last), over n_it 64-deep K slices from element k0. 4 waves, wave (wm, wn) = 128 x 128.
+__device__ __forceinline__ void nt_mainloop(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                            int64_t ld, int m0, int n0, int M, int N, int64_t k0, int n_it,
+                                            uint8_t* smem, f32x16 (&acc)[4][4]) {
   const int lane = threadIdx.x & 63;
   // wave-uniform in a scalar register, so each load's LDS destination (M0) is scalar arithmetic
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int n_it = K / kSliceK;
 
   // Load j of this wave fills LDS rows 8 q .. 8 q + 7 of [A tile; B tile], q = 16 wave + j; the
   // lane loads 16-byte chunk (lane % 8) ^ ((row >> 1) & 7) of row 8 q + lane / 8 into slot lane % 8.
@@ -286,8 +179,8 @@ __global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __rest
     const int q = wave * 16 + j;
     const int r = (q % 32) * 8 + lane / 8;
     const int c = (lane % 8) ^ ((r >> 1) & 7);
-    src[j] = (q < 32 ? A + static_cast<int64_t>(min(m0 + r, M - 1)) * K
-                     : B + static_cast<int64_t>(min(n0 + r, N - 1)) * K) + c * 8;
+    src[j] = (q < 32 ? A + static_cast<int64_t>(min(m0 + r, M - 1)) * ld
+                     : B + static_cast<int64_t>(min(n0 + r, N - 1)) * ld) + k0 + c * 8;
   }
   auto load = [&](int it, int stage, int j) {
     __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[j] + it * kSliceK),
@@ -303,17 +196,11 @@ __global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __rest
   for (int kk = 0; kk < 4; ++kk) vk[kk] = lds0 + (((2 * kk) ^ tx) * 16);
   const uint32_t offA = wm * 128 * 128, offB = kLgTile * 128 + wn * 128 * 128;
 
-  f32x16 acc[4][4];  // [n block][m block]
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-
 #define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
 #define TM_WAIT8(f)                                                                                       \
   asm volatile("s_waitcnt lgkmcnt(0)"                                                                   \
                : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]))
-  // fragment g: g < 4 -> weight (n) block g, g >= 4 -> hidden (m) block g - 4
+  // fragment g: g < 4 -> B (n) block g, g >= 4 -> A (m) block g - 4
   bf16x8 f0[8], f1[8];
 #pragma unroll
   for (int j = 0; j < 16; ++j) load(0, 0, j);
@@ -374,6 +261,29 @@ __global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __rest
   if (i < n_it) stage(i, LgFlags<false, false>{});
 #undef TM_RD
 #undef TM_WAIT8
+}
+
+__global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                                          uint16_t* __restrict__ C, int M, int N, int K, int tiles_m,
+                                                          int tiles_n, int gm, int gn) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int T = tiles_m * tiles_n;
+  const int t8 = (T + 7) / 8;
+  const int p = (blockIdx.x % 8) * t8 + blockIdx.x / 8;  // XCD blockIdx % 8 takes positions [x t8, (x+1) t8)
+  if (p >= T) return;
+  int tm, tn;
+  lg_tile_of(p, tiles_m, tiles_n, gm, gn, tm, tn);
+  const int m0 = tm * kLgTile, n0 = tn * kLgTile;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  f32x16 acc[4][4];  // [n block][m block]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  nt_mainloop(A, B, K, m0, n0, M, N, 0, K / kSliceK, smem, acc);
 
   // D[n][m] of a 32 x 32 block: register r of lane l holds n = 8 (r / 4) + 4 (l / 32) + r % 4,
   // m = l % 32. Each wave stages its 128 x 128 bf16 tile in LDS, then writes whole rows.
@@ -409,6 +319,58 @@ __global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __rest
       for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = static_cast<uint16_t>(w[e / 2] >> (16 * (e & 1)));
     }
   }
+}
+
+// ------------------------------------------------- grad_h = grad_logits @ W, K split over workgroups
+//
+// fused_linear_ce.py:52 `grad_h = grad_logits @ w` per chunk: C (rows x dim) = G (rows x V) times
+// W (V x dim), with W^T (dim x V) as the second operand, so both are K-contiguous as in the
+// logits GEMM and the same main loop runs. K = V is long and the output small (16 tiles for a
+// 1024-row chunk at dim 1024), so workgroup (split, tile) computes one 256 x 256 tile over one
+// range of K slices and writes its fp32 partial tile; grad_h_reduce_kernel adds the partials.
+// Pair p = split x tiles + tile; workgroup w runs on XCD w % 8, which takes pairs
+// [x p8, (x+1) p8): the workgroups of an XCD share a split's K range of both operands in its L2.
+// The partial tile is written straight from the accumulators, 16 bytes a lane (4 consecutive
+// columns of one row); a split with no K slices writes zeros.
+__global__ __launch_bounds__(256) void grad_h_gemm_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ Wt,
+                                                          float* __restrict__ partials, int rows, int dim, int64_t K,
+                                                          int tiles, int splits, int iters_per_split) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int pairs = tiles * splits;
+  const int p8 = (pairs + 7) / 8;
+  const int p = (blockIdx.x % 8) * p8 + blockIdx.x / 8;
+  if (p >= pairs) return;
+  const int s = p / tiles, tile = p - s * tiles;
+  const int tiles_n = dim / kLgTile;
+  const int m0 = (tile / tiles_n) * kLgTile, n0 = (tile % tiles_n) * kLgTile;
+  const int total = static_cast<int>(K / kSliceK);
+  const int it0 = s * iters_per_split;
+  const int n_it = max(0, min(iters_per_split, total - it0));
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  f32x16 acc[4][4];  // [n block][m block]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  if (n_it > 0) nt_mainloop(G, Wt, K, m0, n0, rows, dim, static_cast<int64_t>(it0) * kSliceK, n_it, smem, acc);
+
+  // Register r of lane l of block (ii, jj) holds column 8 (r / 4) + 4 (l / 32) + r % 4 of row
+  // l % 32: registers 4 q .. 4 q + 3 are 4 consecutive columns.
+  float* P = partials + static_cast<int64_t>(s) * rows * dim;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = m0 + wm * 128 + jj * 32 + (lane & 31);
+        const int n = n0 + wn * 128 + ii * 32 + 8 * q + 4 * (lane >> 5);
+        const f32x4 v = {acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1], acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]};
+        *(f32x4*)(P + static_cast<int64_t>(m) * dim + n) = v;
+      }
 }
 
 // ------------------------------------------------------- grad_W = grad_logits^T @ hidden
@@ -584,23 +546,22 @@ void logits_groups(int64_t tiles_m, int& gm, int& gn) {
   gn = 32 / gm;
 }
 
-// Splits of the K range: a multiple of 8 (one group of splits per XCD), chosen by a cost model
-// of the launch. One 128 KB-LDS workgroup fits a CU, so tiles x S workgroups run in
-// ceil(tiles x S / 256) rounds; a workgroup takes about 2 us per 64-deep K slice (256 x 256 x 64
-// MFMA work at the kernel's ~1 PFLOP/s over 256 CUs) plus about 8 us to store its 256 KB fp32
-// partial tile, and the reduction reads S x rows x dim fp32 partials at about 5 TB/s. The
-// model picks S = 16 for the 1024-row Qwen3-0.6B chunk (256 workgroups, one round) and S = 32
-// for a 1024-row chunk of a 2560-wide head (40 tiles: 1280 workgroups, five full rounds).
+// Splits of the K range, chosen by a cost model of the launch. One workgroup (136 KB of LDS) fits
+// a CU, so tiles x S workgroups run in ceil(tiles x S / 256) rounds; a workgroup takes about
+// 1.7 us per 64-deep K slice (256 x 256 x 64 MFMA work at the main loop's pace) plus about 8 us
+// to store its 256 KB partial tile, and the reduction reads S x rows x dim fp32 partials at about
+// 5 TB/s. For the Qwen3-0.6B head (dim 1024) the model picks S = 16 for a 1024-row chunk
+// (16 tiles, 256 workgroups), 4 for 4096 rows and 2 for 8192 rows (128 tiles).
 int64_t splits_for(int64_t rows, int64_t vocab, int64_t dim) {
   const int64_t tiles = (rows / kTile) * (dim / kTile);
   const int64_t iters = vocab / kSliceK;
-  int64_t best = 8;
+  int64_t best = 1;
   double best_us = 0.0;
-  for (int64_t s = 8; s <= 256; s += 8) {
+  for (int64_t s = 1; s <= 256; ++s) {
     const int64_t rounds = (tiles * s + 255) / 256;
-    const double us = static_cast<double>(rounds) * (2.0 * static_cast<double>((iters + s - 1) / s) + 8.0) +
+    const double us = static_cast<double>(rounds) * (1.7 * static_cast<double>((iters + s - 1) / s) + 8.0) +
                       static_cast<double>(s) * static_cast<double>(rows * dim) * 4.0 / 5e6;
-    if (s == 8 || us < best_us) {
+    if (s == 1 || us < best_us) {
       best = s;
       best_us = us;
     }
@@ -610,7 +571,7 @@ int64_t splits_for(int64_t rows, int64_t vocab, int64_t dim) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The GEMM kernels' dynamic LDS (128 KB, 136 KB, 136 KB) exceeds the 64 KB default: the attribute is set
+// The GEMM kernels' dynamic LDS (136 KB each) exceeds the 64 KB default: the attribute is set
 // once per device and kernel, with that device current, before the first launch there.
 constexpr int kMaxDevices = 64;
 std::mutex g_lds_mu;
@@ -628,7 +589,7 @@ hipError_t allow_lds(hipStream_t stream, int which) {
   if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
   if (e == hipSuccess)
     e = which == 0   ? hipFuncSetAttribute(reinterpret_cast<const void*>(grad_h_gemm_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds)
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLgLds)
         : which == 1 ? hipFuncSetAttribute(reinterpret_cast<const void*>(logits_gemm_kernel),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLgLds)
                      : hipFuncSetAttribute(reinterpret_cast<const void*>(grad_w_gemm_kernel),
@@ -675,9 +636,9 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
   const int64_t total_iters = vocab / kSliceK;
   const int64_t per = (total_iters + splits - 1) / splits;
   float* partials = static_cast<float*>(d_ws);
-  hipLaunchKernelGGL(grad_h_gemm_kernel, dim3(static_cast<uint32_t>(tiles * splits)), dim3(kGemmThreads),
-                     kGemmLds, s, d_grad_logits, d_wt, partials, static_cast<int>(rows), static_cast<int>(dim),
-                     vocab, static_cast<int>(splits), static_cast<int>(per));
+  hipLaunchKernelGGL(grad_h_gemm_kernel, dim3(static_cast<uint32_t>((tiles * splits + 7) / 8 * 8)), dim3(256),
+                     kLgLds, s, d_grad_logits, d_wt, partials, static_cast<int>(rows), static_cast<int>(dim),
+                     vocab, static_cast<int>(tiles), static_cast<int>(splits), static_cast<int>(per));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "grad_h_gemm_kernel: launch failed: %s", hipGetErrorString(e));
   const int64_t n = rows * dim;

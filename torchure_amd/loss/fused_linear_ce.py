@@ -12,9 +12,9 @@ Per chunk of rows:
   tm_ce_rows_bf16                   one fused kernel: logsumexp, per-row loss and
                                     grad_logits = bf16(softmax - onehot), in place
   grad_h = grad_logits @ W          bf16 GEMM: tm_ce_grad_h_bf16, a split-K MFMA GEMM with a
-                                    fixed-order reduction, on chunks with at most 64 output tiles
-                                    of 256 x 256 (rows and D multiples of 256, V of 64: up to 4096
-                                    rows for D = 1024); hipBLASLt on other shapes
+                                    fixed-order reduction, on chunks with at most
+                                    SPLITK_GRAD_H_MAX_TILES output tiles of 256 x 256 (rows and D
+                                    multiples of 256, V of 64); hipBLASLt on other shapes
   grad_W += grad_logits^T @ h       bf16 GEMM: tm_ce_grad_w_bf16, this build's MFMA GEMM, for rows a
                                     multiple of 64 (torch.matmul on other shapes), then
                                     tm_ce_grad_w_fold into fp32
