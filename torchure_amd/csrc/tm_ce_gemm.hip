@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(uint16_t* __restric
 // with 256 fp32 accumulators (the AGPRs) on v_mfma_f32_32x32x16_bf16. Operands stream
 // global -> LDS (global_load_lds, 16 bytes a lane, 1 KB = 8 rows of a 64-deep K slice per
 // instruction) into two 64 KB stages whose 128-byte rows hold their 16-byte chunks at slot
-// c ^ ((row >> 1) & 7), as in grad_h_gemm_kernel. Schedule per 64-deep stage (4 K16 steps):
+// c ^ ((row >> 1) & 7). Schedule per 64-deep stage (4 K16 steps), in nt_mainloop below:
 //   - the next step's 8 fragments (16-byte LDS reads, inline asm) are issued one per two MFMAs
 //     of the current step, so the reads run under the MFMAs; sched_barrier pins that order and
 //     an `s_waitcnt lgkmcnt(0)` that names the fragments as operands keeps every MFMA behind
