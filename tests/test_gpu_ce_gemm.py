@@ -227,6 +227,10 @@ def _logits(h, w, pad=64, sentinel=0x7BCD):
     (255, 4095, 128),        # rows and vocab one short of tile multiples
     (257, 4097, 128),        # one past: mostly empty edge tiles
     (1000, 1001, 192),
+    (300, 1000, 256),        # persistent kernel from here: 4 K slices (its minimum), ragged edges
+    (64, 200, 256),          # one tile: one workgroup works, the rest exit at once
+    (2000, 20008, 384),      # 6 K slices; edge tiles in both directions
+    (8200, 4104, 512),       # several tiles per workgroup, a 9-row last tile row
     (1024, 151936, 1024),    # the Qwen3-0.6B head at the reference's 1024-row chunk
     (4096, 151936, 1024),
     (1500, 32768, 2560),     # Qwen3-4B width, ragged rows

@@ -1,6 +1,7 @@
 // tm_ce_gemm.hip -- gfx950 bf16 MFMA GEMMs of the fused linear + cross-entropy, per chunk of rows
 // (torchure/loss/fused_linear_ce.py:38,52,57: bf16 matmuls, fp32 accumulation, bf16 results):
-//   logits_gemm_kernel   logits = h W^T         (rows x V, K = D)
+//   logits_ring_kernel   logits = h W^T         (rows x V, K = D), persistent, for dim a multiple
+//                        of 128 (>= 256) and vocab a multiple of 8; logits_gemm_kernel otherwise
 //   grad_h_gemm_kernel   grad_h = grad_logits W (rows x D, K = V), split over K, with
 //   grad_h_reduce_kernel summing the fp32 partials of each element over the splits in a fixed
 //                        order (split 0 first) and rounding once to bf16 (RNE), so the result
@@ -321,6 +322,275 @@ __global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __rest
   }
 }
 
+// ------------------------------------------------ logits, persistent: one workgroup per CU
+//
+// The same product, tiles, fragments and summation order as logits_gemm_kernel (bit-identical
+// results), for the shapes the Qwen heads have (dim a multiple of 128 and at least 256, vocab a
+// multiple of 8, operands under 4 GiB). With K = dim short (16 slices at dim 1024), a tile's
+// fill (its first two stages' loads) and its epilogue (256 accumulators per lane converted to
+// bf16 and written) were a large share of a tile's time; here both overlap the neighbouring
+// tiles' MFMAs:
+//   - workgroup c of XCD x (blockIdx = 8 c + x) runs tile positions x t8 + c, + W, + 2W, ...
+//     (W workgroups per XCD), so the 32 tiles an XCD runs at a time are the same groups of
+//     tiles as in logits_gemm_kernel;
+//   - the operand stages form one ring across tiles: the next tile's stages 0 and 1 are loaded
+//     during the current tile's last two stages (the tile after the last is the last again, a
+//     harmless reload drained before exit);
+//   - the finished tile's accumulators leave during the next tile's first K16 step: block
+//     (ii, jj) is converted to bf16 (RNE) just before that step's MFMA on it, which restarts
+//     its accumulation from zero; the 4 blocks of a quarter (32 rows of the wave's 128) go to
+//     this wave's 8 KB of LDS past the two stages (chunk c of row r at slot c ^ (r & 15)), and
+//     are written back as whole 256-byte rows, 16 bytes a lane; the last tile's output goes
+//     the same way after the loop.
+// LDS: two 64 KB stages + 4 x 8 KB = 160 KB, the whole of a CU's. Operand addresses are 32-bit
+// byte offsets from the operand's base (scalar), one per load.
+
+constexpr int kRgLds = 2 * kLgStage + 4 * 8192;  // 163,840 B
+
+template <bool kN2, bool kPre, bool kFirst, bool kEpi>
+struct RgFlags {
+  static constexpr bool kNext2V = kN2, kPreV = kPre, kFirstV = kFirst, kEpiV = kEpi;
+};
+
+template <bool kV>
+struct RgBool {
+  static constexpr bool value = kV;
+};
+
+__global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                                          uint16_t* __restrict__ C, int M, int N, int K, int tiles_m,
+                                                          int tiles_n, int gm, int gn, int wpx) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int T = tiles_m * tiles_n;
+  const int t8 = (T + 7) / 8;
+  const int x = blockIdx.x % 8;
+  const int pend = min((x + 1) * t8, T);
+  int p = x * t8 + static_cast<int>(blockIdx.x / 8);
+  if (p >= pend) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n_it = K / kSliceK;  // even, >= 4
+
+  // Waves 0, 1 load the A rows of the tile, waves 2, 3 the B rows; load j of a wave fills rows
+  // 8 j + lane / 8 of its 128-row half, the lane's chunk (lane % 8) ^ ((row >> 1) & 7), which is
+  // (lane % 8) ^ (lane / 16) ^ (4 (j % 2)). The empty asm keeps the per-lane parts from being
+  // precomputed per load outside the tile loop (16 more live registers).
+  const char* opnd = reinterpret_cast<const char*>(wave < 2 ? A : B);
+  const int lim = (wave < 2 ? M : N) - 1;
+  uint32_t soff[16];
+  int lrow = lane / 8;
+  uint32_t lc16 = static_cast<uint32_t>(((lane % 8) ^ (lane / 16)) * 16);
+  auto set_src = [&](int m0, int n0) {
+    asm volatile("" : "+v"(lrow), "+v"(lc16));
+    const int r0 = (wave < 2 ? m0 : n0) + (wave % 2) * 128;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      soff[j] = static_cast<uint32_t>(min(r0 + 8 * j + lrow, lim)) * static_cast<uint32_t>(2 * K) +
+                (lc16 ^ ((j & 1) * 64));
+  };
+  auto load = [&](int it, int stage, int j) {
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(opnd + (soff[j] + it * 128u)),
+                                     (void __attribute__((address_space(3)))*)(smem + stage * kLgStage + (wave * 16 + j) * 1024),
+                                     16, 0, 0);
+  };
+  // fragment reads as in nt_mainloop
+  const int tx = (lane >> 5) ^ ((lane >> 1) & 7);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + (lane & 31) * 128;
+  uint32_t vk[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) vk[kk] = lds0 + (((2 * kk) ^ tx) * 16);
+  const uint32_t offA = wm * 128 * 128, offB = kLgTile * 128 + wn * 128 * 128;
+
+  // Output staging, this wave's 8 KB: row r (of a quarter's 32) at 256 r, chunk c at slot
+  // c ^ (r & 15). A lane writes row lane % 32, half lane / 32 of chunk c at wa ^ (c << 4); it
+  // reads back chunk lane % 16 of row 4 it + lane / 16 at ra[it % 4] + 4096 (it / 4).
+  const uint32_t ebo = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + 2 * kLgStage + wave * 8192;
+  uint32_t wa = ebo + (lane & 31) * 256 + (lane >> 5) * 8 + ((lane & 15) << 4);
+  uint32_t ra[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = k * 4 + (lane >> 4);
+    ra[k] = ebo + r * 256 + (((lane & 15) ^ r) << 4);
+  }
+  uint32_t sl = static_cast<uint32_t>(((lane >> 4) * N + (lane & 15) * 8) * 2);  // byte offset of the lane's store
+
+#define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
+#define TM_WAIT8(f)                                                                                       \
+  asm volatile("s_waitcnt lgkmcnt(0)"                                                                   \
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]))
+  bf16x8 f0[8], f1[8];
+  f32x16 acc[4][4];  // [n block][m block]
+  int pm0 = 0, pn0 = 0;  // origin of the tile whose output is being written
+
+  // Block (ii, jj) of the finished tile to bf16 in the staging; with `mfma`, the next tile's first
+  // MFMA on the block follows the reads. The empty asms fix that order: the block is read after
+  // the previous block's LDS writes, and its MFMA after the conversion (otherwise all 256
+  // accumulators are copied out at once and the registers spill).
+  auto epi_block = [&](int ii, int jj, bool mfma, bf16x8* cur) {
+    asm volatile("" : "+a"(acc[ii][jj]));
+    u32x2 o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o[q].x = pack_bf16x2(acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1]);
+      o[q].y = pack_bf16x2(acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]);
+    }
+    if (mfma) {
+      asm volatile("" : "+v"(cur[ii]) : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]));
+      acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], f32x16{}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a = wa ^ ((ii * 4 + q) << 4);
+      asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(o[q]) : "memory");
+    }
+  };
+  // Quarter jj (32 rows) of the finished tile at (pm0, pn0): staging -> global. N % 8 == 0, so a
+  // lane's 8 columns are all in range or all out.
+  auto epi_store = [&](int jj) {
+    u32x4 v[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it)
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v[it]) : "v"(ra[it & 3]), "i"((it >> 2) * 16 * 256));
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+    const int rows_left = M - (pm0 + wm * 128 + jj * 32), cols_left = N - (pn0 + wn * 128);
+    char* qb = reinterpret_cast<char*>(C) + (static_cast<int64_t>(pm0 + wm * 128 + jj * 32) * N + pn0 + wn * 128) * 2;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      if (it * 4 + (lane >> 4) < rows_left && (lane & 15) * 8 < cols_left)
+        __builtin_nontemporal_store(v[it], reinterpret_cast<u32x4*>(qb + (sl + static_cast<uint32_t>(it * 8 * N))));
+    }
+  };
+
+  int tm, tn;
+  lg_tile_of(p, tiles_m, tiles_n, gm, gn, tm, tn);
+  int m0 = tm * kLgTile, n0 = tn * kLgTile;
+  set_src(m0, n0);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) load(0, 0, j);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) load(1, 1, j);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int g = 0; g < 8; ++g) TM_RD(f0[g], vk[0] + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+  TM_WAIT8(f0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  int pn = p, m0n = m0, n0n = n0;
+  bool has_next = false;
+  // One tile: stage 0 (with the previous tile's output when kEpiFirst), then stages 1 .. n_it - 1,
+  // whose last two load the next tile's first two stages. The first tile is peeled so that every
+  // loop iteration enters with its accumulators in the same registers.
+  auto tile = [&](auto epi_first) {
+    constexpr bool kEpiFirst = decltype(epi_first)::value;
+    asm volatile("" : "+v"(wa), "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]), "+v"(sl));
+    pn = p + wpx;
+    has_next = pn < pend;
+    int tmn, tnn;
+    lg_tile_of(has_next ? pn : p, tiles_m, tiles_n, gm, gn, tmn, tnn);
+    m0n = tmn * kLgTile;
+    n0n = tnn * kLgTile;
+
+    auto stage = [&](int i, auto step) {
+      constexpr bool kNext2 = decltype(step)::kNext2V, kPre = decltype(step)::kPreV;
+      constexpr bool kFirst = decltype(step)::kFirstV, kEpi = decltype(step)::kEpiV;
+      const int s = i & 1;
+      const uint32_t soff_s = s * kLgStage, noff = (s ^ 1) * kLgStage;
+      if (kPre) {
+        set_src(m0n, n0n);  // every load of this tile has been issued
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        bf16x8* cur = (kk & 1) ? f1 : f0;
+        bf16x8* nxt = (kk & 1) ? f0 : f1;
+        if (kEpi && kk == 0) {  // first K16 step, with the previous tile's output
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+              if ((ii & 1) == 0) {
+                const int g = jj * 2 + ii / 2;
+                TM_RD(nxt[g], vk[1] + soff_s + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+              }
+              epi_block(ii, jj, true, cur);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            epi_store(jj);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          TM_WAIT8(nxt);
+          __builtin_amdgcn_sched_barrier(0);
+          continue;
+        }
+        if (kk == 3) {
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wave's loads of the next stage are in LDS
+          __builtin_amdgcn_s_barrier();               // every wave's; and this stage's reads are done
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          if (kk < 3) {
+            TM_RD(nxt[g], vk[kk + 1] + soff_s + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+          } else {
+            TM_RD(nxt[g], vk[0] + noff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+          }
+          if (kk == 3 && kNext2) {
+            const int it2 = i + 2 >= n_it ? i + 2 - n_it : i + 2;  // past the end: the next tile's 0, 1
+            load(it2, s, 2 * g);
+            load(it2, s, 2 * g + 1);
+          }
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int idx = 2 * g + h, ii = idx / 4, jj = idx % 4;
+            if (kFirst && kk == 0)
+              acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], f32x16{}, 0, 0, 0);
+            else
+              acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], acc[ii][jj], 0, 0, 0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        TM_WAIT8(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    stage(0, RgFlags<true, false, true, kEpiFirst>{});
+    for (int i = 1; i < n_it - 2; ++i) stage(i, RgFlags<true, false, false, false>{});
+    stage(n_it - 2, RgFlags<true, true, false, false>{});
+    stage(n_it - 1, RgFlags<true, false, false, false>{});
+    pm0 = m0;
+    pn0 = n0;
+  };
+  tile(RgBool<false>{});
+  while (has_next) {
+    p = pn;
+    m0 = m0n;
+    n0 = n0n;
+    __builtin_amdgcn_sched_barrier(0);
+    tile(RgBool<true>{});
+  }
+  // the last tile's output; then the redundant reload of that tile's first stages completes
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) epi_block(ii, jj, false, f0);
+    epi_store(jj);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+#undef TM_RD
+#undef TM_WAIT8
+}
+
+// The ring kernel's preconditions: K slices in an even number >= 4, whole 8-column store groups,
+// 32-bit operand offsets and store offsets.
+bool logits_ring_fits(int64_t rows, int64_t vocab, int64_t dim) {
+  return dim % 128 == 0 && dim >= 256 && vocab % 8 == 0 && rows * dim * 2 < (int64_t(1) << 32) &&
+         vocab * dim * 2 < (int64_t(1) << 32) && 32 * vocab * 2 < (int64_t(1) << 32);
+}
+
 // ------------------------------------------------- grad_h = grad_logits @ W, K split over workgroups
 //
 // fused_linear_ce.py:52 `grad_h = grad_logits @ w` per chunk: C (rows x dim) = G (rows x V) times
@@ -571,34 +841,42 @@ int64_t splits_for(int64_t rows, int64_t vocab, int64_t dim) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The GEMM kernels' dynamic LDS (136 KB each) exceeds the 64 KB default: the attribute is set
-// once per device and kernel, with that device current, before the first launch there.
+// The GEMM kernels' dynamic LDS (136 KB, 160 KB for the ring kernel) exceeds the 64 KB default:
+// the attribute is set once per device and kernel, with that device current, before the first
+// launch there. The device's CU count (for the ring kernel's workgroups per XCD) is read then.
 constexpr int kMaxDevices = 64;
 std::mutex g_lds_mu;
-bool g_lds_set[3][kMaxDevices] = {};
+bool g_lds_set[4][kMaxDevices] = {};
+int g_cus[kMaxDevices] = {};
 
-hipError_t allow_lds(hipStream_t stream, int which) {
+// which: 0 grad_h_gemm_kernel, 1 logits_gemm_kernel, 2 grad_w_gemm_kernel, 3 logits_ring_kernel.
+// `cus`, when given, receives the device's CU count.
+hipError_t allow_lds(hipStream_t stream, int which, int* cus = nullptr) {
   int dev = -1;
   hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_lds_mu);
-  if (g_lds_set[which][dev]) return hipSuccess;
+  if (g_lds_set[which][dev]) {
+    if (cus) *cus = g_cus[dev];
+    return hipSuccess;
+  }
   int cur = -1;
   e = hipGetDevice(&cur);
   if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+  const void* fn[4] = {reinterpret_cast<const void*>(grad_h_gemm_kernel), reinterpret_cast<const void*>(logits_gemm_kernel),
+                       reinterpret_cast<const void*>(grad_w_gemm_kernel), reinterpret_cast<const void*>(logits_ring_kernel)};
   if (e == hipSuccess)
-    e = which == 0   ? hipFuncSetAttribute(reinterpret_cast<const void*>(grad_h_gemm_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLgLds)
-        : which == 1 ? hipFuncSetAttribute(reinterpret_cast<const void*>(logits_gemm_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLgLds)
-                     : hipFuncSetAttribute(reinterpret_cast<const void*>(grad_w_gemm_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLgLds);
+    e = hipFuncSetAttribute(fn[which], hipFuncAttributeMaxDynamicSharedMemorySize, which == 3 ? kRgLds : kLgLds);
+  if (e == hipSuccess && g_cus[dev] == 0) e = hipDeviceGetAttribute(&g_cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
   if (cur >= 0 && cur != dev) {
     const hipError_t back = hipSetDevice(cur);
     if (e == hipSuccess) e = back;
   }
-  if (e == hipSuccess) g_lds_set[which][dev] = true;
+  if (e == hipSuccess) {
+    g_lds_set[which][dev] = true;
+    if (cus) *cus = g_cus[dev];
+  }
   return e;
 }
 
@@ -662,11 +940,24 @@ int tm_ce_logits_bf16(uint16_t* d_logits, const uint16_t* d_hidden, const uint16
   if (!aligned16(d_logits) || !aligned16(d_hidden) || !aligned16(d_weight))
     return gemm_fail(TM_EINVAL, "tm_ce_logits_bf16: pointers must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  int gm, gn;
+  logits_groups(tiles_m, gm, gn);
+  if (logits_ring_fits(rows, vocab, dim)) {
+    int cus = 0;
+    const hipError_t lds = allow_lds(s, 3, &cus);
+    if (lds != hipSuccess)
+      return gemm_fail(TM_ELAUNCH, "tm_ce_logits_bf16: LDS attribute: %s", hipGetErrorString(lds));
+    const int wpx = cus >= 16 ? cus / 8 : 1;  // one workgroup per CU of each XCD
+    hipLaunchKernelGGL(logits_ring_kernel, dim3(static_cast<uint32_t>(8 * wpx)), dim3(256), kRgLds, s, d_hidden,
+                       d_weight, d_logits, static_cast<int>(rows), static_cast<int>(vocab), static_cast<int>(dim),
+                       static_cast<int>(tiles_m), static_cast<int>(tiles_n), gm, gn, wpx);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "logits_ring_kernel: launch failed: %s", hipGetErrorString(e));
+    return TM_OK;
+  }
   const hipError_t lds = allow_lds(s, 1);
   if (lds != hipSuccess)
     return gemm_fail(TM_ELAUNCH, "tm_ce_logits_bf16: LDS attribute: %s", hipGetErrorString(lds));
-  int gm, gn;
-  logits_groups(tiles_m, gm, gn);
   const int64_t grid = (tiles_m * tiles_n + 7) / 8 * 8;
   hipLaunchKernelGGL(logits_gemm_kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), kLgLds, s, d_hidden, d_weight,
                      d_logits, static_cast<int>(rows), static_cast<int>(vocab), static_cast<int>(dim),
