@@ -314,6 +314,9 @@ def _grad_w(gl, h, pad=64, sentinel=0x7BCD):
     (64, 8, 8, False),            # one K stage, one tile mostly past vocab and dim
     (128, 4104, 264, False),      # vocab and dim one group of 8 past tile multiples
     (192, 1000, 136, True),
+    (256, 1000, 256, True),       # persistent kernel from here: 4 K stages (its minimum), ragged vocab
+    (384, 4104, 520, False),      # 6 K stages; edge tiles in both directions
+    (512, 200, 264, True),        # 2 tiles: most workgroups exit at once
     (1024, 151936, 1024, True),   # the Qwen3-0.6B head at the reference's 1024-row chunk
     (4096, 32768, 2560, True),    # a 4096-row chunk at the Qwen3-4B width
 ])

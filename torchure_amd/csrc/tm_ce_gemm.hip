@@ -6,7 +6,8 @@
 //   grad_h_reduce_kernel summing the fp32 partials of each element over the splits in a fixed
 //                        order (split 0 first) and rounding once to bf16 (RNE), so the result
 //                        does not depend on scheduling
-//   grad_w_gemm_kernel   grad_W = grad_logits^T h (V x D, K = rows)
+//   grad_w_ring_kernel   grad_W = grad_logits^T h (V x D, K = rows), persistent, for rows a
+//                        multiple of 128 (>= 256); grad_w_gemm_kernel otherwise
 // and transpose_bf16_kernel, which makes W^T (D x V) once per call for grad_h.
 //
 // All three are 256 x 256 output tiles per workgroup of 4 wave64 (each 128 x 128, 256 fp32
@@ -808,6 +809,249 @@ __global__ __launch_bounds__(256) void grad_w_gemm_kernel(const uint16_t* __rest
   }
 }
 
+// ------------------------------------------------ grad_W, persistent: one workgroup per CU
+//
+// grad_w_gemm_kernel's tiles, loads, transposing fragment reads and summation order (bit-identical
+// results) in logits_ring_kernel's persistent form: workgroup c of XCD x runs the XCD's tile
+// positions c, c + W, ...; the next tile's first two stages load during the current tile's last
+// two; the finished tile's accumulators are converted and staged block by block during the next
+// tile's first K16 step (a quarter of 32 vocab rows at a time through the wave's 8 KB past the
+// stages) and written as whole 256-byte rows of grad_W. For rows (K) a multiple of 128 and at
+// least 256, vocab and dim multiples of 8, operands under 4 GiB; grad_w_gemm_kernel otherwise.
+
+__global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ H,
+                                                          uint16_t* __restrict__ C, int V, int D, int K, int tiles_v,
+                                                          int tiles_d, int gm, int gn, int wpx) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int T = tiles_v * tiles_d;
+  const int t8 = (T + 7) / 8;
+  const int x = blockIdx.x % 8;
+  const int pend = min((x + 1) * t8, T);
+  int p = x * t8 + static_cast<int>(blockIdx.x / 8);
+  if (p >= pend) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;  // vocab half, dim half
+  const int n_it = K / kSliceK;             // even, >= 4
+
+  // Waves 0, 1 load G (rows 0-31 / 32-63 of a stage), waves 2, 3 H. Load j: stage rows
+  // 32 (wave % 2) + 2 j + lane / 32, slot lane % 32 taking chunk (lane % 32) ^ (4 (row & 3)) =
+  // (lane % 32) ^ (4 (lane / 32)) ^ (8 (j % 2)).
+  const char* opnd = reinterpret_cast<const char*>(wave < 2 ? G : H);
+  const int ld = wave < 2 ? V : D;
+  const int lim8 = ld - 8;
+  const uint32_t step = static_cast<uint32_t>(kSliceK) * static_cast<uint32_t>(ld) * 2u;  // bytes per stage
+  uint32_t soff[16];
+  int lkr = lane >> 5;
+  int lc = (lane & 31) ^ (4 * (lane >> 5));
+  auto set_src = [&](int v0, int d0) {
+    asm volatile("" : "+v"(lkr), "+v"(lc));
+    const int col0 = wave < 2 ? v0 : d0;
+    const int r0 = (wave % 2) * 32;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int kr = r0 + 2 * j + lkr;
+      const int c = lc ^ (8 * (j & 1));
+      soff[j] = (static_cast<uint32_t>(kr) * static_cast<uint32_t>(ld) + static_cast<uint32_t>(min(col0 + 8 * c, lim8))) * 2u;
+    }
+  };
+  auto load = [&](int it, int stage, int j) {
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(opnd + (soff[j] + static_cast<uint32_t>(it) * step)),
+                                     (void __attribute__((address_space(3)))*)(smem + stage * kGwStage + (wave * 16 + j) * 1024),
+                                     16, 0, 0);
+  };
+  // transposing fragment reads as in grad_w_gemm_kernel; output staging as in logits_ring_kernel
+  const int s16 = lane & 15, s4 = s16 >> 2;
+  const int lcf = ((lane >> 4) & 1) * 2 + ((s16 & 3) >> 1);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const uint32_t rowb = (8 * (lane >> 5) + s4) * 512 + (s16 & 1) * 8;
+  uint32_t bv[4], bd[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    bv[b] = lds0 + rowb + (16 * wm + 4 * (b ^ s4) + lcf) * 16;
+    bd[b] = lds0 + kGwOp + rowb + (16 * wn + 4 * (b ^ s4) + lcf) * 16;
+  }
+
+  const uint32_t ebo = lds0 + 2 * kGwStage + wave * 8192;
+  uint32_t wa = ebo + (lane & 31) * 256 + (lane >> 5) * 8 + ((lane & 15) << 4);
+  uint32_t ra[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int r = k * 4 + (lane >> 4);
+    ra[k] = ebo + r * 256 + (((lane & 15) ^ r) << 4);
+  }
+  uint32_t sl = static_cast<uint32_t>(((lane >> 4) * D + (lane & 15) * 8) * 2);
+
+#define TM_TR(dst, base, imm) asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
+#define TM_WAIT16(f)                                                                                        \
+  asm volatile("s_waitcnt lgkmcnt(0)"                                                                     \
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), \
+                 "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]),      \
+                 "+v"(f[15]))
+  bf16x4 f0[16], f1[16];
+  auto rd = [&](bf16x4* f, uint32_t so, int kk, int h) {
+    const int g = h >> 1, r = h & 1;
+    TM_TR(f[h], (g < 4 ? bd[g] : bv[g - 4]) + so, kk * 16 * 512 + r * 4 * 512);
+  };
+  f32x16 acc[4][4];  // [dim block][vocab block]
+  int pv0 = 0, pd0 = 0;  // origin of the tile whose output is being written
+
+  // block (ii, jj) -> staging (and the next tile's first MFMA on it), as in logits_ring_kernel
+
+  auto epi_block = [&](int ii, int jj, bool mfma, bf16x4* cur) {
+    asm volatile("" : "+a"(acc[ii][jj]));
+    u32x2 o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o[q].x = pack_bf16x2(acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1]);
+      o[q].y = pack_bf16x2(acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]);
+    }
+    if (mfma) {
+      asm volatile("" : "+v"(cur[2 * ii]) : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]));
+      const bf16x8 a = __builtin_shufflevector(cur[2 * ii], cur[2 * ii + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      const bf16x8 b = __builtin_shufflevector(cur[8 + 2 * jj], cur[9 + 2 * jj], 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, f32x16{}, 0, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a = wa ^ ((ii * 4 + q) << 4);
+      asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(o[q]) : "memory");
+    }
+  };
+  // quarter jj (32 vocab rows) of the finished tile -> grad_W rows, 16 bytes a lane (D % 8 == 0)
+  auto epi_store = [&](int jj) {
+    u32x4 v[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it)
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v[it]) : "v"(ra[it & 3]), "i"((it >> 2) * 16 * 256));
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+    const int rows_left = V - (pv0 + wm * 128 + jj * 32), cols_left = D - (pd0 + wn * 128);
+    char* qb = reinterpret_cast<char*>(C) + (static_cast<int64_t>(pv0 + wm * 128 + jj * 32) * D + pd0 + wn * 128) * 2;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      if (it * 4 + (lane >> 4) < rows_left && (lane & 15) * 8 < cols_left)
+        __builtin_nontemporal_store(v[it], reinterpret_cast<u32x4*>(qb + (sl + static_cast<uint32_t>(it * 8 * D))));
+    }
+  };
+
+  int tv, td;
+  lg_tile_of(p, tiles_v, tiles_d, gm, gn, tv, td);
+  int v0 = tv * kLgTile, d0 = td * kLgTile;
+  set_src(v0, d0);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) load(0, 0, j);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) load(1, 1, j);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int h = 0; h < 16; ++h) rd(f0, 0, 0, h);
+  TM_WAIT16(f0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  int pn = p, v0n = v0, d0n = d0;
+  bool has_next = false;
+  // one tile, as in logits_ring_kernel
+  auto tile = [&](auto epi_first) {
+    constexpr bool kEpiFirst = decltype(epi_first)::value;
+    asm volatile("" : "+v"(wa), "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]), "+v"(sl));
+    pn = p + wpx;
+    has_next = pn < pend;
+    int tvn, tdn;
+    lg_tile_of(has_next ? pn : p, tiles_v, tiles_d, gm, gn, tvn, tdn);
+    v0n = tvn * kLgTile;
+    d0n = tdn * kLgTile;
+
+    auto stage = [&](int i, auto step) {
+      constexpr bool kNext2 = decltype(step)::kNext2V, kPre = decltype(step)::kPreV;
+      constexpr bool kFirst = decltype(step)::kFirstV, kEpi = decltype(step)::kEpiV;
+      const int s = i & 1;
+      const uint32_t so = s * kGwStage, noff = (s ^ 1) * kGwStage;
+      if (kPre) {
+        set_src(v0n, d0n);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        bf16x4* cur = (kk & 1) ? f1 : f0;
+        bf16x4* nxt = (kk & 1) ? f0 : f1;
+        if (kEpi && kk == 0) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+              rd(nxt, so, 1, jj * 4 + ii);
+              epi_block(ii, jj, true, cur);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+            epi_store(jj);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          TM_WAIT16(nxt);
+          __builtin_amdgcn_sched_barrier(0);
+          continue;
+        }
+        if (kk == 3) {
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+          __builtin_amdgcn_s_barrier();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          if (kk < 3) rd(nxt, so, kk + 1, q);
+          else rd(nxt, noff, 0, q);
+          if (kk == 3 && kNext2) {
+            const int it2 = i + 2 >= n_it ? i + 2 - n_it : i + 2;
+            load(it2, s, q);
+          }
+          const int ii = q / 4, jj = q % 4;
+          const bf16x8 a = __builtin_shufflevector(cur[2 * ii], cur[2 * ii + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+          const bf16x8 b = __builtin_shufflevector(cur[8 + 2 * jj], cur[9 + 2 * jj], 0, 1, 2, 3, 4, 5, 6, 7);
+          if (kFirst && kk == 0)
+            acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, f32x16{}, 0, 0, 0);
+          else
+            acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[ii][jj], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        TM_WAIT16(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    stage(0, RgFlags<true, false, true, kEpiFirst>{});
+    for (int i = 1; i < n_it - 2; ++i) stage(i, RgFlags<true, false, false, false>{});
+    stage(n_it - 2, RgFlags<true, true, false, false>{});
+    stage(n_it - 1, RgFlags<true, false, false, false>{});
+    pv0 = v0;
+    pd0 = d0;
+  };
+  tile(RgBool<false>{});
+  while (has_next) {
+    p = pn;
+    v0 = v0n;
+    d0 = d0n;
+    __builtin_amdgcn_sched_barrier(0);
+    tile(RgBool<true>{});
+  }
+  // the last tile's output; then the redundant reload of that tile's first stages completes
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) epi_block(ii, jj, false, f0);
+    epi_store(jj);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+#undef TM_TR
+#undef TM_WAIT16
+}
+
+
+bool grad_w_ring_fits(int64_t rows, int64_t vocab, int64_t dim) {
+  return rows % 128 == 0 && rows >= 256 && vocab % 8 == 0 && dim % 8 == 0 && rows * vocab * 2 < (int64_t(1) << 32) &&
+         rows * dim * 2 < (int64_t(1) << 32) && 32 * dim * 2 < (int64_t(1) << 32);
+}
+
 // Tile groups per XCD round: with few row tiles the whole hidden chunk sits in every XCD's L2,
 // so a round takes one row of 32 weight panels (measured 0.334 ms at 1024 x 151,936 x 1024
 // against 0.365 for 4 x 8); with more, 4 x 8 keeps the panels of a round within the L2.
@@ -841,15 +1085,16 @@ int64_t splits_for(int64_t rows, int64_t vocab, int64_t dim) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The GEMM kernels' dynamic LDS (136 KB, 160 KB for the ring kernel) exceeds the 64 KB default:
+// The GEMM kernels' dynamic LDS (136 KB, 160 KB for the ring kernels) exceeds the 64 KB default:
 // the attribute is set once per device and kernel, with that device current, before the first
-// launch there. The device's CU count (for the ring kernel's workgroups per XCD) is read then.
+// launch there. The device's CU count (for the ring kernels' workgroups per XCD) is read then.
 constexpr int kMaxDevices = 64;
 std::mutex g_lds_mu;
-bool g_lds_set[4][kMaxDevices] = {};
+bool g_lds_set[5][kMaxDevices] = {};
 int g_cus[kMaxDevices] = {};
 
-// which: 0 grad_h_gemm_kernel, 1 logits_gemm_kernel, 2 grad_w_gemm_kernel, 3 logits_ring_kernel.
+// which: 0 grad_h_gemm_kernel, 1 logits_gemm_kernel, 2 grad_w_gemm_kernel, 3 logits_ring_kernel,
+// 4 grad_w_ring_kernel.
 // `cus`, when given, receives the device's CU count.
 hipError_t allow_lds(hipStream_t stream, int which, int* cus = nullptr) {
   int dev = -1;
@@ -864,10 +1109,11 @@ hipError_t allow_lds(hipStream_t stream, int which, int* cus = nullptr) {
   int cur = -1;
   e = hipGetDevice(&cur);
   if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
-  const void* fn[4] = {reinterpret_cast<const void*>(grad_h_gemm_kernel), reinterpret_cast<const void*>(logits_gemm_kernel),
-                       reinterpret_cast<const void*>(grad_w_gemm_kernel), reinterpret_cast<const void*>(logits_ring_kernel)};
+  const void* fn[5] = {reinterpret_cast<const void*>(grad_h_gemm_kernel), reinterpret_cast<const void*>(logits_gemm_kernel),
+                       reinterpret_cast<const void*>(grad_w_gemm_kernel), reinterpret_cast<const void*>(logits_ring_kernel),
+                       reinterpret_cast<const void*>(grad_w_ring_kernel)};
   if (e == hipSuccess)
-    e = hipFuncSetAttribute(fn[which], hipFuncAttributeMaxDynamicSharedMemorySize, which == 3 ? kRgLds : kLgLds);
+    e = hipFuncSetAttribute(fn[which], hipFuncAttributeMaxDynamicSharedMemorySize, which >= 3 ? kRgLds : kLgLds);
   if (e == hipSuccess && g_cus[dev] == 0) e = hipDeviceGetAttribute(&g_cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
   if (cur >= 0 && cur != dev) {
     const hipError_t back = hipSetDevice(cur);
@@ -980,10 +1226,23 @@ int tm_ce_grad_w_bf16(uint16_t* d_grad_w, const uint16_t* d_grad_logits, const u
   if (!aligned16(d_grad_w) || !aligned16(d_grad_logits) || !aligned16(d_hidden))
     return gemm_fail(TM_EINVAL, "tm_ce_grad_w_bf16: pointers must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int gn = static_cast<int>(tiles_d < 4 ? tiles_d : 4), gm = 32 / gn;  // a round of 32: 8 x 4
+  if (grad_w_ring_fits(rows, vocab, dim)) {
+    int cus = 0;
+    const hipError_t lds = allow_lds(s, 4, &cus);
+    if (lds != hipSuccess)
+      return gemm_fail(TM_ELAUNCH, "tm_ce_grad_w_bf16: LDS attribute: %s", hipGetErrorString(lds));
+    const int wpx = cus >= 16 ? cus / 8 : 1;
+    hipLaunchKernelGGL(grad_w_ring_kernel, dim3(static_cast<uint32_t>(8 * wpx)), dim3(256), kRgLds, s, d_grad_logits,
+                       d_hidden, d_grad_w, static_cast<int>(vocab), static_cast<int>(dim), static_cast<int>(rows),
+                       static_cast<int>(tiles_v), static_cast<int>(tiles_d), gm, gn, wpx);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "grad_w_ring_kernel: launch failed: %s", hipGetErrorString(e));
+    return TM_OK;
+  }
   const hipError_t lds = allow_lds(s, 2);
   if (lds != hipSuccess)
     return gemm_fail(TM_ELAUNCH, "tm_ce_grad_w_bf16: LDS attribute: %s", hipGetErrorString(lds));
-  const int gn = static_cast<int>(tiles_d < 4 ? tiles_d : 4), gm = 32 / gn;  // a round of 32: 8 x 4
   const int64_t grid = (tiles_v * tiles_d + 7) / 8 * 8;
   hipLaunchKernelGGL(grad_w_gemm_kernel, dim3(static_cast<uint32_t>(grid)), dim3(256), kLgLds, s, d_grad_logits,
                      d_hidden, d_grad_w, static_cast<int>(vocab), static_cast<int>(dim), static_cast<int>(rows),
