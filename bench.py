@@ -66,6 +66,8 @@ def parse():
                          "calibrating HBM byte counters (for rocprofv3 --pmc); ce: the fused linear "
                          "+ CE legs only; ce-gemm: the fused CE's grad_h GEMM, split-K kernel and "
                          "torch.matmul, at --gemm-shapes")
+    ap.add_argument("--ce-dim", type=int, default=1024,
+                    help="ce mode: hidden size of the head (1024: Qwen3-0.6B, 2560: Qwen3-4B)")
     ap.add_argument("--gemm-shapes", default="1024x1024,4096x1024,8192x1024,1024x2560,4096x2560",
                     help="ce-gemm mode: comma list of ROWSxDIM grad_h shapes (vocabulary 151,936)")
     ap.add_argument("--reps", type=int, default=3)
@@ -562,15 +564,17 @@ def run_torch_gpu_reference(config: str, steps: int, warmup: int, dev):
                 ms_per_step_without_bf16_cast=round(ms_nocast, 4))
 
 
-def run_fused_ce(reps: int, dev, with_reference: bool = True):
+def run_fused_ce(reps: int, dev, with_reference: bool = True, d: int = 1024):
     """Chunked fused linear + CE on the Qwen3-0.6B head: 8192 tokens (2 x 4096),
     hidden 1024, vocab 151936 (tied embedding), bf16 activations, fp32 weight,
-    forward + backward. Roofline: the three GEMMs, 6 * N * D * V flops, bf16 MFMA."""
+    forward + backward (or another hidden size `d`: 2560 is the Qwen3-4B head). Roofline:
+    the three GEMMs, 6 * N * D * V flops, bf16 MFMA."""
     import torch
 
     from torchure_amd.loss import fused_linear_cross_entropy
 
-    n, d, v = 8192, 1024, 151936
+    n, v = 8192, 151936
+    head_name = {1024: "qwen3-0.6b", 2560: "qwen3-4b", 4096: "qwen3-8b", 5120: "qwen3-14b"}.get(d, "D %d" % d)
     g = torch.Generator(device=dev).manual_seed(0)
     hidden = torch.randn(n, d, device=dev, generator=g).to(torch.bfloat16)
     weight = torch.randn(v, d, device=dev, generator=g) * 0.02
@@ -592,7 +596,7 @@ def run_fused_ce(reps: int, dev, with_reference: bool = True):
         w = weight.detach().requires_grad_(True)
         fused_linear_cross_entropy(h, w, labels, -100, chunk).backward()
 
-    out = {"workload": "qwen3-0.6b lm_head: N 8192, D 1024, V 151936, fwd+bwd, chunk_size='auto'",
+    out = {"workload": "%s lm_head: N 8192, D %d, V 151936, fwd+bwd, chunk_size='auto'" % (head_name, d),
            "flops": flops, "ms": round(timed(ours), 4)}
     out["TFLOPs"] = round(flops / (out["ms"] * 1e-3) / 1e12, 1)
     out["frac_of_bf16_mfma_peak"] = round(out["TFLOPs"] / 2500.0, 4)
@@ -888,7 +892,7 @@ def main():
                          [x for x in args.state_layouts.split(",") if x])
         return
     if args.mode == "ce":  # fused linear CE only (for rocprofv3)
-        print(json.dumps(run_fused_ce(args.reps, dev, with_reference=False)), flush=True)
+        print(json.dumps(run_fused_ce(args.reps, dev, with_reference=False, d=args.ce_dim)), flush=True)
         return
     if args.mode == "ce-gemm":
         shapes = [tuple(int(x) for x in sh.split("x")) for sh in args.gemm_shapes.split(",") if sh]

@@ -207,6 +207,39 @@ def test_op_mixes_the_gemm_and_the_library_on_ragged_chunks():
     assert torch.equal(h1.grad.view(torch.int16), want.view(torch.int16))
 
 
+@pytest.mark.parametrize("d,split", [(768, True), (1024, False)])
+def test_op_grad_h_choice_above_64_tiles(d, split):
+    """One 8192-row chunk (V 4096): at a hidden size that is not a power of two (768, 96 output
+    tiles) grad_h takes the split-K GEMM, at a power of two (1024, 128 tiles) torch.matmul; the
+    op's grad_h equals the chosen product times the bf16 scale, bit for bit."""
+    from torchure_amd import _native
+    from torchure_amd.loss import fused_linear_cross_entropy
+    from torchure_amd.loss.fused_linear_ce import splitk_grad_h_fits
+
+    g = torch.Generator(device=DEV).manual_seed(d)
+    n, v = 8192, 4096
+    assert splitk_grad_h_fits(n, d, v) == split
+    hidden = torch.randn(n, d, device=DEV, generator=g).to(torch.bfloat16)
+    weight = torch.randn(v, d, device=DEV, generator=g) * 0.05
+    labels = torch.randint(0, v, (n,), device=DEV, generator=g)
+    labels[::17] = -100
+    h1 = hidden.clone().requires_grad_(True)
+    fused_linear_cross_entropy(h1, weight, labels, -100, None).backward()
+
+    lib, stream = _native.lib(), _native.stream_handle(DEV)
+    w = weight.to(torch.bfloat16)
+    logits, _ = _logits(hidden, w)  # the op's logits GEMM
+    logits = logits.contiguous()
+    row_loss = torch.empty(n, dtype=torch.float32, device=DEV)
+    _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels.data_ptr(), n, v, -100, row_loss.data_ptr(),
+                                      stream), "tm_ce_rows_bf16")
+    want = _grad_h(logits, w) if split else torch.matmul(logits, w)
+    n_valid = (labels != -100).sum().clamp_min(1)
+    want.mul_((torch.tensor(1.0, device=DEV) / n_valid).to(torch.bfloat16))
+    torch.cuda.synchronize()
+    assert torch.equal(h1.grad.view(torch.int16), want.view(torch.int16))
+
+
 def _logits(h, w, pad=64, sentinel=0x7BCD):
     """tm_ce_logits_bf16 into a view with `pad` guard elements on both sides (sentinel bits),
     returning (logits, guard intact)."""

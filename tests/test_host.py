@@ -333,8 +333,9 @@ def test_bench_cpu_baseline_on_a_small_set():
 
 def test_fused_ce_grad_h_gemm_choice():
     """Chunks whose grad_h runs on the split-K MFMA GEMM: shapes it tiles (rows and hidden
-    size multiples of 256, vocabulary of 64) with at most 64 output tiles of 256 x 256;
-    everything else stays on torch.matmul."""
+    size multiples of 256, vocabulary of 64), except more than 64 output tiles of 256 x 256
+    with a power-of-two hidden size, where the library GEMM measured faster; everything else
+    stays on torch.matmul."""
     from torchure_amd.loss.fused_linear_ce import splitk_grad_h_fits
 
     v = 151936
@@ -342,6 +343,10 @@ def test_fused_ce_grad_h_gemm_choice():
     assert splitk_grad_h_fits(4096, 1024, v)  # the trainer's chunk: 64 tiles
     assert not splitk_grad_h_fits(8192, 1024, v)  # 128 tiles
     assert splitk_grad_h_fits(1024, 4096, v) and not splitk_grad_h_fits(2048, 4096, v)
+    assert splitk_grad_h_fits(2048, 2048, v) and not splitk_grad_h_fits(4096, 2048, v)
+    # Qwen3-4B (2560) and 14B/32B (5120) heads: split-K at every chunk size
+    assert splitk_grad_h_fits(4096, 2560, v) and splitk_grad_h_fits(8192, 2560, v)
+    assert splitk_grad_h_fits(8192, 5120, v) and splitk_grad_h_fits(32768, 2560, v)
     assert not splitk_grad_h_fits(1000, 1024, v) and not splitk_grad_h_fits(1024, 1000, v)
     assert not splitk_grad_h_fits(1024, 1024, 151937) and not splitk_grad_h_fits(0, 1024, v)
 

@@ -1052,11 +1052,22 @@ bool grad_w_ring_fits(int64_t rows, int64_t vocab, int64_t dim) {
          rows * dim * 2 < (int64_t(1) << 32) && 32 * dim * 2 < (int64_t(1) << 32);
 }
 
-// Tile groups per XCD round: with few row tiles the whole hidden chunk sits in every XCD's L2,
-// so a round takes one row of 32 weight panels (measured 0.334 ms at 1024 x 151,936 x 1024
-// against 0.365 for 4 x 8); with more, 4 x 8 keeps the panels of a round within the L2.
-void logits_groups(int64_t tiles_m, int& gm, int& gn) {
-  gm = tiles_m <= 4 ? 1 : (tiles_m <= 8 ? 2 : 4);
+// Tile groups per XCD round (gm row tiles x gn weight panels, gm gn = 32), chosen from a sweep of
+// the logits ring kernel on MI355X (V = 151,936; TFLOP/s of the best against the next best):
+//   dim <= 1024: 1 x 32 up to 4 row tiles (1063 against 855 for 4 x 8 at 1024 rows: the hidden
+//                chunk sits in every XCD's L2 and a round takes one row of 32 panels), 2 x 16 up
+//                to 8, 4 x 8 above;
+//   dim <= 2560: 2 x 16 up to 8 row tiles (1048 against 899 for 1 x 32 at 1024 x 2560), 4 x 8
+//                above;
+//   dim <= 4096: 4 x 8 (1118 against 1008 for 1 x 32 at 1024 x 4096);
+//   wider:       8 x 4 from 8 row tiles (1195 against 1125 for 4 x 8 at 8192 x 5120), 4 x 8 below.
+// Wider panels (256 x dim) leave fewer in an XCD's 4 MB L2, so rounds share each panel among more
+// tiles.
+void logits_groups(int64_t tiles_m, int64_t dim, int& gm, int& gn) {
+  if (dim <= 1024) gm = tiles_m <= 4 ? 1 : (tiles_m <= 8 ? 2 : 4);
+  else if (dim <= 2560) gm = tiles_m <= 8 ? 2 : 4;
+  else if (dim <= 4096) gm = 4;
+  else gm = tiles_m >= 8 ? 8 : 4;
   gn = 32 / gm;
 }
 
@@ -1187,7 +1198,7 @@ int tm_ce_logits_bf16(uint16_t* d_logits, const uint16_t* d_hidden, const uint16
     return gemm_fail(TM_EINVAL, "tm_ce_logits_bf16: pointers must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   int gm, gn;
-  logits_groups(tiles_m, gm, gn);
+  logits_groups(tiles_m, dim, gm, gn);
   if (logits_ring_fits(rows, vocab, dim)) {
     int cus = 0;
     const hipError_t lds = allow_lds(s, 3, &cus);

@@ -13,8 +13,9 @@ Per chunk of rows:
                                     grad_logits = bf16(softmax - onehot), in place
   grad_h = grad_logits @ W          bf16 GEMM: tm_ce_grad_h_bf16, a split-K MFMA GEMM with a
                                     fixed-order reduction, on chunks with at most
-                                    SPLITK_GRAD_H_MAX_TILES output tiles of 256 x 256 (rows and D
-                                    multiples of 256, V of 64); hipBLASLt on other shapes
+                                    SPLITK_GRAD_H_MAX_TILES output tiles of 256 x 256, or any
+                                    number when D is not a power of two (rows and D multiples of
+                                    256, V of 64); hipBLASLt on other shapes
   grad_W += grad_logits^T @ h       bf16 GEMM: tm_ce_grad_w_bf16, this build's MFMA GEMM, for rows a
                                     multiple of 64 (torch.matmul on other shapes), then
                                     tm_ce_grad_w_fold into fp32
@@ -233,13 +234,24 @@ SPLITK_GRAD_H_MAX_TILES = 64
 
 def splitk_grad_h_fits(rows: int, dim: int, vocab: int) -> bool:
     """Chunks whose grad_h runs on the split-K MFMA GEMM (tm_ce_grad_h_bf16): the shapes it
-    tiles (rows and dim multiples of 256, vocab of 64) with at most SPLITK_GRAD_H_MAX_TILES
-    output tiles of 256 x 256. With so few tiles and K = vocab, a library GEMM leaves most of the
-    256 CUs idle; the split-K kernel spreads K over them (1024 x 1024 at 151,936: 0.30 ms against
-    0.73; 4096 x 1024: 1.20 against 1.50). With more tiles the library's kernels fill the chip
-    themselves (8192 x 1024: 1.97 ms against this kernel's 2.11)."""
-    return (rows > 0 and dim > 0 and rows % 256 == 0 and dim % 256 == 0 and dim <= 65536
-            and (rows // 256) * (dim // 256) <= SPLITK_GRAD_H_MAX_TILES and vocab > 0 and vocab % 64 == 0)
+    tiles (rows and dim multiples of 256, vocab of 64), except where the library GEMM measured
+    faster on MI355X: more than SPLITK_GRAD_H_MAX_TILES output tiles of 256 x 256 with dim a
+    power of two. With few tiles and K = vocab a library GEMM leaves most of the 256 CUs idle and
+    the split-K kernel spreads K over them; with many, the library's kernels fill the chip
+    themselves, and beat this kernel by 7-11% when dim is a power of two, but run 15-39% behind
+    it at the other Qwen3 head widths (ms per call at V = 151,936, split-K / hipBLASLt):
+
+        dim   rows 1024      2048           4096           8192
+        1024  0.29 / 0.72    0.57 / 0.94    1.07 / 1.43    2.08 / 1.94
+        2048  0.55 / 0.90    1.06 / 1.63    2.04 / 1.89    4.03 / 3.67
+        2560  0.72 / 1.00    1.35 / 1.83    2.79 / 3.38    5.33 / 7.40
+        4096  1.10 / 1.80    2.07 / 1.89    4.08 / 3.62    8.16 / 7.32
+        5120  1.43 / 1.84    2.94 / 3.38    5.47 / 6.83    10.52 / 13.14
+    """
+    if not (rows > 0 and dim > 0 and rows % 256 == 0 and dim % 256 == 0 and dim <= 65536
+            and vocab > 0 and vocab % 64 == 0):
+        return False
+    return (rows // 256) * (dim // 256) <= SPLITK_GRAD_H_MAX_TILES or (dim & (dim - 1)) != 0
 
 
 FOLD_CHUNKS = 8  # chunks per grad_W fold (tm_ce_grad_w_fold takes at most 8)
