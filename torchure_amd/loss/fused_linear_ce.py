@@ -238,7 +238,7 @@ def splitk_grad_h_fits(rows: int, dim: int, vocab: int) -> bool:
     faster on MI355X: more than SPLITK_GRAD_H_MAX_TILES output tiles of 256 x 256 with dim a
     power of two. With few tiles and K = vocab a library GEMM leaves most of the 256 CUs idle and
     the split-K kernel spreads K over them; with many, the library's kernels fill the chip
-    themselves, and beat this kernel by 7-11% when dim is a power of two, but run 15-39% behind
+    themselves, and beat this kernel by 7-12% when dim is a power of two, but run 9-43% behind
     it at the other Qwen3 head widths (ms per call at V = 151,936, split-K / hipBLASLt):
 
         dim   rows 1024      2048           4096           8192
