@@ -1,19 +1,21 @@
-"""GPU parity of the split-K MFMA GEMM that computes the fused CE's grad_hidden
-(tm_ce_grad_h_bf16: grad_h = grad_logits @ W, torchure/loss/fused_linear_ce.py:52) and of
-the W^T it reads (tm_ce_transpose_bf16).
+"""GPU parity of the fused CE's three bf16 MFMA GEMMs (torchure/loss/fused_linear_ce.py:38,52,57):
+tm_ce_logits_bf16 (logits = h W^T), tm_ce_grad_h_bf16 (split-K grad_h = grad_logits W, with the
+W^T it reads from tm_ce_transpose_bf16) and tm_ce_grad_w_bf16 (grad_W = grad_logits^T h).
 
 Checks:
 - the transpose bit for bit against torch's;
-- the GEMM against an fp64 product of the same bf16 operands: every element within one bf16
-  ulp of the exact value plus 2^-20 of sum_k |a_ik b_kj| (the fp32 accumulation), at chunk
-  shapes from one output tile split into single K slices up to the Qwen3 head's 1024 x
-  151,936 x 1024 and a 4096-row chunk of a 2560-wide head;
+- each GEMM against an fp64 product of the same bf16 operands: every element within one bf16
+  ulp of the exact value plus 2^-20 of sum_k |a_ik b_kj| (the fp32 accumulation), at shapes
+  from one tile (or one K slice per split) with ragged edges up to the Qwen3 heads' chunks;
 - against torch.matmul (hipBLASLt) on the same operands: within one bf16 ulp plus the two
   fp32 accumulation budgets everywhere, and equal on at least 99% of the elements (the two
   differ only in fp32 summation order);
-- deterministic: the same bits on a repeat call over a workspace holding other data;
-- inside the op: the fused CE's grad_h on eligible chunks equals the GEMM's result for the
-  chunk's grad_logits, and the whole op stays within the reference composition's bars.
+- deterministic: the same bits on a repeat call (for grad_h over a workspace holding other
+  data); no write outside the output;
+- the persistent logits and grad_W kernels against the one-tile-per-workgroup kernels on the
+  same products: the same bits;
+- inside the op: the fused CE's grad_h equals the chosen GEMM's result for the chunk's
+  grad_logits, and the whole op stays within the reference composition's bars.
 """
 
 from __future__ import annotations
@@ -157,7 +159,8 @@ def test_op_grad_h_uses_the_gemm_on_eligible_chunks(chunk):
     for s in range(0, n, step):
         e = min(s + step, n)
         assert splitk_grad_h_fits(e - s, d, v)
-        logits = torch.matmul(hidden[s:e], w.t())
+        logits, _ = _logits(hidden[s:e], w)  # the op's logits GEMM
+        logits = logits.contiguous()
         _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, -100,
                                           row_loss[s:].data_ptr(), stream), "tm_ce_rows_bf16")
         want[s:e] = _grad_h(logits, w)
@@ -194,7 +197,8 @@ def test_op_mixes_the_gemm_and_the_library_on_ragged_chunks():
     kinds = []
     for s in range(0, n, chunk):
         e = min(s + chunk, n)
-        logits = torch.matmul(hidden[s:e], w.t())
+        logits, _ = _logits(hidden[s:e], w)  # the op's logits GEMM
+        logits = logits.contiguous()
         _native.check(lib.tm_ce_rows_bf16(logits.data_ptr(), v, labels[s:e].data_ptr(), e - s, v, -100,
                                           row_loss[s:].data_ptr(), stream), "tm_ce_rows_bf16")
         fits = splitk_grad_h_fits(e - s, d, v)
@@ -318,6 +322,28 @@ def test_logits_gemm_full_chunk_vs_library():
     assert same >= 0.99
 
 
+@pytest.mark.parametrize("rows,vocab,dim", [
+    (300, 1000, 256),
+    (2000, 20008, 384),
+    (1500, 32768, 2560),
+    (1024, 151936, 1024),
+    (8192, 151936, 1024),
+])
+def test_logits_ring_kernel_equals_one_tile_kernel(rows, vocab, dim):
+    """The persistent logits kernel (vocab a multiple of 8) and the one-tile-per-workgroup kernel
+    give the same bits: with one more weight row the vocabulary is no longer a multiple of 8, the
+    call takes the one-tile kernel, and every element of the first `vocab` columns keeps its
+    tile, its lanes and its MFMA sequence."""
+    g = torch.Generator(device=DEV).manual_seed(rows + vocab + 7 * dim)
+    h = torch.randn(rows, dim, device=DEV, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(vocab + 1, dim, device=DEV, generator=g) * 0.05).to(torch.bfloat16)
+    ring, guard = _logits(h, w1[:vocab])
+    assert guard
+    tile, guard = _logits(h, w1)
+    assert guard
+    assert torch.equal(ring.view(torch.int16), tile[:, :vocab].view(torch.int16))
+
+
 def test_logits_gemm_argument_checks():
     """Shapes the GEMM does not take and misaligned pointers are refused before any launch."""
     native, lib, stream = _lib()
@@ -410,6 +436,36 @@ def test_grad_w_gemm_full_chunk_vs_library():
     same /= vocab * dim
     print(f"equal to torch.matmul on {same:.5f} of the elements")
     assert same >= 0.99
+
+
+@pytest.mark.parametrize("rows,vocab,dim", [
+    (256, 1000, 256),
+    (384, 4104, 520),
+    (1024, 151936, 1024),
+    (4096, 32768, 2560),
+    (8192, 151936, 1024),
+])
+def test_grad_w_ring_kernel_equals_one_tile_kernel(rows, vocab, dim):
+    """The persistent grad_W kernel (rows a multiple of 128) and the one-tile-per-workgroup
+    kernel give the same values: 64 zero rows appended to grad_logits (and any 64 rows to h) make
+    the call take the one-tile kernel with one more K slice, whose products are all zero, so every
+    sum is the same; only the sign of an exact zero could differ, which a value comparison
+    ignores."""
+    g = torch.Generator(device=DEV).manual_seed(rows * 11 + vocab + dim)
+    x = torch.randn(rows, vocab, device=DEV, generator=g) * 3.0
+    p = torch.softmax(x, dim=1)
+    del x
+    lab = torch.randint(0, vocab, (rows,), device=DEV, generator=g)
+    p[torch.arange(rows, device=DEV), lab] -= 1.0
+    gl = torch.zeros(rows + 64, vocab, dtype=torch.bfloat16, device=DEV)
+    gl[:rows] = p.to(torch.bfloat16)
+    del p
+    h = torch.randn(rows + 64, dim, device=DEV, generator=g).to(torch.bfloat16)
+    ring, guard = _grad_w(gl[:rows], h[:rows])
+    assert guard
+    tile, guard = _grad_w(gl, h)
+    assert guard
+    assert torch.equal(ring, tile)
 
 
 def test_grad_w_gemm_argument_checks():
