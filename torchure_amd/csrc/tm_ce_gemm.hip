@@ -2,7 +2,8 @@
 // (torchure/loss/fused_linear_ce.py:38,52,57: bf16 matmuls, fp32 accumulation, bf16 results):
 //   logits_ring_kernel   logits = h W^T         (rows x V, K = D), persistent, for dim a multiple
 //                        of 128 (>= 256) and vocab a multiple of 8; logits_gemm_kernel otherwise
-//   grad_h_gemm_kernel   grad_h = grad_logits W (rows x D, K = V), split over K, with
+//   grad_h_gemm_kernel   grad_h = grad_logits W (rows x D, K = V), split over K (long splits on
+//   grad_h_gemm8_kernel  8 waves, two a SIMD), with
 //   grad_h_reduce_kernel summing the fp32 partials of each element over the splits in a fixed
 //                        order (split 0 first) and rounding once to bf16 (RNE), so the result
 //                        does not depend on scheduling
@@ -644,6 +645,146 @@ __global__ __launch_bounds__(256) void grad_h_gemm_kernel(const uint16_t* __rest
       }
 }
 
+// The same (split, tile) work on 8 waves, two a SIMD: wave (wm, wn) = (w / 2, w % 2) computes
+// rows wm * 64 .. +63 and columns wn * 128 .. +127 of the tile, 2 x 4 blocks of 32 x 32 (128
+// accumulators, which fit in the VGPRs beside the fragments). While one wave of a SIMD waits for
+// LDS reads, its loads or the stage barrier, the other's MFMAs run. LDS stages, swizzle, fragment
+// reads and stage schedule are nt_mainloop's, with 6 fragment reads and 8 MFMAs per K16 step and
+// 8 loads per stage a wave; every element sees the same MFMA sequence, so the bits are those of
+// grad_h_gemm_kernel. Measured on MI355X at V = 151,936 against grad_h_gemm_kernel: 8% faster
+// with 1187 K slices a split (8192 x 1024, 2 splits), 3-5% with 594-792 (4 and 3 splits), 5-7%
+// with 297 (8 splits); with 149 (1024 x 1024, 16 splits) 4-6% slower on one device and 5% faster
+// on another. The entry point takes it from kGh8MinIters slices a split.
+constexpr int kGh8MinIters = 256;
+
+__device__ __forceinline__ void nt8_mainloop(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                                             int64_t ld, int m0, int n0, int M, int N, int64_t k0, int n_it,
+                                             uint8_t* smem, f32x16 (&acc)[4][2]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  // Load j of this wave fills LDS rows 8 q .. 8 q + 7 of [A tile; B tile], q = 8 wave + j.
+  const uint16_t* src[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int q = wave * 8 + j;
+    const int r = (q % 32) * 8 + lane / 8;
+    const int c = (lane % 8) ^ ((r >> 1) & 7);
+    src[j] = (q < 32 ? A + static_cast<int64_t>(min(m0 + r, M - 1)) * ld
+                     : B + static_cast<int64_t>(min(n0 + r, N - 1)) * ld) + k0 + c * 8;
+  }
+  auto load = [&](int it, int stage, int j) {
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[j] + it * kSliceK),
+                                     (void __attribute__((address_space(3)))*)(smem + stage * kLgStage + (wave * 8 + j) * 1024),
+                                     16, 0, 0);
+  };
+  const int tx = (lane >> 5) ^ ((lane >> 1) & 7);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + (lane & 31) * 128;
+  uint32_t vk[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) vk[kk] = lds0 + (((2 * kk) ^ tx) * 16);
+  const uint32_t offA = wm * 64 * 128, offB = kLgTile * 128 + wn * 128 * 128;
+#define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
+#define TM_WAIT6(f) \
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]))
+  // fragment g: g < 4 -> B (n) block g, g >= 4 -> A (m) block g - 4
+  bf16x8 f0[6], f1[6];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) load(0, 0, j);
+  if (n_it > 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) load(1, 1, j);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int g = 0; g < 6; ++g) TM_RD(f0[g], vk[0] + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+  TM_WAIT6(f0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  auto stage = [&](int i, auto step) {
+    constexpr bool kNext = decltype(step)::kNextV, kNext2 = decltype(step)::kNext2V;
+    const int s = i & 1;
+    const uint32_t soff = s * kLgStage, noff = (s ^ 1) * kLgStage;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x8* cur = (kk & 1) ? f1 : f0;
+      bf16x8* nxt = (kk & 1) ? f0 : f1;
+      if (kk == 3 && kNext) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wave's loads of stage i + 1 are in LDS
+        __builtin_amdgcn_s_barrier();               // every wave's; and stage i's reads are done
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {  // one MFMA, at most one fragment read, at most one load
+        if (g < 6) {
+          if (kk < 3) {
+            TM_RD(nxt[g], vk[kk + 1] + soff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+          } else if (kNext) {
+            TM_RD(nxt[g], vk[0] + noff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+          }
+        }
+        if (kk == 3 && kNext2) load(i + 2, s, g);
+        const int ii = g / 2, jj = g % 2;
+        acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], acc[ii][jj], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (kk < 3 || kNext) {
+        TM_WAIT6(nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  int i = 0;
+  for (; i + 2 < n_it; ++i) stage(i, LgFlags<true, true>{});
+  if (i + 1 < n_it) stage(i++, LgFlags<true, false>{});
+  if (i < n_it) stage(i, LgFlags<false, false>{});
+#undef TM_RD
+#undef TM_WAIT6
+}
+
+__global__ __launch_bounds__(512) void grad_h_gemm8_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ Wt,
+                                                           float* __restrict__ partials, int rows, int dim, int64_t K,
+                                                           int tiles, int splits, int iters_per_split) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int pairs = tiles * splits;
+  const int p8 = (pairs + 7) / 8;
+  const int p = (blockIdx.x % 8) * p8 + blockIdx.x / 8;
+  if (p >= pairs) return;
+  const int s = p / tiles, tile = p - s * tiles;
+  const int tiles_n = dim / kLgTile;
+  const int m0 = (tile / tiles_n) * kLgTile, n0 = (tile % tiles_n) * kLgTile;
+  const int total = static_cast<int>(K / kSliceK);
+  const int it0 = s * iters_per_split;
+  const int n_it = max(0, min(iters_per_split, total - it0));
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  f32x16 acc[4][2];  // [n block][m block]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  if (n_it > 0) nt8_mainloop(G, Wt, K, m0, n0, rows, dim, static_cast<int64_t>(it0) * kSliceK, n_it, smem, acc);
+
+  float* P = partials + static_cast<int64_t>(s) * rows * dim;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = m0 + wm * 64 + jj * 32 + (lane & 31);
+        const int n = n0 + wn * 128 + ii * 32 + 8 * q + 4 * (lane >> 5);
+        const f32x4 v = {acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1], acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]};
+        *(f32x4*)(P + static_cast<int64_t>(m) * dim + n) = v;
+      }
+}
+
 // ------------------------------------------------------- grad_W = grad_logits^T @ hidden
 //
 // fused_linear_ce.py:57 `gw = grad_logits.t() @ h` per chunk: C (vocab x dim) = G^T H with
@@ -1101,11 +1242,11 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // launch there. The device's CU count (for the ring kernels' workgroups per XCD) is read then.
 constexpr int kMaxDevices = 64;
 std::mutex g_lds_mu;
-bool g_lds_set[5][kMaxDevices] = {};
+bool g_lds_set[6][kMaxDevices] = {};
 int g_cus[kMaxDevices] = {};
 
 // which: 0 grad_h_gemm_kernel, 1 logits_gemm_kernel, 2 grad_w_gemm_kernel, 3 logits_ring_kernel,
-// 4 grad_w_ring_kernel.
+// 4 grad_w_ring_kernel, 5 grad_h_gemm8_kernel.
 // `cus`, when given, receives the device's CU count.
 hipError_t allow_lds(hipStream_t stream, int which, int* cus = nullptr) {
   int dev = -1;
@@ -1120,11 +1261,11 @@ hipError_t allow_lds(hipStream_t stream, int which, int* cus = nullptr) {
   int cur = -1;
   e = hipGetDevice(&cur);
   if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
-  const void* fn[5] = {reinterpret_cast<const void*>(grad_h_gemm_kernel), reinterpret_cast<const void*>(logits_gemm_kernel),
+  const void* fn[6] = {reinterpret_cast<const void*>(grad_h_gemm_kernel), reinterpret_cast<const void*>(logits_gemm_kernel),
                        reinterpret_cast<const void*>(grad_w_gemm_kernel), reinterpret_cast<const void*>(logits_ring_kernel),
-                       reinterpret_cast<const void*>(grad_w_ring_kernel)};
-  if (e == hipSuccess)
-    e = hipFuncSetAttribute(fn[which], hipFuncAttributeMaxDynamicSharedMemorySize, which >= 3 ? kRgLds : kLgLds);
+                       reinterpret_cast<const void*>(grad_w_ring_kernel), reinterpret_cast<const void*>(grad_h_gemm8_kernel)};
+  const int bytes[6] = {kLgLds, kLgLds, kLgLds, kRgLds, kRgLds, 2 * kLgStage};
+  if (e == hipSuccess) e = hipFuncSetAttribute(fn[which], hipFuncAttributeMaxDynamicSharedMemorySize, bytes[which]);
   if (e == hipSuccess && g_cus[dev] == 0) e = hipDeviceGetAttribute(&g_cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
   if (cur >= 0 && cur != dev) {
     const hipError_t back = hipSetDevice(cur);
@@ -1163,19 +1304,28 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
     return gemm_fail(TM_EINVAL, "tm_ce_grad_h_bf16: workspace of %zu bytes, %zu needed", ws_bytes,
                      tm_ce_grad_h_workspace_bytes(rows, vocab, dim));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t lds = allow_lds(s, 0);
-  if (lds != hipSuccess)
-    return gemm_fail(TM_ELAUNCH, "tm_ce_grad_h_bf16: LDS attribute: %s", hipGetErrorString(lds));
   const int64_t splits = splits_for(rows, vocab, dim);
   const int64_t tiles = (rows / kTile) * (dim / kTile);
   const int64_t total_iters = vocab / kSliceK;
   const int64_t per = (total_iters + splits - 1) / splits;
+  const bool eight = per >= kGh8MinIters;  // same bits either way
+  const hipError_t lds = allow_lds(s, eight ? 5 : 0);
+  if (lds != hipSuccess)
+    return gemm_fail(TM_ELAUNCH, "tm_ce_grad_h_bf16: LDS attribute: %s", hipGetErrorString(lds));
   float* partials = static_cast<float*>(d_ws);
-  hipLaunchKernelGGL(grad_h_gemm_kernel, dim3(static_cast<uint32_t>((tiles * splits + 7) / 8 * 8)), dim3(256),
-                     kLgLds, s, d_grad_logits, d_wt, partials, static_cast<int>(rows), static_cast<int>(dim),
-                     vocab, static_cast<int>(tiles), static_cast<int>(splits), static_cast<int>(per));
+  const dim3 grid(static_cast<uint32_t>((tiles * splits + 7) / 8 * 8));
+  if (eight)
+    hipLaunchKernelGGL(grad_h_gemm8_kernel, grid, dim3(512), 2 * kLgStage, s, d_grad_logits, d_wt, partials,
+                       static_cast<int>(rows), static_cast<int>(dim), vocab, static_cast<int>(tiles),
+                       static_cast<int>(splits), static_cast<int>(per));
+  else
+    hipLaunchKernelGGL(grad_h_gemm_kernel, grid, dim3(256), kLgLds, s, d_grad_logits, d_wt, partials,
+                       static_cast<int>(rows), static_cast<int>(dim), vocab, static_cast<int>(tiles),
+                       static_cast<int>(splits), static_cast<int>(per));
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "grad_h_gemm_kernel: launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess)
+    return gemm_fail(TM_ELAUNCH, "%s: launch failed: %s", eight ? "grad_h_gemm8_kernel" : "grad_h_gemm_kernel",
+                     hipGetErrorString(e));
   const int64_t n = rows * dim;
   hipLaunchKernelGGL(grad_h_reduce_kernel, dim3(static_cast<uint32_t>((n / 4 + 255) / 256)), dim3(256), 0, s,
                      partials, d_grad_h, n, static_cast<int>(splits));
