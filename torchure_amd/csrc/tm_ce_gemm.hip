@@ -11,16 +11,20 @@
 //                        multiple of 128 (>= 256); grad_w_gemm_kernel otherwise
 // and transpose_bf16_kernel, which makes W^T (D x V) once per call for grad_h.
 //
-// All three are 256 x 256 output tiles per workgroup of 4 wave64 (each 128 x 128, 256 fp32
-// accumulators) on v_mfma_f32_32x32x16_bf16. Operands stream global -> LDS with direct loads
-// (global_load_lds, 16 bytes a lane) into two 64 KB stages of 64-deep K slices. gfx950's LDS has
-// 64 four-byte banks and serves a 16-byte-per-lane read 16 lanes at a time, so the 16 lanes
-// reading 16 consecutive 128-byte rows must hit 16 different 16-byte bank groups: a row's chunk c
-// sits at slot c ^ ((row >> 1) & 7), which gives rows 2j and 2j+1 (one even, one odd: the two
-// halves of the banks) the slot pattern c ^ j. (The 32-bank pattern c ^ (row & 7) put rows r and
-// r+8 on one bank group and doubled the read time.) Workgroup w runs on XCD w % 8; each XCD takes
-// a contiguous range of tiles (or of split-tile pairs), so the operand panels its 32 CUs share
-// are read from HBM about once and then served from that XCD's L2.
+// All three are 256 x 256 output tiles per workgroup on v_mfma_f32_32x32x16_bf16 with fp32
+// accumulation: the ring kernels and grad_h_gemm8_kernel on 8 wave64, two a SIMD (each 128 x 64
+// or 64 x 128, 128 accumulators), so that one wave's MFMAs run while the other waits; the
+// one-tile kernels and grad_h_gemm_kernel on 4 wave64 (each 128 x 128, 256 accumulators in the
+// AGPRs). Every element sees the same MFMA sequence in all of them. Operands stream
+// global -> LDS with direct loads (global_load_lds, 16 bytes a lane) into two 64 KB stages of
+// 64-deep K slices. gfx950's LDS has 64 four-byte banks and serves a 16-byte-per-lane read 16
+// lanes at a time, so the 16 lanes reading 16 consecutive 128-byte rows must hit 16 different
+// 16-byte bank groups: a row's chunk c sits at slot c ^ ((row >> 1) & 7), which gives rows 2j and
+// 2j+1 (one even, one odd: the two halves of the banks) the slot pattern c ^ j. (The 32-bank
+// pattern c ^ (row & 7) put rows r and r+8 on one bank group and doubled the read time.)
+// Workgroup w runs on XCD w % 8; each XCD takes a contiguous range of tiles (or of split-tile
+// pairs), so the operand panels its 32 CUs share are read from HBM about once and then served
+// from that XCD's L2.
 //
 // For the reference's default chunk of 1024 rows, grad_h is a long-K GEMM (K = V = 151,936 for
 // the Qwen3 head) with a small output (1024 x 1024): 16 tiles for 256 CUs, which the library GEMM
@@ -329,25 +333,30 @@ __global__ __launch_bounds__(256) void logits_gemm_kernel(const uint16_t* __rest
 // The same product, tiles, fragments and summation order as logits_gemm_kernel (bit-identical
 // results), for the shapes the Qwen heads have (dim a multiple of 128 and at least 256, vocab a
 // multiple of 8, operands under 4 GiB). With K = dim short (16 slices at dim 1024), a tile's
-// fill (its first two stages' loads) and its epilogue (256 accumulators per lane converted to
-// bf16 and written) were a large share of a tile's time; here both overlap the neighbouring
-// tiles' MFMAs:
+// fill (its first two stages' loads) and its epilogue (its accumulators converted to bf16 and
+// written) were a large share of a tile's time; here both overlap the neighbouring tiles' MFMAs:
 //   - workgroup c of XCD x (blockIdx = 8 c + x) runs tile positions x t8 + c, + W, + 2W, ...
 //     (W workgroups per XCD), so the 32 tiles an XCD runs at a time are the same groups of
 //     tiles as in logits_gemm_kernel;
 //   - the operand stages form one ring across tiles: the next tile's stages 0 and 1 are loaded
 //     during the current tile's last two stages (the tile after the last is the last again, a
 //     harmless reload drained before exit);
+//   - 8 waves, two a SIMD: wave (wm, wn) = (w / 4, w % 4) computes rows wm * 128 .. +127 and
+//     columns wn * 64 .. +63 of the tile, 4 m blocks x 2 n blocks of 32 x 32 (128 accumulators,
+//     in VGPRs); while one wave of a SIMD waits for LDS, its loads, the stage barrier or its
+//     stores, the other's MFMAs run (measured on MI355X: 4-12% faster than one wave a SIMD with
+//     128 x 128 each, the same bits). Per K16 step a wave reads 6 fragments and issues 8 MFMAs;
+//     waves 0-3 load the hidden rows, waves 4-7 the weight rows, 8 loads a stage each;
 //   - the finished tile's accumulators leave during the next tile's first K16 step: block
 //     (ii, jj) is converted to bf16 (RNE) just before that step's MFMA on it, which restarts
-//     its accumulation from zero; the 4 blocks of a quarter (32 rows of the wave's 128) go to
-//     this wave's 8 KB of LDS past the two stages (chunk c of row r at slot c ^ (r & 15)), and
-//     are written back as whole 256-byte rows, 16 bytes a lane; the last tile's output goes
-//     the same way after the loop.
-// LDS: two 64 KB stages + 4 x 8 KB = 160 KB, the whole of a CU's. Operand addresses are 32-bit
+//     its accumulation from zero; the 2 blocks of an m block (32 rows x the wave's 64 columns)
+//     go to this wave's 4 KB of LDS past the two stages (128-byte rows, chunk c of row r at slot
+//     c ^ ((r >> 1) & 7)) and are written back as 128-byte row pieces, 16 bytes a lane; the
+//     last tile's output goes the same way after the loop.
+// LDS: two 64 KB stages + 8 x 4 KB = 160 KB, the whole of a CU's. Operand addresses are 32-bit
 // byte offsets from the operand's base (scalar), one per load.
 
-constexpr int kRgLds = 2 * kLgStage + 4 * 8192;  // 163,840 B
+constexpr int kRgLds = 2 * kLgStage + 8 * 4096;  // 163,840 B
 
 template <bool kN2, bool kPre, bool kFirst, bool kEpi>
 struct RgFlags {
@@ -359,7 +368,7 @@ struct RgBool {
   static constexpr bool value = kV;
 };
 
-__global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+__global__ __launch_bounds__(512) void logits_ring_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                                                           uint16_t* __restrict__ C, int M, int N, int K, int tiles_m,
                                                           int tiles_n, int gm, int gn, int wpx) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -371,66 +380,61 @@ __global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __rest
   if (p >= pend) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   const int n_it = K / kSliceK;  // even, >= 4
 
-  // Waves 0, 1 load the A rows of the tile, waves 2, 3 the B rows; load j of a wave fills rows
-  // 8 j + lane / 8 of its 128-row half, the lane's chunk (lane % 8) ^ ((row >> 1) & 7), which is
-  // (lane % 8) ^ (lane / 16) ^ (4 (j % 2)). The empty asm keeps the per-lane parts from being
-  // precomputed per load outside the tile loop (16 more live registers).
-  const char* opnd = reinterpret_cast<const char*>(wave < 2 ? A : B);
-  const int lim = (wave < 2 ? M : N) - 1;
-  uint32_t soff[16];
+  // Waves 0-3 load the A rows of the tile, waves 4-7 the B rows; load j of wave w fills rows
+  // 64 (w % 4) + 8 j + lane / 8 of its operand, the lane's chunk (lane % 8) ^ (lane / 16) ^ (4 (j % 2)).
+  const char* opnd = reinterpret_cast<const char*>(wave < 4 ? A : B);
+  const int lim = (wave < 4 ? M : N) - 1;
+  uint32_t soff[8];
   int lrow = lane / 8;
   uint32_t lc16 = static_cast<uint32_t>(((lane % 8) ^ (lane / 16)) * 16);
   auto set_src = [&](int m0, int n0) {
     asm volatile("" : "+v"(lrow), "+v"(lc16));
-    const int r0 = (wave < 2 ? m0 : n0) + (wave % 2) * 128;
+    const int r0 = (wave < 4 ? m0 : n0) + (wave % 4) * 64;
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
+    for (int j = 0; j < 8; ++j)
       soff[j] = static_cast<uint32_t>(min(r0 + 8 * j + lrow, lim)) * static_cast<uint32_t>(2 * K) +
                 (lc16 ^ ((j & 1) * 64));
   };
   auto load = [&](int it, int stage, int j) {
     __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(opnd + (soff[j] + it * 128u)),
-                                     (void __attribute__((address_space(3)))*)(smem + stage * kLgStage + (wave * 16 + j) * 1024),
+                                     (void __attribute__((address_space(3)))*)(smem + stage * kLgStage + (wave * 8 + j) * 1024),
                                      16, 0, 0);
   };
-  // fragment reads as in nt_mainloop
   const int tx = (lane >> 5) ^ ((lane >> 1) & 7);
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + (lane & 31) * 128;
   uint32_t vk[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) vk[kk] = lds0 + (((2 * kk) ^ tx) * 16);
-  const uint32_t offA = wm * 128 * 128, offB = kLgTile * 128 + wn * 128 * 128;
+  const uint32_t offA = wm * 128 * 128, offB = kLgTile * 128 + wn * 64 * 128;
 
-  // Output staging, this wave's 8 KB: row r (of a quarter's 32) at 256 r, chunk c at slot
-  // c ^ (r & 15). A lane writes row lane % 32, half lane / 32 of chunk c at wa ^ (c << 4); it
-  // reads back chunk lane % 16 of row 4 it + lane / 16 at ra[it % 4] + 4096 (it / 4).
-  const uint32_t ebo = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + 2 * kLgStage + wave * 8192;
-  uint32_t wa = ebo + (lane & 31) * 256 + (lane >> 5) * 8 + ((lane & 15) << 4);
+  // Output staging, this wave's 4 KB: row r (of an m block's 32) at 128 r, chunk c at slot
+  // c ^ ((r >> 1) & 7). A lane writes row lane % 32, half lane / 32 of chunk c; it reads back chunk
+  // lane % 8 of row 8 it + lane / 8.
+  const uint32_t ebo = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + 2 * kLgStage + wave * 4096;
+  const int wr = lane & 31;
+  uint32_t wa = ebo + wr * 128 + (lane >> 5) * 8;
+  const uint32_t wsw = static_cast<uint32_t>((wr >> 1) & 7);
   uint32_t ra[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int r = k * 4 + (lane >> 4);
-    ra[k] = ebo + r * 256 + (((lane & 15) ^ r) << 4);
+    const int r = k * 8 + (lane >> 3);
+    ra[k] = ebo + r * 128 + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
   }
-  uint32_t sl = static_cast<uint32_t>(((lane >> 4) * N + (lane & 15) * 8) * 2);  // byte offset of the lane's store
+  uint32_t sl = static_cast<uint32_t>(((lane >> 3) * N + (lane & 7) * 8) * 2);  // byte offset of the lane's store
 
 #define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
-#define TM_WAIT8(f)                                                                                       \
-  asm volatile("s_waitcnt lgkmcnt(0)"                                                                   \
-               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]))
-  bf16x8 f0[8], f1[8];
-  f32x16 acc[4][4];  // [n block][m block]
-  int pm0 = 0, pn0 = 0;  // origin of the tile whose output is being written
+#define TM_WAIT6(f) \
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]))
+  // fragment g: g < 2 -> B (n) block g, g >= 2 -> A (m) block g - 2
+  bf16x8 f0[6], f1[6];
+  f32x16 acc[2][4];  // [n block][m block]
+  int pm0 = 0, pn0 = 0;
 
-  // Block (ii, jj) of the finished tile to bf16 in the staging; with `mfma`, the next tile's first
-  // MFMA on the block follows the reads. The empty asms fix that order: the block is read after
-  // the previous block's LDS writes, and its MFMA after the conversion (otherwise all 256
-  // accumulators are copied out at once and the registers spill).
   auto epi_block = [&](int ii, int jj, bool mfma, bf16x8* cur) {
-    asm volatile("" : "+a"(acc[ii][jj]));
+    asm volatile("" : "+v"(acc[ii][jj]));
     u32x2 o[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -439,29 +443,25 @@ __global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __rest
     }
     if (mfma) {
       asm volatile("" : "+v"(cur[ii]) : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]));
-      acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], f32x16{}, 0, 0, 0);
+      acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[2 + jj], f32x16{}, 0, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint32_t a = wa ^ ((ii * 4 + q) << 4);
+      const uint32_t a = wa + (((static_cast<uint32_t>(ii * 4 + q)) ^ wsw) << 4);
       asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(o[q]) : "memory");
     }
   };
-  // Quarter jj (32 rows) of the finished tile at (pm0, pn0): staging -> global. N % 8 == 0, so a
-  // lane's 8 columns are all in range or all out.
   auto epi_store = [&](int jj) {
-    u32x4 v[8];
+    u32x4 v[4];
 #pragma unroll
-    for (int it = 0; it < 8; ++it)
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v[it]) : "v"(ra[it & 3]), "i"((it >> 2) * 16 * 256));
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
-    const int rows_left = M - (pm0 + wm * 128 + jj * 32), cols_left = N - (pn0 + wn * 128);
-    char* qb = reinterpret_cast<char*>(C) + (static_cast<int64_t>(pm0 + wm * 128 + jj * 32) * N + pn0 + wn * 128) * 2;
+    for (int it = 0; it < 4; ++it) asm volatile("ds_read_b128 %0, %1" : "=v"(v[it]) : "v"(ra[it]));
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+    const int rows_left = M - (pm0 + wm * 128 + jj * 32), cols_left = N - (pn0 + wn * 64);
+    char* qb = reinterpret_cast<char*>(C) + (static_cast<int64_t>(pm0 + wm * 128 + jj * 32) * N + pn0 + wn * 64) * 2;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      if (it * 4 + (lane >> 4) < rows_left && (lane & 15) * 8 < cols_left)
-        __builtin_nontemporal_store(v[it], reinterpret_cast<u32x4*>(qb + (sl + static_cast<uint32_t>(it * 8 * N))));
+    for (int it = 0; it < 4; ++it) {
+      if (it * 8 + (lane >> 3) < rows_left && (lane & 7) * 8 < cols_left)
+        __builtin_nontemporal_store(v[it], reinterpret_cast<u32x4*>(qb + (sl + static_cast<uint32_t>(it * 8 * N * 2))));
     }
   };
 
@@ -470,22 +470,19 @@ __global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __rest
   int m0 = tm * kLgTile, n0 = tn * kLgTile;
   set_src(m0, n0);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) load(0, 0, j);
+  for (int j = 0; j < 8; ++j) load(0, 0, j);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) load(1, 1, j);
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+  for (int j = 0; j < 8; ++j) load(1, 1, j);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int g = 0; g < 8; ++g) TM_RD(f0[g], vk[0] + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
-  TM_WAIT8(f0);
+  for (int g = 0; g < 6; ++g) TM_RD(f0[g], vk[0] + (g < 2 ? offB : offA), (g < 2 ? g : g - 2) * 32 * 128);
+  TM_WAIT6(f0);
   __builtin_amdgcn_sched_barrier(0);
 
   int pn = p, m0n = m0, n0n = n0;
   bool has_next = false;
-  // One tile: stage 0 (with the previous tile's output when kEpiFirst), then stages 1 .. n_it - 1,
-  // whose last two load the next tile's first two stages. The first tile is peeled so that every
-  // loop iteration enters with its accumulators in the same registers.
   auto tile = [&](auto epi_first) {
     constexpr bool kEpiFirst = decltype(epi_first)::value;
     asm volatile("" : "+v"(wa), "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]), "+v"(sl));
@@ -502,7 +499,7 @@ __global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __rest
       const int s = i & 1;
       const uint32_t soff_s = s * kLgStage, noff = (s ^ 1) * kLgStage;
       if (kPre) {
-        set_src(m0n, n0n);  // every load of this tile has been issued
+        set_src(m0n, n0n);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -513,49 +510,45 @@ __global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __rest
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-              if ((ii & 1) == 0) {
-                const int g = jj * 2 + ii / 2;
-                TM_RD(nxt[g], vk[1] + soff_s + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
-              }
+            for (int ii = 0; ii < 2; ++ii) {
+              const int g = jj * 2 + ii;
+              if (g < 6) TM_RD(nxt[g], vk[1] + soff_s + (g < 2 ? offB : offA), (g < 2 ? g : g - 2) * 32 * 128);
               epi_block(ii, jj, true, cur);
               __builtin_amdgcn_sched_barrier(0);
             }
             epi_store(jj);
             __builtin_amdgcn_sched_barrier(0);
           }
-          TM_WAIT8(nxt);
+          TM_WAIT6(nxt);
           __builtin_amdgcn_sched_barrier(0);
           continue;
         }
         if (kk == 3) {
-          __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wave's loads of the next stage are in LDS
-          __builtin_amdgcn_s_barrier();               // every wave's; and this stage's reads are done
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+          __builtin_amdgcn_s_barrier();
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
-          if (kk < 3) {
-            TM_RD(nxt[g], vk[kk + 1] + soff_s + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
-          } else {
-            TM_RD(nxt[g], vk[0] + noff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
+          if (g < 6) {
+            if (kk < 3) {
+              TM_RD(nxt[g], vk[kk + 1] + soff_s + (g < 2 ? offB : offA), (g < 2 ? g : g - 2) * 32 * 128);
+            } else {
+              TM_RD(nxt[g], vk[0] + noff + (g < 2 ? offB : offA), (g < 2 ? g : g - 2) * 32 * 128);
+            }
           }
           if (kk == 3 && kNext2) {
-            const int it2 = i + 2 >= n_it ? i + 2 - n_it : i + 2;  // past the end: the next tile's 0, 1
-            load(it2, s, 2 * g);
-            load(it2, s, 2 * g + 1);
+            const int it2 = i + 2 >= n_it ? i + 2 - n_it : i + 2;
+            load(it2, s, g);
           }
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const int idx = 2 * g + h, ii = idx / 4, jj = idx % 4;
-            if (kFirst && kk == 0)
-              acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], f32x16{}, 0, 0, 0);
-            else
-              acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], acc[ii][jj], 0, 0, 0);
-          }
+          const int jj = g / 2, ii = g % 2;
+          if (kFirst && kk == 0)
+            acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[2 + jj], f32x16{}, 0, 0, 0);
+          else
+            acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[2 + jj], acc[ii][jj], 0, 0, 0);
           __builtin_amdgcn_sched_barrier(0);
         }
-        TM_WAIT8(nxt);
+        TM_WAIT6(nxt);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -574,16 +567,15 @@ __global__ __launch_bounds__(256) void logits_ring_kernel(const uint16_t* __rest
     __builtin_amdgcn_sched_barrier(0);
     tile(RgBool<true>{});
   }
-  // the last tile's output; then the redundant reload of that tile's first stages completes
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) epi_block(ii, jj, false, f0);
+    for (int ii = 0; ii < 2; ++ii) epi_block(ii, jj, false, f0);
     epi_store(jj);
   }
   __builtin_amdgcn_s_waitcnt(0);
 #undef TM_RD
-#undef TM_WAIT8
+#undef TM_WAIT6
 }
 
 // The ring kernel's preconditions: K slices in an even number >= 4, whole 8-column store groups,
@@ -955,12 +947,15 @@ __global__ __launch_bounds__(256) void grad_w_gemm_kernel(const uint16_t* __rest
 // grad_w_gemm_kernel's tiles, loads, transposing fragment reads and summation order (bit-identical
 // results) in logits_ring_kernel's persistent form: workgroup c of XCD x runs the XCD's tile
 // positions c, c + W, ...; the next tile's first two stages load during the current tile's last
-// two; the finished tile's accumulators are converted and staged block by block during the next
-// tile's first K16 step (a quarter of 32 vocab rows at a time through the wave's 8 KB past the
-// stages) and written as whole 256-byte rows of grad_W. For rows (K) a multiple of 128 and at
+// two; 8 waves, two a SIMD, wave (wm, wn) = (w / 4, w % 4) computing vocab rows wm * 128 .. +127
+// and dim columns wn * 64 .. +63 (4 vocab x 2 dim blocks; 12 transposing half-fragment reads and
+// 8 MFMAs per K16 step; measured on MI355X: 4-10% faster than one wave a SIMD, the same bits);
+// the finished tile's accumulators are converted and staged block by block during the next tile's
+// first K16 step (32 vocab rows x the wave's 64 dim columns at a time through the wave's 4 KB past
+// the stages) and written as 128-byte row pieces of grad_W. For rows (K) a multiple of 128 and at
 // least 256, vocab and dim multiples of 8, operands under 4 GiB; grad_w_gemm_kernel otherwise.
 
-__global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ H,
+__global__ __launch_bounds__(512) void grad_w_ring_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ H,
                                                           uint16_t* __restrict__ C, int V, int D, int K, int tiles_v,
                                                           int tiles_d, int gm, int gn, int wpx) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -972,25 +967,25 @@ __global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __rest
   if (p >= pend) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;  // vocab half, dim half
+  const int wm = wave >> 2, wn = wave & 3;  // vocab half, dim quarter
   const int n_it = K / kSliceK;             // even, >= 4
 
-  // Waves 0, 1 load G (rows 0-31 / 32-63 of a stage), waves 2, 3 H. Load j: stage rows
-  // 32 (wave % 2) + 2 j + lane / 32, slot lane % 32 taking chunk (lane % 32) ^ (4 (row & 3)) =
+  // Waves 0-3 load G (rows 16 (wave % 4) .. +15 of a stage), waves 4-7 H. Load j: stage rows
+  // 16 (wave % 4) + 2 j + lane / 32, slot lane % 32 taking chunk (lane % 32) ^ (4 (row & 3)) =
   // (lane % 32) ^ (4 (lane / 32)) ^ (8 (j % 2)).
-  const char* opnd = reinterpret_cast<const char*>(wave < 2 ? G : H);
-  const int ld = wave < 2 ? V : D;
+  const char* opnd = reinterpret_cast<const char*>(wave < 4 ? G : H);
+  const int ld = wave < 4 ? V : D;
   const int lim8 = ld - 8;
   const uint32_t step = static_cast<uint32_t>(kSliceK) * static_cast<uint32_t>(ld) * 2u;  // bytes per stage
-  uint32_t soff[16];
+  uint32_t soff[8];
   int lkr = lane >> 5;
   int lc = (lane & 31) ^ (4 * (lane >> 5));
   auto set_src = [&](int v0, int d0) {
     asm volatile("" : "+v"(lkr), "+v"(lc));
-    const int col0 = wave < 2 ? v0 : d0;
-    const int r0 = (wave % 2) * 32;
+    const int col0 = wave < 4 ? v0 : d0;
+    const int r0 = (wave % 4) * 16;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
+    for (int j = 0; j < 8; ++j) {
       const int kr = r0 + 2 * j + lkr;
       const int c = lc ^ (8 * (j & 1));
       soff[j] = (static_cast<uint32_t>(kr) * static_cast<uint32_t>(ld) + static_cast<uint32_t>(min(col0 + 8 * c, lim8))) * 2u;
@@ -998,49 +993,52 @@ __global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __rest
   };
   auto load = [&](int it, int stage, int j) {
     __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(opnd + (soff[j] + static_cast<uint32_t>(it) * step)),
-                                     (void __attribute__((address_space(3)))*)(smem + stage * kGwStage + (wave * 16 + j) * 1024),
+                                     (void __attribute__((address_space(3)))*)(smem + stage * kGwStage + (wave * 8 + j) * 1024),
                                      16, 0, 0);
   };
-  // transposing fragment reads as in grad_w_gemm_kernel; output staging as in logits_ring_kernel
+  // transposing fragment reads as in grad_w_gemm_kernel, for the wave's 4 vocab and 2 dim blocks
   const int s16 = lane & 15, s4 = s16 >> 2;
   const int lcf = ((lane >> 4) & 1) * 2 + ((s16 & 3) >> 1);
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
   const uint32_t rowb = (8 * (lane >> 5) + s4) * 512 + (s16 & 1) * 8;
-  uint32_t bv[4], bd[4];
+  uint32_t bv[4], bd[2];
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    bv[b] = lds0 + rowb + (16 * wm + 4 * (b ^ s4) + lcf) * 16;
-    bd[b] = lds0 + kGwOp + rowb + (16 * wn + 4 * (b ^ s4) + lcf) * 16;
-  }
+  for (int b = 0; b < 4; ++b) bv[b] = lds0 + rowb + (16 * wm + 4 * (b ^ s4) + lcf) * 16;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) bd[b] = lds0 + kGwOp + rowb + (4 * ((2 * wn + b) ^ s4) + lcf) * 16;
 
-  const uint32_t ebo = lds0 + 2 * kGwStage + wave * 8192;
-  uint32_t wa = ebo + (lane & 31) * 256 + (lane >> 5) * 8 + ((lane & 15) << 4);
+  // Output staging, this wave's 4 KB: vocab row r (of a vocab block's 32) at 128 r, chunk c at
+  // slot c ^ ((r >> 1) & 7); read back as chunk lane % 8 of row 8 it + lane / 8.
+  const uint32_t ebo = lds0 + 2 * kGwStage + wave * 4096;
+  const int wr = lane & 31;
+  uint32_t wa = ebo + wr * 128 + (lane >> 5) * 8;
+  const uint32_t wsw = static_cast<uint32_t>((wr >> 1) & 7);
   uint32_t ra[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int r = k * 4 + (lane >> 4);
-    ra[k] = ebo + r * 256 + (((lane & 15) ^ r) << 4);
+  for (int kq = 0; kq < 4; ++kq) {
+    const int r = kq * 8 + (lane >> 3);
+    ra[kq] = ebo + r * 128 + (((lane & 7) ^ ((r >> 1) & 7)) << 4);
   }
-  uint32_t sl = static_cast<uint32_t>(((lane >> 4) * D + (lane & 15) * 8) * 2);
+  uint32_t sl = static_cast<uint32_t>(((lane >> 3) * D + (lane & 7) * 8) * 2);
 
 #define TM_TR(dst, base, imm) asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
-#define TM_WAIT16(f)                                                                                        \
+#define TM_WAIT12(f)                                                                                        \
   asm volatile("s_waitcnt lgkmcnt(0)"                                                                     \
                : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7]), \
-                 "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]), "+v"(f[12]), "+v"(f[13]), "+v"(f[14]),      \
-                 "+v"(f[15]))
-  bf16x4 f0[16], f1[16];
+                 "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]))
+  // half-fragment h = 2 g + r: g < 2 -> dim block g, g >= 2 -> vocab block g - 2; r: rows +0 / +4
+  bf16x4 f0[12], f1[12];
   auto rd = [&](bf16x4* f, uint32_t so, int kk, int h) {
     const int g = h >> 1, r = h & 1;
-    TM_TR(f[h], (g < 4 ? bd[g] : bv[g - 4]) + so, kk * 16 * 512 + r * 4 * 512);
+    TM_TR(f[h], (g < 2 ? bd[g] : bv[g - 2]) + so, kk * 16 * 512 + r * 4 * 512);
   };
-  f32x16 acc[4][4];  // [dim block][vocab block]
+  f32x16 acc[2][4];  // [dim block][vocab block]
   int pv0 = 0, pd0 = 0;  // origin of the tile whose output is being written
 
   // block (ii, jj) -> staging (and the next tile's first MFMA on it), as in logits_ring_kernel
 
   auto epi_block = [&](int ii, int jj, bool mfma, bf16x4* cur) {
-    asm volatile("" : "+a"(acc[ii][jj]));
+    asm volatile("" : "+v"(acc[ii][jj]));
     u32x2 o[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -1050,29 +1048,27 @@ __global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __rest
     if (mfma) {
       asm volatile("" : "+v"(cur[2 * ii]) : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]));
       const bf16x8 a = __builtin_shufflevector(cur[2 * ii], cur[2 * ii + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-      const bf16x8 b = __builtin_shufflevector(cur[8 + 2 * jj], cur[9 + 2 * jj], 0, 1, 2, 3, 4, 5, 6, 7);
+      const bf16x8 b = __builtin_shufflevector(cur[4 + 2 * jj], cur[5 + 2 * jj], 0, 1, 2, 3, 4, 5, 6, 7);
       acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, f32x16{}, 0, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint32_t a = wa ^ ((ii * 4 + q) << 4);
+      const uint32_t a = wa + (((static_cast<uint32_t>(ii * 4 + q)) ^ wsw) << 4);
       asm volatile("ds_write_b64 %0, %1" ::"v"(a), "v"(o[q]) : "memory");
     }
   };
-  // quarter jj (32 vocab rows) of the finished tile -> grad_W rows, 16 bytes a lane (D % 8 == 0)
+  // vocab block jj (32 rows x the wave's 64 dim columns) -> grad_W, 16 bytes a lane (D % 8 == 0)
   auto epi_store = [&](int jj) {
-    u32x4 v[8];
+    u32x4 v[4];
 #pragma unroll
-    for (int it = 0; it < 8; ++it)
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v[it]) : "v"(ra[it & 3]), "i"((it >> 2) * 16 * 256));
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
-    const int rows_left = V - (pv0 + wm * 128 + jj * 32), cols_left = D - (pd0 + wn * 128);
-    char* qb = reinterpret_cast<char*>(C) + (static_cast<int64_t>(pv0 + wm * 128 + jj * 32) * D + pd0 + wn * 128) * 2;
+    for (int it = 0; it < 4; ++it) asm volatile("ds_read_b128 %0, %1" : "=v"(v[it]) : "v"(ra[it]));
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+    const int rows_left = V - (pv0 + wm * 128 + jj * 32), cols_left = D - (pd0 + wn * 64);
+    char* qb = reinterpret_cast<char*>(C) + (static_cast<int64_t>(pv0 + wm * 128 + jj * 32) * D + pd0 + wn * 64) * 2;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      if (it * 4 + (lane >> 4) < rows_left && (lane & 15) * 8 < cols_left)
-        __builtin_nontemporal_store(v[it], reinterpret_cast<u32x4*>(qb + (sl + static_cast<uint32_t>(it * 8 * D))));
+    for (int it = 0; it < 4; ++it) {
+      if (it * 8 + (lane >> 3) < rows_left && (lane & 7) * 8 < cols_left)
+        __builtin_nontemporal_store(v[it], reinterpret_cast<u32x4*>(qb + (sl + static_cast<uint32_t>(it * 8 * D * 2))));
     }
   };
 
@@ -1081,15 +1077,15 @@ __global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __rest
   int v0 = tv * kLgTile, d0 = td * kLgTile;
   set_src(v0, d0);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) load(0, 0, j);
+  for (int j = 0; j < 8; ++j) load(0, 0, j);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) load(1, 1, j);
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(16));
+  for (int j = 0; j < 8; ++j) load(1, 1, j);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int h = 0; h < 16; ++h) rd(f0, 0, 0, h);
-  TM_WAIT16(f0);
+  for (int h = 0; h < 12; ++h) rd(f0, 0, 0, h);
+  TM_WAIT12(f0);
   __builtin_amdgcn_sched_barrier(0);
 
   int pn = p, v0n = v0, d0n = d0;
@@ -1122,15 +1118,17 @@ __global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __rest
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-              rd(nxt, so, 1, jj * 4 + ii);
+            for (int ii = 0; ii < 2; ++ii) {
+              const int bi = jj * 2 + ii;
+              rd(nxt, so, 1, bi);
+              if (bi < 4) rd(nxt, so, 1, 8 + bi);
               epi_block(ii, jj, true, cur);
               __builtin_amdgcn_sched_barrier(0);
             }
             epi_store(jj);
             __builtin_amdgcn_sched_barrier(0);
           }
-          TM_WAIT16(nxt);
+          TM_WAIT12(nxt);
           __builtin_amdgcn_sched_barrier(0);
           continue;
         }
@@ -1140,23 +1138,28 @@ __global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __rest
           __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          if (kk < 3) rd(nxt, so, kk + 1, q);
-          else rd(nxt, noff, 0, q);
+        for (int q = 0; q < 8; ++q) {  // one MFMA, one or two half-fragment reads, at most one load
+          if (kk < 3) {
+            rd(nxt, so, kk + 1, q);
+            if (q < 4) rd(nxt, so, kk + 1, 8 + q);
+          } else {
+            rd(nxt, noff, 0, q);
+            if (q < 4) rd(nxt, noff, 0, 8 + q);
+          }
           if (kk == 3 && kNext2) {
             const int it2 = i + 2 >= n_it ? i + 2 - n_it : i + 2;
             load(it2, s, q);
           }
-          const int ii = q / 4, jj = q % 4;
+          const int jj = q / 2, ii = q % 2;
           const bf16x8 a = __builtin_shufflevector(cur[2 * ii], cur[2 * ii + 1], 0, 1, 2, 3, 4, 5, 6, 7);
-          const bf16x8 b = __builtin_shufflevector(cur[8 + 2 * jj], cur[9 + 2 * jj], 0, 1, 2, 3, 4, 5, 6, 7);
+          const bf16x8 b = __builtin_shufflevector(cur[4 + 2 * jj], cur[5 + 2 * jj], 0, 1, 2, 3, 4, 5, 6, 7);
           if (kFirst && kk == 0)
             acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, f32x16{}, 0, 0, 0);
           else
             acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[ii][jj], 0, 0, 0);
           __builtin_amdgcn_sched_barrier(0);
         }
-        TM_WAIT16(nxt);
+        TM_WAIT12(nxt);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -1179,12 +1182,12 @@ __global__ __launch_bounds__(256) void grad_w_ring_kernel(const uint16_t* __rest
 #pragma unroll
   for (int jj = 0; jj < 4; ++jj) {
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) epi_block(ii, jj, false, f0);
+    for (int ii = 0; ii < 2; ++ii) epi_block(ii, jj, false, f0);
     epi_store(jj);
   }
   __builtin_amdgcn_s_waitcnt(0);
 #undef TM_TR
-#undef TM_WAIT16
+#undef TM_WAIT12
 }
 
 
@@ -1355,7 +1358,7 @@ int tm_ce_logits_bf16(uint16_t* d_logits, const uint16_t* d_hidden, const uint16
     if (lds != hipSuccess)
       return gemm_fail(TM_ELAUNCH, "tm_ce_logits_bf16: LDS attribute: %s", hipGetErrorString(lds));
     const int wpx = cus >= 16 ? cus / 8 : 1;  // one workgroup per CU of each XCD
-    hipLaunchKernelGGL(logits_ring_kernel, dim3(static_cast<uint32_t>(8 * wpx)), dim3(256), kRgLds, s, d_hidden,
+    hipLaunchKernelGGL(logits_ring_kernel, dim3(static_cast<uint32_t>(8 * wpx)), dim3(512), kRgLds, s, d_hidden,
                        d_weight, d_logits, static_cast<int>(rows), static_cast<int>(vocab), static_cast<int>(dim),
                        static_cast<int>(tiles_m), static_cast<int>(tiles_n), gm, gn, wpx);
     const hipError_t e = hipGetLastError();
@@ -1394,7 +1397,7 @@ int tm_ce_grad_w_bf16(uint16_t* d_grad_w, const uint16_t* d_grad_logits, const u
     if (lds != hipSuccess)
       return gemm_fail(TM_ELAUNCH, "tm_ce_grad_w_bf16: LDS attribute: %s", hipGetErrorString(lds));
     const int wpx = cus >= 16 ? cus / 8 : 1;
-    hipLaunchKernelGGL(grad_w_ring_kernel, dim3(static_cast<uint32_t>(8 * wpx)), dim3(256), kRgLds, s, d_grad_logits,
+    hipLaunchKernelGGL(grad_w_ring_kernel, dim3(static_cast<uint32_t>(8 * wpx)), dim3(512), kRgLds, s, d_grad_logits,
                        d_hidden, d_grad_w, static_cast<int>(vocab), static_cast<int>(dim), static_cast<int>(rows),
                        static_cast<int>(tiles_v), static_cast<int>(tiles_d), gm, gn, wpx);
     const hipError_t e = hipGetLastError();
