@@ -678,7 +678,7 @@ def run_ce_gemm(shapes, reps: int, dev, vocab: int = 151936):
     against torch.matmul (hipBLASLt) on the same bf16 operands, timed over `reps` launches after
     one warm-up: logits = h @ W^T (fused_linear_ce.py:38, tm_ce_logits_bf16), grad_h =
     grad_logits @ W (:52, the split-K tm_ce_grad_h_bf16 with its fixed-order reduction) and
-    grad_W = grad_logits^T @ h (:57, tm_ce_grad_w_bf16), plus the once-per-call W^T transpose."""
+    grad_W = grad_logits^T @ h (:57, tm_ce_grad_w_bf16)."""
     import torch
 
     from torchure_amd import _native
@@ -700,16 +700,12 @@ def run_ce_gemm(shapes, reps: int, dev, vocab: int = 151936):
     g = torch.Generator(device=dev).manual_seed(0)
     for dim in sorted({d for _, d in shapes}):
         w = (torch.randn(vocab, dim, device=dev, generator=g) * 0.05).to(torch.bfloat16)
-        wt = torch.empty((dim, vocab), dtype=torch.bfloat16, device=dev)
-        ms_t = timed(lambda: _native.check(lib.tm_ce_transpose_bf16(wt.data_ptr(), w.data_ptr(), vocab, dim, stream),
-                                           "tm_ce_transpose_bf16"))
-        out["transpose_ms_dim%d" % dim] = round(ms_t, 4)
         for rows in [r for r, d in shapes if d == dim]:
             a = torch.randn(rows, vocab, device=dev, generator=g).to(torch.bfloat16)
             o = torch.empty((rows, dim), dtype=torch.bfloat16, device=dev)
             nb = lib.tm_ce_grad_h_workspace_bytes(rows, vocab, dim)
             ws = torch.empty(nb, dtype=torch.uint8, device=dev)
-            ms_s = timed(lambda: _native.check(lib.tm_ce_grad_h_bf16(o.data_ptr(), a.data_ptr(), wt.data_ptr(), rows,
+            ms_s = timed(lambda: _native.check(lib.tm_ce_grad_h_bf16(o.data_ptr(), a.data_ptr(), w.data_ptr(), rows,
                                                                      vocab, dim, ws.data_ptr(), nb, stream),
                                                "tm_ce_grad_h_bf16"))
             ms_l = timed(lambda: torch.matmul(a, w, out=o))
@@ -732,7 +728,7 @@ def run_ce_gemm(shapes, reps: int, dev, vocab: int = 151936):
                 "grad_w_ms": round(ms_gw, 4), "grad_w_TFLOPs": round(fl / ms_gw / 1e9, 1),
                 "grad_w_hipblaslt_ms": round(ms_gw_l, 4), "grad_w_hipblaslt_TFLOPs": round(fl / ms_gw_l / 1e9, 1)}
             del a, o, ws, h, logits, gw
-        del w, wt
+        del w
     return out
 
 

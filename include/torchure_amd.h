@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TM_ABI_VERSION 2
+#define TM_ABI_VERSION 3
 
 /* status codes */
 #define TM_OK 0
@@ -352,16 +352,17 @@ int tm_ce_widen_scale(float* d_dst, const uint16_t* d_src, int64_t n, const floa
  * grad_hidden of one chunk, fused_linear_ce.py:52 `grad_hidden = grad_logits @ weight` (and its
  * store at :79), for the chunk shapes where a split-K GEMM pays: rows and dim positive
  * multiples of 256, vocab a multiple of 64, all pointers 16-byte aligned, every matrix
- * contiguous. d_grad_h (rows x dim) = bf16(d_grad_logits (rows x vocab) @ W) with fp32
- * accumulation, where d_wt is W transposed (dim x vocab, from tm_ce_transpose_bf16). The K range
+ * contiguous. d_grad_h (rows x dim) = bf16(d_grad_logits (rows x vocab) @ d_w) with fp32
+ * accumulation, d_w the weight as the op holds it (vocab x dim, row-major). The K range
  * is split into S ranges whose fp32 partial tiles go to d_ws and are summed in the fixed order
  * 0..S-1 before the single bf16 rounding: the result is deterministic; it differs from another
  * GEMM's only by fp32 summation order. d_ws holds tm_ce_grad_h_workspace_bytes(rows, vocab, dim)
  * bytes (S x rows x dim fp32, 0 for shapes the GEMM does not take); calls that share a
- * workspace on one stream are ordered, on different streams they race.
+ * workspace on one stream are ordered, on different streams they race. (ABI version 3: d_w is
+ * the weight itself; version 2 took its transpose, made by a tm_ce_transpose_bf16 since removed.)
  */
 size_t tm_ce_grad_h_workspace_bytes(int64_t rows, int64_t vocab, int64_t dim);
-int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const uint16_t* d_wt, int64_t rows,
+int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const uint16_t* d_w, int64_t rows,
                       int64_t vocab, int64_t dim, void* d_ws, size_t ws_bytes, void* stream);
 
 /*
@@ -384,14 +385,6 @@ int tm_ce_logits_bf16(uint16_t* d_logits, const uint16_t* d_hidden, const uint16
  */
 int tm_ce_grad_w_bf16(uint16_t* d_grad_w, const uint16_t* d_grad_logits, const uint16_t* d_hidden, int64_t rows,
                       int64_t vocab, int64_t dim, void* stream);
-
-/*
- * d_dst (cols x rows) = d_src (rows x cols) transposed, bf16, both contiguous, rows and cols
- * multiples of 64, pointers 8-byte aligned: the W^T operand of tm_ce_grad_h_bf16, made once per
- * forward (fused_linear_ce.py:65 casts the weight once for all chunks; this is the same
- * once-per-call preparation of the operand).
- */
-int tm_ce_transpose_bf16(uint16_t* d_dst, const uint16_t* d_src, int64_t rows, int64_t cols, void* stream);
 
 #ifdef __cplusplus
 }

@@ -141,9 +141,6 @@ def test_grad_h_gemm_workspace_and_shape_checks_without_gpu():
     assert lib.tm_ce_grad_h_bf16(fake, fake, fake, 256, 4096, 256, fake, ws(256, 4096, 256) - 1, None) < 0
     assert b"workspace" in lib.tm_last_error()
     assert lib.tm_ce_grad_h_bf16(fake, None, fake, 256, 4096, 256, fake, big, None) < 0
-    assert lib.tm_ce_transpose_bf16(fake, fake, 100, 64, None) < 0
-    assert b"multiples of 64" in lib.tm_last_error()
-    assert lib.tm_ce_transpose_bf16(fake, ctypes.c_void_p(0x1002), 64, 64, None) < 0
 
 
 def test_grad_w_fold_argument_checks_without_gpu():

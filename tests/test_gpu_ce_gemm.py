@@ -1,9 +1,8 @@
 """GPU parity of the fused CE's three bf16 MFMA GEMMs (torchure/loss/fused_linear_ce.py:38,52,57):
-tm_ce_logits_bf16 (logits = h W^T), tm_ce_grad_h_bf16 (split-K grad_h = grad_logits W, with the
-W^T it reads from tm_ce_transpose_bf16) and tm_ce_grad_w_bf16 (grad_W = grad_logits^T h).
+tm_ce_logits_bf16 (logits = h W^T), tm_ce_grad_h_bf16 (split-K grad_h = grad_logits W) and
+tm_ce_grad_w_bf16 (grad_W = grad_logits^T h).
 
 Checks:
-- the transpose bit for bit against torch's;
 - each GEMM against an fp64 product of the same bf16 operands: every element within one bf16
   ulp of the exact value plus 2^-20 of sum_k |a_ik b_kj| (the fp32 accumulation), at shapes
   from one tile (or one K slice per split) with ragged edges up to the Qwen3 heads' chunks;
@@ -45,25 +44,16 @@ def _lib():
     return _native, _native.lib(), _native.stream_handle(DEV)
 
 
-def _transpose(w):
-    native, lib, stream = _lib()
-    v, d = w.shape
-    wt = torch.empty((d, v), dtype=torch.bfloat16, device=DEV)
-    native.check(lib.tm_ce_transpose_bf16(wt.data_ptr(), w.data_ptr(), v, d, stream), "tm_ce_transpose_bf16")
-    return wt
-
-
 def _grad_h(a, w, ws_fill=None):
     native, lib, stream = _lib()
     rows, vocab = a.shape
     dim = w.shape[1]
-    wt = _transpose(w)
     nbytes = lib.tm_ce_grad_h_workspace_bytes(rows, vocab, dim)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
     if ws_fill is not None:
         ws.fill_(ws_fill)
     out = torch.empty((rows, dim), dtype=torch.bfloat16, device=DEV)
-    native.check(lib.tm_ce_grad_h_bf16(out.data_ptr(), a.data_ptr(), wt.data_ptr(), rows, vocab, dim,
+    native.check(lib.tm_ce_grad_h_bf16(out.data_ptr(), a.data_ptr(), w.data_ptr(), rows, vocab, dim,
                                        ws.data_ptr(), nbytes, stream), "tm_ce_grad_h_bf16")
     return out
 
@@ -72,15 +62,6 @@ def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
     """Spacing of bf16 numbers at |x| (x in fp64): 2^(e - 7) for |x| in [2^e, 2^(e+1))."""
     e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -126)))
     return torch.pow(2.0, e - 7)
-
-
-@pytest.mark.parametrize("rows,cols", [(64, 64), (128, 192), (151936, 1024)])
-def test_transpose_is_exact(rows, cols):
-    g = torch.Generator(device=DEV).manual_seed(rows + cols)
-    w = torch.randn(rows, cols, device=DEV, generator=g).to(torch.bfloat16)
-    wt = _transpose(w)
-    torch.cuda.synchronize()
-    assert torch.equal(wt.view(torch.int16), w.t().contiguous().view(torch.int16))
 
 
 @pytest.mark.parametrize("rows,vocab,dim,softmax", [

@@ -21,7 +21,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libtorchure_amd.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "torchure_amd.h")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TM_OK = 0
 TM_GRAD_BF16 = 0
@@ -108,7 +108,6 @@ _SIGNATURES = {
     "tm_ce_widen_scale": (ctypes.c_int, [_vp, _vp, _i64, _vp, _vp, _vp]),
     "tm_ce_grad_h_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "tm_ce_grad_h_bf16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, ctypes.c_size_t, _vp]),
-    "tm_ce_transpose_bf16": (ctypes.c_int, [_vp, _vp, _i64, _i64, _vp]),
     "tm_ce_logits_bf16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "tm_ce_grad_w_bf16": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
 }

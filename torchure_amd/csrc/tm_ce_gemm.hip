@@ -2,20 +2,19 @@
 // (torchure/loss/fused_linear_ce.py:38,52,57: bf16 matmuls, fp32 accumulation, bf16 results):
 //   logits_ring_kernel   logits = h W^T         (rows x V, K = D), persistent, for dim a multiple
 //                        of 128 (>= 256) and vocab a multiple of 8; logits_gemm_kernel otherwise
-//   grad_h_gemm_kernel   grad_h = grad_logits W (rows x D, K = V), split over K (long splits on
-//   grad_h_gemm8_kernel  8 waves, two a SIMD), with
+//   grad_h_gemm_kernel   grad_h = grad_logits W (rows x D, K = V), split over K, reading W as it
+//                        is stored (V x D), with
 //   grad_h_reduce_kernel summing the fp32 partials of each element over the splits in a fixed
 //                        order (split 0 first) and rounding once to bf16 (RNE), so the result
 //                        does not depend on scheduling
 //   grad_w_ring_kernel   grad_W = grad_logits^T h (V x D, K = rows), persistent, for rows a
 //                        multiple of 128 (>= 256); grad_w_gemm_kernel otherwise
-// and transpose_bf16_kernel, which makes W^T (D x V) once per call for grad_h.
 //
 // All three are 256 x 256 output tiles per workgroup on v_mfma_f32_32x32x16_bf16 with fp32
-// accumulation: the ring kernels and grad_h_gemm8_kernel on 8 wave64, two a SIMD (each 128 x 64
-// or 64 x 128, 128 accumulators), so that one wave's MFMAs run while the other waits; the
-// one-tile kernels and grad_h_gemm_kernel on 4 wave64 (each 128 x 128, 256 accumulators in the
-// AGPRs). Every element sees the same MFMA sequence in all of them. Operands stream
+// accumulation: the ring kernels and grad_h_gemm_kernel on 8 wave64, two a SIMD (each 128 x 64,
+// 128 accumulators), so that one wave's MFMAs run while the other waits; the one-tile kernels on
+// 4 wave64 (each 128 x 128, 256 accumulators in the AGPRs). Every element sees the same MFMA
+// sequence in the ring and one-tile kernels. Operands stream
 // global -> LDS with direct loads (global_load_lds, 16 bytes a lane) into two 64 KB stages of
 // 64-deep K slices. gfx950's LDS has 64 four-byte banks and serves a 16-byte-per-lane read 16
 // lanes at a time, so the 16 lanes reading 16 consecutive 128-byte rows must hit 16 different
@@ -85,32 +84,6 @@ __global__ __launch_bounds__(256) void grad_h_reduce_kernel(const float* __restr
   *(u32x2*)(out + e) = o;
 }
 
-// dst (cols x rows) = src (rows x cols)^T, bf16, in 64 x 64 tiles through LDS.
-__global__ __launch_bounds__(256) void transpose_bf16_kernel(uint16_t* __restrict__ dst,
-                                                             const uint16_t* __restrict__ src, int64_t rows,
-                                                             int64_t cols) {
-  __shared__ uint16_t t[64][64 + 4];
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {  // 64 rows x 16 eight-byte pieces
-    const int v = threadIdx.x + 256 * i, r = v >> 4, c = (v & 15) * 4;
-    const u32x2 w = *(const u32x2*)(src + (r0 + r) * cols + c0 + c);
-    t[r][c] = static_cast<uint16_t>(w.x);
-    t[r][c + 1] = static_cast<uint16_t>(w.x >> 16);
-    t[r][c + 2] = static_cast<uint16_t>(w.y);
-    t[r][c + 3] = static_cast<uint16_t>(w.y >> 16);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {  // 64 dst rows (src columns) x 16 eight-byte pieces
-    const int v = threadIdx.x + 256 * i, c = v >> 4, r = (v & 15) * 4;
-    u32x2 w;
-    w.x = static_cast<uint32_t>(t[r][c]) | (static_cast<uint32_t>(t[r + 1][c]) << 16);
-    w.y = static_cast<uint32_t>(t[r + 2][c]) | (static_cast<uint32_t>(t[r + 3][c]) << 16);
-    *(u32x2*)(dst + (c0 + c) * rows + r0 + r) = w;
-  }
-}
-
 // ------------------------------------------------------------------ logits = hidden @ W^T
 //
 // fused_linear_ce.py:38 `logits = h @ w.t()` per chunk: C (rows x vocab) = A (rows x dim) times
@@ -167,7 +140,7 @@ struct LgFlags {
   static constexpr bool kNextV = kN, kNext2V = kN2;
 };
 
-// Main loop of the NT GEMMs (logits_gemm_kernel, grad_h_gemm_kernel): acc[n block][m block] of a
+// Main loop of logits_gemm_kernel (both operands K-contiguous): acc[n block][m block] of a
 // 256 x 256 tile, rows m0.. of A and n0.. of B (`ld` elements apart, rows past M or N clamped to
 // the last), over n_it 64-deep K slices from element k0. 4 waves, wave (wm, wn) = 128 x 128.
 __device__ __forceinline__ void nt_mainloop(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
@@ -588,15 +561,22 @@ bool logits_ring_fits(int64_t rows, int64_t vocab, int64_t dim) {
 // ------------------------------------------------- grad_h = grad_logits @ W, K split over workgroups
 //
 // fused_linear_ce.py:52 `grad_h = grad_logits @ w` per chunk: C (rows x dim) = G (rows x V) times
-// W (V x dim), with W^T (dim x V) as the second operand, so both are K-contiguous as in the
-// logits GEMM and the same main loop runs. K = V is long and the output small (16 tiles for a
-// 1024-row chunk at dim 1024), so workgroup (split, tile) computes one 256 x 256 tile over one
-// range of K slices and writes its fp32 partial tile; grad_h_reduce_kernel adds the partials.
-// Pair p = split x tiles + tile; workgroup w runs on XCD w % 8, which takes pairs
+// W (V x dim), K = V. K is long and the output small (16 tiles for a 1024-row chunk at dim
+// 1024), so workgroup (split, tile) computes one 256 x 256 tile over one range of K slices and
+// writes its fp32 partial tile (straight from the accumulators, 16 bytes a lane: 4 consecutive
+// columns of one row; a split with no K slices writes zeros); grad_h_reduce_kernel adds the
+// partials. Pair p = split x tiles + tile; workgroup w runs on XCD w % 8, which takes pairs
 // [x p8, (x+1) p8): the workgroups of an XCD share a split's K range of both operands in its L2.
-// The partial tile is written straight from the accumulators, 16 bytes a lane (4 consecutive
-// columns of one row); a split with no K slices writes zeros.
-__global__ __launch_bounds__(256) void grad_h_gemm_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ Wt,
+// A stage holds G's 256 rows x 64 K as 128-byte rows (the logits GEMM's layout and fragment
+// reads) and W's 64 K rows x 256 columns as 512-byte rows (grad_W's layout for its K-major
+// operand, fragments from two ds_read_b64_tr_b16), so W is read as it is stored: no transposed
+// copy. 8 waves, two a SIMD, wave (wm, wn) = (w / 4, w % 4) computing rows wm * 128 .. +127 and
+// columns wn * 64 .. +63 (4 x 2 blocks, 128 accumulators; 4 fragment reads, 4 half-fragment
+// reads and 8 MFMAs per K16 step; 8 loads a stage a wave: waves 0-3 G, waves 4-7 W). Measured on
+// MI355X: as fast as, or up to 6% faster than, the same schedule on W^T (the bits are the same),
+// which also needed the transpose (0.13 ms at dim 1024, 0.34 at 2560).
+
+__global__ __launch_bounds__(512) void grad_h_gemm_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ W,
                                                           float* __restrict__ partials, int rows, int dim, int64_t K,
                                                           int tiles, int splits, int iters_per_split) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -612,166 +592,129 @@ __global__ __launch_bounds__(256) void grad_h_gemm_kernel(const uint16_t* __rest
   const int n_it = max(0, min(iters_per_split, total - it0));
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int64_t k0 = static_cast<int64_t>(it0) * kSliceK;
 
-  f32x16 acc[4][4];  // [n block][m block]
+  // Loads, 8 a wave a stage. Waves 0-3: G rows (m) 64 (w % 4) + 8 j + lane / 8 of the tile, the
+  // lane's chunk (lane % 8) ^ ((row >> 1) & 7), into LDS rows 8 (8 w + j) .. of the A half (32 KB).
+  // Waves 4-7: W rows (k) 16 (w % 4) + 2 j + lane / 32 of the slice, columns n0 + 8 c with
+  // c = (lane % 32) ^ (4 (row & 3)), into the B half (512-byte rows), slot lane % 32.
+  const uint16_t* src[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int j = 0; j < 8; ++j) {
+    if (wave < 4) {
+      const int r = (wave % 4) * 64 + 8 * j + lane / 8;
+      const int c = (lane % 8) ^ ((r >> 1) & 7);
+      src[j] = G + static_cast<int64_t>(min(m0 + r, rows - 1)) * K + k0 + c * 8;
+    } else {
+      const int kr = (wave % 4) * 16 + 2 * j + lane / 32;
+      const int c = (lane % 32) ^ (4 * (kr & 3));
+      src[j] = W + (k0 + kr) * dim + n0 + 8 * c;
+    }
+  }
+  const int64_t step = wave < 4 ? kSliceK : static_cast<int64_t>(kSliceK) * dim;  // elements per stage
+  auto load = [&](int it, int stage, int j) {
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[j] + it * step),
+                                     (void __attribute__((address_space(3)))*)(smem + stage * kLgStage + (wave * 8 + j) * 1024),
+                                     16, 0, 0);
+  };
+  // A fragments (m blocks) as nt_mainloop: row R0 + lane % 32, chunk 2 kk + lane / 32
+  const int tx = (lane >> 5) ^ ((lane >> 1) & 7);
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const uint32_t la = lds0 + (lane & 31) * 128;
+  uint32_t vk[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) vk[kk] = la + (((2 * kk) ^ tx) * 16) + wm * 128 * 128;
+  // B half-fragments (n blocks) as grad_W's H operand
+  const int s16 = lane & 15, s4 = s16 >> 2;
+  const int lcf = ((lane >> 4) & 1) * 2 + ((s16 & 3) >> 1);
+  const uint32_t rowb = (8 * (lane >> 5) + s4) * 512 + (s16 & 1) * 8;
+  uint32_t bd[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) bd[b] = lds0 + kLgTile * 128 + rowb + (4 * ((2 * wn + b) ^ s4) + lcf) * 16;
+#define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
+#define TM_TR(dst, base, imm) asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
+#define TM_WAIT(a, b) \
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]))
+  // per K16 step: A blocks 0-3 (bf16x8), B half-fragments h = 2 b + r (bf16x4): b = n block, r = rows +0/+4
+  bf16x8 a0[4], a1[4];
+  bf16x4 b0[4], b1[4];
+  auto rd = [&](bf16x8* fa, bf16x4* fb, uint32_t so, int kk, int g) {  // g 0..3: A block g; 4..7: B half g - 4
+    if (g < 4) TM_RD(fa[g], vk[kk] + so, g * 32 * 128);
+    else {
+      const int h = g - 4, b = h >> 1, r = h & 1;
+      TM_TR(fb[h], bd[b] + so, kk * 16 * 512 + r * 4 * 512);
+    }
+  };
+  f32x16 acc[2][4];  // [n block][m block]
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  if (n_it > 0) nt_mainloop(G, Wt, K, m0, n0, rows, dim, static_cast<int64_t>(it0) * kSliceK, n_it, smem, acc);
-
-  // Register r of lane l of block (ii, jj) holds column 8 (r / 4) + 4 (l / 32) + r % 4 of row
-  // l % 32: registers 4 q .. 4 q + 3 are 4 consecutive columns.
+  if (n_it > 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) load(0, 0, j);
+    if (n_it > 1) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) load(1, 1, j);
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+    } else {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) rd(a0, b0, 0, 0, g);
+    TM_WAIT(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    auto stage = [&](int i, auto step_f) {
+      constexpr bool kNext = decltype(step_f)::kNextV, kNext2 = decltype(step_f)::kNext2V;
+      const int st = i & 1;
+      const uint32_t soff = st * kLgStage, noff = (st ^ 1) * kLgStage;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        bf16x8* ca = (kk & 1) ? a1 : a0;
+        bf16x8* na = (kk & 1) ? a0 : a1;
+        bf16x4* cb = (kk & 1) ? b1 : b0;
+        bf16x4* nb = (kk & 1) ? b0 : b1;
+        if (kk == 3 && kNext) {
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+          __builtin_amdgcn_s_barrier();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          if (kk < 3) rd(na, nb, soff, kk + 1, g);
+          else if (kNext) rd(na, nb, noff, 0, g);
+          if (kk == 3 && kNext2) load(i + 2, st, g);
+          const int jj = g / 2, ii = g % 2;
+          const bf16x8 bf = __builtin_shufflevector(cb[2 * ii], cb[2 * ii + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+          acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf, ca[jj], acc[ii][jj], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (kk < 3 || kNext) {
+          TM_WAIT(na, nb);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    int i = 0;
+    for (; i + 2 < n_it; ++i) stage(i, LgFlags<true, true>{});
+    if (i + 1 < n_it) stage(i++, LgFlags<true, false>{});
+    if (i < n_it) stage(i, LgFlags<false, false>{});
+  }
+#undef TM_RD
+#undef TM_TR
+#undef TM_WAIT
   float* P = partials + static_cast<int64_t>(s) * rows * dim;
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii)
+  for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = m0 + wm * 128 + jj * 32 + (lane & 31);
-        const int n = n0 + wn * 128 + ii * 32 + 8 * q + 4 * (lane >> 5);
-        const f32x4 v = {acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1], acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]};
-        *(f32x4*)(P + static_cast<int64_t>(m) * dim + n) = v;
-      }
-}
-
-// The same (split, tile) work on 8 waves, two a SIMD: wave (wm, wn) = (w / 2, w % 2) computes
-// rows wm * 64 .. +63 and columns wn * 128 .. +127 of the tile, 2 x 4 blocks of 32 x 32 (128
-// accumulators, which fit in the VGPRs beside the fragments). While one wave of a SIMD waits for
-// LDS reads, its loads or the stage barrier, the other's MFMAs run. LDS stages, swizzle, fragment
-// reads and stage schedule are nt_mainloop's, with 6 fragment reads and 8 MFMAs per K16 step and
-// 8 loads per stage a wave; every element sees the same MFMA sequence, so the bits are those of
-// grad_h_gemm_kernel. Measured on MI355X at V = 151,936 against grad_h_gemm_kernel: 8% faster
-// with 1187 K slices a split (8192 x 1024, 2 splits), 3-5% with 594-792 (4 and 3 splits), 5-7%
-// with 297 (8 splits); with 149 (1024 x 1024, 16 splits) 4-6% slower on one device and 5% faster
-// on another. The entry point takes it from kGh8MinIters slices a split.
-constexpr int kGh8MinIters = 256;
-
-__device__ __forceinline__ void nt8_mainloop(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-                                             int64_t ld, int m0, int n0, int M, int N, int64_t k0, int n_it,
-                                             uint8_t* smem, f32x16 (&acc)[4][2]) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  // Load j of this wave fills LDS rows 8 q .. 8 q + 7 of [A tile; B tile], q = 8 wave + j.
-  const uint16_t* src[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int q = wave * 8 + j;
-    const int r = (q % 32) * 8 + lane / 8;
-    const int c = (lane % 8) ^ ((r >> 1) & 7);
-    src[j] = (q < 32 ? A + static_cast<int64_t>(min(m0 + r, M - 1)) * ld
-                     : B + static_cast<int64_t>(min(n0 + r, N - 1)) * ld) + k0 + c * 8;
-  }
-  auto load = [&](int it, int stage, int j) {
-    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)(src[j] + it * kSliceK),
-                                     (void __attribute__((address_space(3)))*)(smem + stage * kLgStage + (wave * 8 + j) * 1024),
-                                     16, 0, 0);
-  };
-  const int tx = (lane >> 5) ^ ((lane >> 1) & 7);
-  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)) + (lane & 31) * 128;
-  uint32_t vk[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) vk[kk] = lds0 + (((2 * kk) ^ tx) * 16);
-  const uint32_t offA = wm * 64 * 128, offB = kLgTile * 128 + wn * 128 * 128;
-#define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
-#define TM_WAIT6(f) \
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]))
-  // fragment g: g < 4 -> B (n) block g, g >= 4 -> A (m) block g - 4
-  bf16x8 f0[6], f1[6];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) load(0, 0, j);
-  if (n_it > 1) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) load(1, 1, j);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
-  } else {
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  }
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int g = 0; g < 6; ++g) TM_RD(f0[g], vk[0] + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
-  TM_WAIT6(f0);
-  __builtin_amdgcn_sched_barrier(0);
-
-  auto stage = [&](int i, auto step) {
-    constexpr bool kNext = decltype(step)::kNextV, kNext2 = decltype(step)::kNext2V;
-    const int s = i & 1;
-    const uint32_t soff = s * kLgStage, noff = (s ^ 1) * kLgStage;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      bf16x8* cur = (kk & 1) ? f1 : f0;
-      bf16x8* nxt = (kk & 1) ? f0 : f1;
-      if (kk == 3 && kNext) {
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // this wave's loads of stage i + 1 are in LDS
-        __builtin_amdgcn_s_barrier();               // every wave's; and stage i's reads are done
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {  // one MFMA, at most one fragment read, at most one load
-        if (g < 6) {
-          if (kk < 3) {
-            TM_RD(nxt[g], vk[kk + 1] + soff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
-          } else if (kNext) {
-            TM_RD(nxt[g], vk[0] + noff + (g < 4 ? offB : offA), (g % 4) * 32 * 128);
-          }
-        }
-        if (kk == 3 && kNext2) load(i + 2, s, g);
-        const int ii = g / 2, jj = g % 2;
-        acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur[ii], cur[4 + jj], acc[ii][jj], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (kk < 3 || kNext) {
-        TM_WAIT6(nxt);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  };
-  int i = 0;
-  for (; i + 2 < n_it; ++i) stage(i, LgFlags<true, true>{});
-  if (i + 1 < n_it) stage(i++, LgFlags<true, false>{});
-  if (i < n_it) stage(i, LgFlags<false, false>{});
-#undef TM_RD
-#undef TM_WAIT6
-}
-
-__global__ __launch_bounds__(512) void grad_h_gemm8_kernel(const uint16_t* __restrict__ G, const uint16_t* __restrict__ Wt,
-                                                           float* __restrict__ partials, int rows, int dim, int64_t K,
-                                                           int tiles, int splits, int iters_per_split) {
-  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  const int pairs = tiles * splits;
-  const int p8 = (pairs + 7) / 8;
-  const int p = (blockIdx.x % 8) * p8 + blockIdx.x / 8;
-  if (p >= pairs) return;
-  const int s = p / tiles, tile = p - s * tiles;
-  const int tiles_n = dim / kLgTile;
-  const int m0 = (tile / tiles_n) * kLgTile, n0 = (tile % tiles_n) * kLgTile;
-  const int total = static_cast<int>(K / kSliceK);
-  const int it0 = s * iters_per_split;
-  const int n_it = max(0, min(iters_per_split, total - it0));
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-
-  f32x16 acc[4][2];  // [n block][m block]
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-  if (n_it > 0) nt8_mainloop(G, Wt, K, m0, n0, rows, dim, static_cast<int64_t>(it0) * kSliceK, n_it, smem, acc);
-
-  float* P = partials + static_cast<int64_t>(s) * rows * dim;
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii)
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = m0 + wm * 64 + jj * 32 + (lane & 31);
-        const int n = n0 + wn * 128 + ii * 32 + 8 * q + 4 * (lane >> 5);
+        const int n = n0 + wn * 64 + ii * 32 + 8 * q + 4 * (lane >> 5);
         const f32x4 v = {acc[ii][jj][4 * q], acc[ii][jj][4 * q + 1], acc[ii][jj][4 * q + 2], acc[ii][jj][4 * q + 3]};
         *(f32x4*)(P + static_cast<int64_t>(m) * dim + n) = v;
       }
@@ -1215,7 +1158,7 @@ void logits_groups(int64_t tiles_m, int64_t dim, int& gm, int& gn) {
   gn = 32 / gm;
 }
 
-// Splits of the K range, chosen by a cost model of the launch. One workgroup (136 KB of LDS) fits
+// Splits of the K range, chosen by a cost model of the launch. One workgroup (128 KB of LDS) fits
 // a CU, so tiles x S workgroups run in ceil(tiles x S / 256) rounds; a workgroup takes about
 // 1.7 us per 64-deep K slice (256 x 256 x 64 MFMA work at the main loop's pace) plus about 8 us
 // to store its 256 KB partial tile, and the reduction reads S x rows x dim fp32 partials at about
@@ -1240,16 +1183,16 @@ int64_t splits_for(int64_t rows, int64_t vocab, int64_t dim) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The GEMM kernels' dynamic LDS (136 KB, 160 KB for the ring kernels) exceeds the 64 KB default:
+// The GEMM kernels' dynamic LDS (128-160 KB) exceeds the 64 KB default:
 // the attribute is set once per device and kernel, with that device current, before the first
 // launch there. The device's CU count (for the ring kernels' workgroups per XCD) is read then.
 constexpr int kMaxDevices = 64;
 std::mutex g_lds_mu;
-bool g_lds_set[6][kMaxDevices] = {};
+bool g_lds_set[5][kMaxDevices] = {};
 int g_cus[kMaxDevices] = {};
 
 // which: 0 grad_h_gemm_kernel, 1 logits_gemm_kernel, 2 grad_w_gemm_kernel, 3 logits_ring_kernel,
-// 4 grad_w_ring_kernel, 5 grad_h_gemm8_kernel.
+// 4 grad_w_ring_kernel.
 // `cus`, when given, receives the device's CU count.
 hipError_t allow_lds(hipStream_t stream, int which, int* cus = nullptr) {
   int dev = -1;
@@ -1264,10 +1207,10 @@ hipError_t allow_lds(hipStream_t stream, int which, int* cus = nullptr) {
   int cur = -1;
   e = hipGetDevice(&cur);
   if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
-  const void* fn[6] = {reinterpret_cast<const void*>(grad_h_gemm_kernel), reinterpret_cast<const void*>(logits_gemm_kernel),
+  const void* fn[5] = {reinterpret_cast<const void*>(grad_h_gemm_kernel), reinterpret_cast<const void*>(logits_gemm_kernel),
                        reinterpret_cast<const void*>(grad_w_gemm_kernel), reinterpret_cast<const void*>(logits_ring_kernel),
-                       reinterpret_cast<const void*>(grad_w_ring_kernel), reinterpret_cast<const void*>(grad_h_gemm8_kernel)};
-  const int bytes[6] = {kLgLds, kLgLds, kLgLds, kRgLds, kRgLds, 2 * kLgStage};
+                       reinterpret_cast<const void*>(grad_w_ring_kernel)};
+  const int bytes[5] = {2 * kLgStage, kLgLds, kLgLds, kRgLds, kRgLds};
   if (e == hipSuccess) e = hipFuncSetAttribute(fn[which], hipFuncAttributeMaxDynamicSharedMemorySize, bytes[which]);
   if (e == hipSuccess && g_cus[dev] == 0) e = hipDeviceGetAttribute(&g_cus[dev], hipDeviceAttributeMultiprocessorCount, dev);
   if (cur >= 0 && cur != dev) {
@@ -1290,7 +1233,7 @@ size_t tm_ce_grad_h_workspace_bytes(int64_t rows, int64_t vocab, int64_t dim) {
   return static_cast<size_t>(splits_for(rows, vocab, dim)) * rows * dim * sizeof(float);
 }
 
-int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const uint16_t* d_wt, int64_t rows,
+int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const uint16_t* d_w, int64_t rows,
                       int64_t vocab, int64_t dim, void* d_ws, size_t ws_bytes, void* stream) {
   if (rows <= 0 || dim <= 0 || vocab <= 0 || rows % kTile || dim % kTile || vocab % kSliceK)
     return gemm_fail(TM_EINVAL,
@@ -1299,9 +1242,9 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
   if (rows > (1 << 20) || dim > (1 << 16))
     return gemm_fail(TM_EINVAL, "tm_ce_grad_h_bf16: rows %lld or dim %lld too large", (long long)rows,
                      (long long)dim);
-  if (!d_grad_h || !d_grad_logits || !d_wt || !d_ws)
+  if (!d_grad_h || !d_grad_logits || !d_w || !d_ws)
     return gemm_fail(TM_EINVAL, "tm_ce_grad_h_bf16: null pointer");
-  if (!aligned16(d_grad_h) || !aligned16(d_grad_logits) || !aligned16(d_wt) || !aligned16(d_ws))
+  if (!aligned16(d_grad_h) || !aligned16(d_grad_logits) || !aligned16(d_w) || !aligned16(d_ws))
     return gemm_fail(TM_EINVAL, "tm_ce_grad_h_bf16: pointers must be 16-byte aligned");
   if (ws_bytes < tm_ce_grad_h_workspace_bytes(rows, vocab, dim))
     return gemm_fail(TM_EINVAL, "tm_ce_grad_h_bf16: workspace of %zu bytes, %zu needed", ws_bytes,
@@ -1311,24 +1254,15 @@ int tm_ce_grad_h_bf16(uint16_t* d_grad_h, const uint16_t* d_grad_logits, const u
   const int64_t tiles = (rows / kTile) * (dim / kTile);
   const int64_t total_iters = vocab / kSliceK;
   const int64_t per = (total_iters + splits - 1) / splits;
-  const bool eight = per >= kGh8MinIters;  // same bits either way
-  const hipError_t lds = allow_lds(s, eight ? 5 : 0);
+  const hipError_t lds = allow_lds(s, 0);
   if (lds != hipSuccess)
     return gemm_fail(TM_ELAUNCH, "tm_ce_grad_h_bf16: LDS attribute: %s", hipGetErrorString(lds));
   float* partials = static_cast<float*>(d_ws);
-  const dim3 grid(static_cast<uint32_t>((tiles * splits + 7) / 8 * 8));
-  if (eight)
-    hipLaunchKernelGGL(grad_h_gemm8_kernel, grid, dim3(512), 2 * kLgStage, s, d_grad_logits, d_wt, partials,
-                       static_cast<int>(rows), static_cast<int>(dim), vocab, static_cast<int>(tiles),
-                       static_cast<int>(splits), static_cast<int>(per));
-  else
-    hipLaunchKernelGGL(grad_h_gemm_kernel, grid, dim3(256), kLgLds, s, d_grad_logits, d_wt, partials,
-                       static_cast<int>(rows), static_cast<int>(dim), vocab, static_cast<int>(tiles),
-                       static_cast<int>(splits), static_cast<int>(per));
+  hipLaunchKernelGGL(grad_h_gemm_kernel, dim3(static_cast<uint32_t>((tiles * splits + 7) / 8 * 8)), dim3(512),
+                     2 * kLgStage, s, d_grad_logits, d_w, partials, static_cast<int>(rows), static_cast<int>(dim),
+                     vocab, static_cast<int>(tiles), static_cast<int>(splits), static_cast<int>(per));
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess)
-    return gemm_fail(TM_ELAUNCH, "%s: launch failed: %s", eight ? "grad_h_gemm8_kernel" : "grad_h_gemm_kernel",
-                     hipGetErrorString(e));
+  if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "grad_h_gemm_kernel: launch failed: %s", hipGetErrorString(e));
   const int64_t n = rows * dim;
   hipLaunchKernelGGL(grad_h_reduce_kernel, dim3(static_cast<uint32_t>((n / 4 + 255) / 256)), dim3(256), 0, s,
                      partials, d_grad_h, n, static_cast<int>(splits));
@@ -1413,21 +1347,6 @@ int tm_ce_grad_w_bf16(uint16_t* d_grad_w, const uint16_t* d_grad_logits, const u
                      static_cast<int>(tiles_v), static_cast<int>(tiles_d), gm, gn);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "grad_w_gemm_kernel: launch failed: %s", hipGetErrorString(e));
-  return TM_OK;
-}
-
-int tm_ce_transpose_bf16(uint16_t* d_dst, const uint16_t* d_src, int64_t rows, int64_t cols, void* stream) {
-  if (rows <= 0 || cols <= 0 || rows % 64 || cols % 64)
-    return gemm_fail(TM_EINVAL, "tm_ce_transpose_bf16: rows %lld and cols %lld must be positive multiples of 64",
-                     (long long)rows, (long long)cols);
-  if (rows / 64 > 65535 || cols / 64 > 0x7FFFFFFF)
-    return gemm_fail(TM_EINVAL, "tm_ce_transpose_bf16: %lld rows is too many", (long long)rows);
-  if (!d_dst || !d_src || (reinterpret_cast<uintptr_t>(d_dst) & 7u) || (reinterpret_cast<uintptr_t>(d_src) & 7u))
-    return gemm_fail(TM_EINVAL, "tm_ce_transpose_bf16: null or not 8-byte aligned pointer");
-  hipLaunchKernelGGL(transpose_bf16_kernel, dim3(static_cast<uint32_t>(cols / 64), static_cast<uint32_t>(rows / 64)),
-                     dim3(256), 0, static_cast<hipStream_t>(stream), d_dst, d_src, rows, cols);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return gemm_fail(TM_ELAUNCH, "transpose_bf16_kernel: launch failed: %s", hipGetErrorString(e));
   return TM_OK;
 }
 

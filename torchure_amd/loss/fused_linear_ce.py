@@ -238,15 +238,15 @@ def splitk_grad_h_fits(rows: int, dim: int, vocab: int) -> bool:
     faster on MI355X: more than SPLITK_GRAD_H_MAX_TILES output tiles of 256 x 256 with dim a
     power of two. With few tiles and K = vocab a library GEMM leaves most of the 256 CUs idle and
     the split-K kernel spreads K over them; with many, the library's kernels fill the chip
-    themselves, and beat this kernel by 7-12% when dim is a power of two, but run 9-43% behind
+    themselves, and beat this kernel by 1.5-7% when dim is a power of two, but run 12-50% behind
     it at the other Qwen3 head widths (ms per call at V = 151,936, split-K / hipBLASLt):
 
         dim   rows 1024      2048           4096           8192
-        1024  0.29 / 0.72    0.57 / 0.94    1.07 / 1.43    2.08 / 1.94
-        2048  0.55 / 0.90    1.06 / 1.63    2.04 / 1.89    4.03 / 3.67
-        2560  0.72 / 1.00    1.35 / 1.83    2.79 / 3.38    5.33 / 7.40
-        4096  1.10 / 1.80    2.07 / 1.89    4.08 / 3.62    8.16 / 7.32
-        5120  1.43 / 1.84    2.94 / 3.38    5.47 / 6.83    10.52 / 13.14
+        1024  0.30 / 0.78    0.65 / 1.08    1.07 / 1.51    2.11 / 2.08
+        2048  0.55 / 0.90    1.04 / 1.65    2.06 / 2.01    4.11 / 3.95
+        2560  0.69 / 1.03    1.35 / 1.90    2.82 / 3.52    5.42 / 7.40
+        4096  1.07 / 1.88    2.11 / 2.03    4.16 / 3.88    8.35 / 7.76
+        5120  1.43 / 1.89    3.11 / 3.48    5.70 / 7.07    11.34 / 13.41
     """
     if not (rows > 0 and dim > 0 and rows % 256 == 0 and dim % 256 == 0 and dim <= 65536
             and vocab > 0 and vocab % 64 == 0):
@@ -271,30 +271,27 @@ def _fold(lib, grad_weight, chunks, accumulated, g, n_valid, stream) -> None:
 
 class GradHidden:
     """grad_h = grad_logits @ W (fused_linear_ce.py:52, stored at :79) for the chunks of one
-    call: the split-K MFMA GEMM on the chunks ``splitk_grad_h_fits`` accepts, with W^T made
-    once for the call and one fp32 partials workspace shared by the chunks (stream-ordered),
-    and torch.matmul (hipBLASLt) on the others. ``w`` is the contiguous bf16 weight (V x D)."""
+    call: the split-K MFMA GEMM on the chunks ``splitk_grad_h_fits`` accepts, reading W as it is
+    stored, with one fp32 partials workspace shared by the chunks (stream-ordered), and
+    torch.matmul (hipBLASLt) on the others. ``w`` is the contiguous bf16 weight (V x D)."""
 
     def __init__(self, w: torch.Tensor, chunk_rows, lib, stream):
         self.w, self.lib, self.stream = w, lib, stream
         self.vocab, self.dim = w.shape
         fits = [r for r in set(chunk_rows) if splitk_grad_h_fits(r, self.dim, self.vocab)]
-        self.wt = self.ws = None
+        self.ws = None
         if fits:
-            self.wt = torch.empty((self.dim, self.vocab), dtype=torch.bfloat16, device=w.device)
-            _native.check(lib.tm_ce_transpose_bf16(self.wt.data_ptr(), w.data_ptr(), self.vocab, self.dim,
-                                                   stream), "tm_ce_transpose_bf16")
             nbytes = max(lib.tm_ce_grad_h_workspace_bytes(r, self.vocab, self.dim) for r in fits)
             self.ws = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
 
     def __call__(self, grad_logits: torch.Tensor, out: torch.Tensor) -> None:
         rows = grad_logits.shape[0]
-        if self.wt is None or not splitk_grad_h_fits(rows, self.dim, self.vocab):
+        if self.ws is None or not splitk_grad_h_fits(rows, self.dim, self.vocab):
             torch.matmul(grad_logits, self.w, out=out)
             return
         if not (grad_logits.is_contiguous() and out.is_contiguous() and out.dtype == torch.bfloat16):
             raise RuntimeError("fused_linear_cross_entropy: grad_h GEMM operands must be contiguous bf16")
-        _native.check(self.lib.tm_ce_grad_h_bf16(out.data_ptr(), grad_logits.data_ptr(), self.wt.data_ptr(), rows,
+        _native.check(self.lib.tm_ce_grad_h_bf16(out.data_ptr(), grad_logits.data_ptr(), self.w.data_ptr(), rows,
                                                  self.vocab, self.dim, self.ws.data_ptr(), self.ws.numel(),
                                                  self.stream), "tm_ce_grad_h_bf16")
 
