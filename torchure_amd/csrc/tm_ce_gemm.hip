@@ -634,12 +634,15 @@ __global__ __launch_bounds__(512) void grad_h_gemm_kernel(const uint16_t* __rest
   for (int b = 0; b < 2; ++b) bd[b] = lds0 + kLgTile * 128 + rowb + (4 * ((2 * wn + b) ^ s4) + lcf) * 16;
 #define TM_RD(dst, base, imm) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
 #define TM_TR(dst, base, imm) asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(base), "i"(imm))
-#define TM_WAIT(a, b) \
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]))
-  // per K16 step: A blocks 0-3 (bf16x8), B half-fragments h = 2 b + r (bf16x4): b = n block, r = rows +0/+4
+#define TM_WAIT(a, b)                                                                                 \
+  asm volatile("s_waitcnt lgkmcnt(0)"                                                                \
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]))
+  // per K16 step: A blocks 0-3 (bf16x8); B half-fragments h = 2 b + r (bf16x4), b the n block,
+  // r rows +0 / +4
   bf16x8 a0[4], a1[4];
   bf16x4 b0[4], b1[4];
-  auto rd = [&](bf16x8* fa, bf16x4* fb, uint32_t so, int kk, int g) {  // g 0..3: A block g; 4..7: B half g - 4
+  // g 0..3: A block g; 4..7: B half-fragment g - 4
+  auto rd = [&](bf16x8* fa, bf16x4* fb, uint32_t so, int kk, int g) {
     if (g < 4) TM_RD(fa[g], vk[kk] + so, g * 32 * 128);
     else {
       const int h = g - 4, b = h >> 1, r = h & 1;
