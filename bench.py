@@ -55,11 +55,14 @@ def parse():
                     help="keep timing CPU steps of a set until this much CPU work has been timed "
                          "(at most 100 steps)")
     ap.add_argument("--also", default="qwen3-4b-again,qwen3-0.6b,qwen3-0.6b-ref,qwen3-0.6b-fp32acc,"
-                                      "qwen3-4b-dropin,qwen3-4b-ddpbuckets,qwen3-4b-eager,ragged",
+                                      "qwen3-4b-dropin,qwen3-4b-ddpbuckets,qwen3-4b-eager,ragged,"
+                                      "qwen3-4b-shard8",
                     help="comma list of extra configs reported under 'extra' (empty = none); "
                          "'<config>-again' runs that config once more, on fresh allocations made "
                          "after the earlier legs' memory was released; '<config>-eager' steps with "
-                         "the clip scaling the grads in place first (defer_clip=False)")
+                         "the clip scaling the grads in place first (defer_clip=False); "
+                         "'<config>-shard<N>' steps rank 0's share of that set sharded on dim 0 over "
+                         "N ranks (one GPU's part of a sharded step; its norm is the rank's partial)")
     ap.add_argument("--mode", choices=("bench", "kernels", "ce", "ce-gemm"), default="bench",
                     help="kernels: only the norm and update launches (for an -fp32acc config, the "
                          "accumulation launches), --reps times each, plus a 2 GiB device copy for "

@@ -273,6 +273,28 @@ def test_host_list_primitives():
     assert isinstance(ptr, np.ndarray)
 
 
+def test_shard_shapes_split_dim0_like_torch_chunk():
+    """One rank's share of a dim-0 sharded parameter set has torch.chunk's pieces (FSDP2's
+    Shard(0)): the ranks' shares put together are the whole set, rank 0 of the 4B set over 8
+    ranks holds 502,808,512 params, and ranks past the last non-empty piece hold nothing."""
+    from torchure_amd.workloads import numel, shapes_for, shard_shapes
+
+    full = shapes_for("qwen3-4b")
+    for ranks in (1, 3, 8):
+        shares = [shard_shapes(full, ranks, r) for r in range(ranks)]
+        assert sum(numel(s) for sh in shares for s in sh) == sum(numel(s) for s in full)
+        for shape in set(full) | {(3, 5), (130,)}:
+            want = [t.shape[0] for t in torch.zeros(shape[0]).chunk(ranks)]
+            want += [0] * (ranks - len(want))
+            got = [sum(s[0] for s in shard_shapes([shape], ranks, r)) for r in range(ranks)]
+            assert got == want, (shape, ranks, got, want)
+    r0 = shapes_for("qwen3-4b-shard8")
+    assert r0 == shard_shapes(full, 8, 0) and sum(numel(s) for s in r0) == 502_808_512
+    assert shard_shapes([(3, 5)], 8, 7) == [] and shard_shapes([(3, 5)], 8, 1) == [(1, 5)]
+    with pytest.raises(ValueError):
+        shard_shapes(full, 8, 8)
+
+
 def test_bench_ddp_bucket_layout():
     """bench.py's DDP bucket leg lays grads out as torchure's DDP does
     (torchure/parallelism/data_parallel.py:86-105): reverse parameter order, a bucket closes

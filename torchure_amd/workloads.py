@@ -49,11 +49,31 @@ CONFIGS = {
 }
 
 
+def shard_shapes(shapes, ranks: int, rank: int = 0) -> list[tuple[int, ...]]:
+    """One rank's share of a parameter set sharded on dim 0 in ``ranks`` pieces, as
+    ``torch.chunk`` splits it (FSDP2's ``Shard(0)``): pieces of ceil(d0 / ranks) rows,
+    the last ones shorter or empty. Empty shares are left out."""
+    if ranks < 1 or not 0 <= rank < ranks:
+        raise ValueError(f"rank {rank} of {ranks}")
+    out = []
+    for shape in shapes:
+        d0 = shape[0]
+        step = -(-d0 // ranks)
+        rows = max(0, min(d0, (rank + 1) * step) - rank * step)
+        if rows:
+            out.append((rows,) + tuple(shape[1:]))
+    return out
+
+
 def shapes_for(name: str) -> list[tuple[int, ...]]:
-    """Shapes of a named configuration: a Qwen3 set from CONFIGS, or "ragged"
-    (the 10,000-tensor stress list of ragged_shapes)."""
+    """Shapes of a named configuration: a Qwen3 set from CONFIGS, "ragged" (the
+    10,000-tensor stress list of ragged_shapes), or "<set>-shard<N>": rank 0's share of
+    that set sharded on dim 0 over N ranks (one GPU's part of a sharded step)."""
     if name == "ragged":
         return ragged_shapes()
+    base, sep, ranks = name.rpartition("-shard")
+    if sep and ranks.isdigit():
+        return shard_shapes(shapes_for(base), int(ranks))
     return qwen3_param_shapes(**CONFIGS[name])
 
 
